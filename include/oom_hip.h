@@ -1,0 +1,136 @@
+/*
+ * oom_hip.h -- C ABI of the MI355X (gfx950) decode hot path of oom-inference.
+ *
+ * These entry points are what an `oominf-rocm` backend crate binds to implement
+ * the reference's operation traits (crates/oominf-core/src/backend.rs:1020-1049)
+ * on ROCm. Every call:
+ *   - takes device pointers, sizes and a HIP stream (`stream`, a hipStream_t;
+ *     NULL is the null stream) and enqueues work on that stream in order;
+ *   - returns OOM_OK (0) or a negative OOM_ERR_*; the message of the last failure
+ *     on the calling thread is oom_last_error() (as the reference's
+ *     "...: buffer too small or shape unsupported", crates/oominf-cuda/src/lib.rs:157-160);
+ *   - allocates nothing: scratch comes from a caller workspace whose size the
+ *     matching *_workspace_size() returns. A workspace must be zero-filled once
+ *     before its first use (oom_workspace_init); calls leave it ready for the next
+ *     call. Calls sharing one workspace must be ordered (one stream).
+ *   - is deterministic: the same inputs give the same bits.
+ * Activations are fp32 or bf16 (OOM_F32 / OOM_BF16); accumulation is fp32.
+ */
+#ifndef OOM_HIP_H
+#define OOM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OOM_OK 0
+#define OOM_ERR_ARG (-1)       /* shape unsupported, null pointer, misaligned buffer */
+#define OOM_ERR_WORKSPACE (-2) /* workspace smaller than *_workspace_size() */
+#define OOM_ERR_LAUNCH (-3)    /* the HIP runtime refused a launch */
+
+/* Element types of activations and outputs. */
+#define OOM_F32 0
+#define OOM_BF16 1
+
+/* Scale layouts of e4m3 weights [n, k] (w = e4m3(q) * scale):
+ *   OOM_SCALE_ROW      scale[r]                              one per output row
+ *   OOM_SCALE_1X128    scale[r * ceil(k/128) + c/128]        the reference's Weight::Fp8
+ *                                                            (crates/oominf-core/src/backend.rs:163-167)
+ *   OOM_SCALE_128X128  scale[(r/128) * ceil(k/128) + c/128]  128 x 128 blocks */
+#define OOM_SCALE_ROW 0
+#define OOM_SCALE_1X128 1
+#define OOM_SCALE_128X128 2
+
+/* Byte layout of an FP8 expert record (layout tag "fp8-e4m3-b128"): byte offsets of
+ * each part from the record start, every part 256-byte aligned (the reference's
+ * PART_ALIGN, docs/dev/format.md:37-39). gate and up weights are e4m3 [inter,
+ * hidden], down e4m3 [hidden, inter], all row-major; each scale part is fp32 in
+ * the OOM_SCALE_128X128 layout of its weight. The FP8 counterpart of
+ * Nvfp4Record (crates/oominf-core/src/backend.rs:780-796). */
+typedef struct OomFp8Record {
+    int64_t hidden;
+    int64_t inter;
+    int64_t gate_weight;
+    int64_t gate_scale;
+    int64_t up_weight;
+    int64_t up_scale;
+    int64_t down_weight;
+    int64_t down_scale;
+} OomFp8Record;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* oom_last_error(void);
+
+/* Zero-fills `bytes` of workspace at `ws` on `stream` with a fill kernel (no
+ * hipMemset node, so it is safe inside graph capture). */
+int oom_workspace_init(void* ws, size_t bytes, void* stream);
+
+/* Router: softmax over E logits per token, top k (ties to the lower id), weights
+ * renormalised over the k picks, in pick order. logits f32 [T, E]; ids i32 [T, k];
+ * weights f32 [T, k]. k <= 32, E <= 8192.
+ * Replaces Experts::router_topk (crates/oominf-core/src/backend.rs:814-824;
+ * crates/oominf-cuda/src/experts.rs:10-38). */
+int oom_router_topk(const float* logits, int32_t* ids, float* weights, int T, int E, int k, void* stream);
+
+/* Decode GEMV over e4m3 weights: y[t, n] = sum_k x[t, k] * e4m3(q[n, k]) * scale(n, k)
+ * for t < T <= 16. x [T, K] in x_dtype; q [N, K] (16-byte aligned, K % 16 == 0);
+ * scale in scale_layout; y [T, N] in y_dtype.
+ * Replaces Linear::gemm_fp8 at decode sizes (crates/oominf-core/src/backend.rs:194-209;
+ * crates/oominf-cuda/src/linear.rs:35-56,220-350). */
+size_t oom_gemv_fp8_workspace_size(int T, int64_t N, int64_t K);
+int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const float* scale, int scale_layout, void* y,
+                 int y_dtype, int T, int64_t N, int64_t K, void* ws, size_t ws_bytes, void* stream);
+
+/* Routed-expert gate/up + SwiGLU over FP8 records read in place:
+ * h[a, j] = silu(x[assign_tok[a]] . Wg_e[j]) * (x[assign_tok[a]] . Wu_e[j]) for the
+ * assignments a in [off[i], off[i+1]) of expert i < n_experts, whose record starts
+ * at device address recs[i]. x [T, hidden] in x_dtype; h f32 [A, inter].
+ * Replaces Experts::moe_gate_up (crates/oominf-core/src/backend.rs:825-836;
+ * crates/oominf-cuda/src/experts.rs:43-93). */
+int oom_moe_gate_up_fp8(const uint64_t* recs, const int32_t* off, const int32_t* assign_tok, int n_experts,
+                        const void* x, int x_dtype, float* h, const OomFp8Record* geo, void* stream);
+
+/* Down projection: y[a, r] = h[a] . Wd_e[r]; h f32 [A, inter]; y f32 [A, hidden].
+ * Replaces Experts::moe_down (crates/oominf-core/src/backend.rs:859-868;
+ * crates/oominf-cuda/src/experts.rs:174-209). */
+int oom_moe_down_fp8(const uint64_t* recs, const int32_t* off, int n_experts, const float* h, float* y,
+                     const OomFp8Record* geo, void* stream);
+
+/* out[t, c] = sum_s w[t, s] * y[slot_assign[t, s], c], summed in slot order.
+ * y f32 [A, H]; w f32 [T, k]; out [T, H] in out_dtype.
+ * Replaces Experts::moe_combine_slots (crates/oominf-core/src/backend.rs:896-907;
+ * crates/oominf-cuda/src/experts.rs:303-329). */
+int oom_moe_combine_slots(const float* y, const int32_t* slot_assign, const float* w, void* out, int out_dtype,
+                          int T, int H, int k, void* stream);
+
+/* Routing plan on the device: groups the T*k slots of `ids` by expert in id
+ * order, as the host does in crates/oominf-models-qwen/src/moe.rs:539-582,638-649.
+ * Writes plan[0] = n_e, then experts[E] (distinct ids, ascending; unused entries
+ * -1), off[E + 1], assign_tok[T*k], slot_assign[T*k], all i32 in that order
+ * (oom_moe_plan_size() elements), and recs[i] = all_recs[experts[i]] for i < n_e.
+ * No host synchronisation: later kernels read n_e from the device. */
+size_t oom_moe_plan_size(int T, int E, int k);
+int oom_moe_plan(const int32_t* ids, int T, int E, int k, const uint64_t* all_recs, int32_t* plan, uint64_t* recs,
+                 void* stream);
+
+/* One decode MoE FFN step on the device, with no host synchronisation: router
+ * top-k over logits f32 [T, E], routing plan, gate/up + SwiGLU, down projection
+ * and slot-order weighted combine, reading the records of the routed experts
+ * (all_recs[e] = device address of expert e's record, for all E experts) once per
+ * step for all their tokens. x [T, hidden] in x_dtype; out [T, hidden] in
+ * out_dtype; ids i32 [T, k] and weights f32 [T, k] are written as by
+ * oom_router_topk. T <= 64. The fused equivalent of Moe::forward's routed part
+ * (crates/oominf-models-qwen/src/moe.rs:290-366: router_topk, begin_routed,
+ * finish_routed, run_group, moe_combine_slots). */
+size_t oom_moe_decode_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo);
+int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T, int E,
+                       int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
+                       void* ws, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

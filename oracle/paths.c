@@ -1,0 +1,350 @@
+/*
+ * paths.c -- router, FP8 GEMV, routed experts, prefill grouped GEMM and paged
+ * decode attention, restated on the CPU in fp32.
+ * TEST INFRASTRUCTURE (the oracle): never linked into the product library.
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oom_oracle.h"
+
+static int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+/* ---- router ---------------------------------------------------------------- */
+
+/* v[i] += v[i ^ o] for o = 16, 8, 4, 2, 1 over one 32-lane warp; lane 0's value.
+ * The __shfl_xor_sync reduction of crates/oominf-cuda/kernels/ops.cu:17,24. */
+static float warp_xor_sum(float* v) {
+    for (int o = 16; o > 0; o >>= 1) {
+        float n[32];
+        for (int i = 0; i < 32; i++) n[i] = v[i] + v[i ^ o];
+        memcpy(v, n, sizeof(n));
+    }
+    return v[0];
+}
+
+/* block_sum for a 256-thread block (ops.cu:15-31): per-warp xor sums, then warp 0
+ * xor-sums the 8 warp totals (lanes past 8 hold 0). */
+static float block_sum_256(const float* per_thread) {
+    float warp_sums[8];
+    for (int w = 0; w < 8; w++) {
+        float v[32];
+        memcpy(v, per_thread + 32 * w, sizeof(v));
+        warp_sums[w] = warp_xor_sum(v);
+    }
+    float v[32] = {0};
+    for (int i = 0; i < 8; i++) v[i] = warp_sums[i];
+    return warp_xor_sum(v);
+}
+
+/* ops.cu:234-258: max, then per-thread serial sums of exp(l - max) over e = tid,
+ * tid + 256, ..., block_sum, p = exp(l - max) / sum. */
+static void router_row_probs(const float* l, int E, float* p) {
+    float mx = -INFINITY;
+    for (int e = 0; e < E; e++) mx = fmaxf(mx, l[e]);
+    float part[256];
+    for (int t = 0; t < 256; t++) {
+        float s = 0.0f;
+        for (int e = t; e < E; e += 256) s += expf(l[e] - mx);
+        part[t] = s;
+    }
+    float sum = block_sum_256(part);
+    for (int e = 0; e < E; e++) p[e] = expf(l[e] - mx) / sum;
+}
+
+void oracle_router_probs(const float* logits, int T, int E, float* p) {
+    for (int t = 0; t < T; t++) router_row_probs(logits + (size_t)t * E, E, p + (size_t)t * E);
+}
+
+/* ops.cu:259-293: k rounds of argmax (ties to the lower id), picks marked -2;
+ * weights = p / (sum of picked p in pick order). */
+void oracle_router_topk(const float* logits, int T, int E, int k, int32_t* ids, float* weights) {
+    float* p = (float*)malloc(sizeof(float) * (size_t)E);
+    for (int t = 0; t < T; t++) {
+        router_row_probs(logits + (size_t)t * E, E, p);
+        float chosen_p[32];
+        int chosen[32];
+        for (int r = 0; r < k; r++) {
+            float bv = -3.0f;
+            int bi = 0x7fffffff;
+            for (int e = 0; e < E; e++)
+                if (p[e] > bv || (p[e] == bv && e < bi)) {
+                    bv = p[e];
+                    bi = e;
+                }
+            chosen[r] = bi;
+            chosen_p[r] = bv;
+            p[bi] = -2.0f;
+        }
+        float picked = 0.0f;
+        for (int r = 0; r < k; r++) picked += chosen_p[r];
+        for (int r = 0; r < k; r++) {
+            ids[t * k + r] = chosen[r];
+            weights[t * k + r] = chosen_p[r] / picked;
+        }
+    }
+    free(p);
+}
+
+/* ---- dense FP8 GEMV ---------------------------------------------------------- */
+
+/* ops.cu:374-399: w = e4m3(q) * scale, acc += x * w, fp32. */
+void oracle_gemv_fp8(const float* x, int T, const uint8_t* q, const float* scale, int layout, int64_t N,
+                     int64_t K, float* y) {
+    for (int t = 0; t < T; t++)
+        for (int64_t n = 0; n < N; n++) {
+            float acc = 0.0f;
+            for (int64_t c = 0; c < K; c++)
+                acc += x[(size_t)t * K + c] * (oracle_e4m3_to_f32(q[n * K + c]) * oracle_scale_at(scale, N, K, layout, n, c));
+            y[(size_t)t * N + n] = acc;
+        }
+}
+
+/* ---- routed experts ---------------------------------------------------------- */
+
+int oracle_moe_plan(const int32_t* ids, int T, int k, int E, int32_t* experts, int32_t* off, int32_t* assign_tok,
+                    int32_t* slot_assign) {
+    int A = T * k;
+    int32_t* count = (int32_t*)calloc((size_t)E, sizeof(int32_t));
+    for (int s = 0; s < A; s++) {
+        if (ids[s] < 0 || ids[s] >= E) {
+            free(count);
+            return -1;
+        }
+        count[ids[s]]++;
+    }
+    /* moe.rs:549-551: the distinct experts in id order (all resident: no reorder). */
+    int n_e = 0;
+    int32_t* start = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+    int a = 0;
+    for (int e = 0; e < E; e++) {
+        start[e] = a;
+        if (count[e]) {
+            experts[n_e] = e;
+            off[n_e] = a;
+            n_e++;
+            a += count[e];
+        }
+    }
+    off[n_e] = a;
+    /* moe.rs:641-647: within an expert, its slots in slot order. */
+    for (int s = 0; s < A; s++) {
+        int pos = start[ids[s]]++;
+        assign_tok[pos] = s / k;
+        slot_assign[s] = pos;
+    }
+    free(start);
+    free(count);
+    return n_e;
+}
+
+static inline float siluf(float v) { return v / (1.0f + expf(-v)); }
+
+/* row `r` of an e4m3 [rows, cols] matrix with 128x128 scales, dotted with x. */
+static float dot_row(const uint8_t* w, const float* s, int64_t rows, int64_t cols, int64_t r, const float* x) {
+    float acc = 0.0f;
+    for (int64_t c = 0; c < cols; c++)
+        acc += x[c] * (oracle_e4m3_to_f32(w[r * cols + c]) * oracle_scale_at(s, rows, cols, OOM_SCALE_128X128, r, c));
+    return acc;
+}
+
+void oracle_moe_gate_up_fp8(const uint8_t* const* recs, const int32_t* off, const int32_t* assign_tok, int n_e,
+                            const float* x, float* h, const OomFp8Record* geo) {
+    int64_t H = geo->hidden, I = geo->inter;
+    for (int i = 0; i < n_e; i++) {
+        const uint8_t* rec = recs[i];
+        const uint8_t* gw = rec + geo->gate_weight;
+        const uint8_t* uw = rec + geo->up_weight;
+        const float* gs = (const float*)(rec + geo->gate_scale);
+        const float* us = (const float*)(rec + geo->up_scale);
+        for (int a = off[i]; a < off[i + 1]; a++) {
+            const float* xt = x + (size_t)assign_tok[a] * H;
+            for (int64_t j = 0; j < I; j++) {
+                float g = dot_row(gw, gs, I, H, j, xt);
+                float u = dot_row(uw, us, I, H, j, xt);
+                h[(size_t)a * I + j] = siluf(g) * u;
+            }
+        }
+    }
+}
+
+void oracle_moe_down_fp8(const uint8_t* const* recs, const int32_t* off, int n_e, const float* h, float* y,
+                         const OomFp8Record* geo) {
+    int64_t H = geo->hidden, I = geo->inter;
+    for (int i = 0; i < n_e; i++) {
+        const uint8_t* rec = recs[i];
+        const uint8_t* dw = rec + geo->down_weight;
+        const float* ds = (const float*)(rec + geo->down_scale);
+        for (int a = off[i]; a < off[i + 1]; a++)
+            for (int64_t r = 0; r < H; r++) y[(size_t)a * H + r] = dot_row(dw, ds, H, I, r, h + (size_t)a * I);
+    }
+}
+
+void oracle_moe_combine_slots(const float* y, const int32_t* slot_assign, const float* w, float* out, int T,
+                              int H, int k) {
+    for (int t = 0; t < T; t++)
+        for (int c = 0; c < H; c++) {
+            float acc = 0.0f;
+            for (int s = 0; s < k; s++) acc += w[t * k + s] * y[(size_t)slot_assign[t * k + s] * H + c];
+            out[(size_t)t * H + c] = acc;
+        }
+}
+
+int oracle_moe_decode_fp8(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
+                          const OomFp8Record* geo, int32_t* ids, float* weights, float* out) {
+    int A = T * k;
+    int64_t H = geo->hidden, I = geo->inter;
+    oracle_router_topk(logits, T, E, k, ids, weights);
+    int32_t* experts = (int32_t*)malloc(sizeof(int32_t) * (size_t)(A + 1));
+    int32_t* off = (int32_t*)malloc(sizeof(int32_t) * (size_t)(A + 2));
+    int32_t* tok = (int32_t*)malloc(sizeof(int32_t) * (size_t)A);
+    int32_t* slot = (int32_t*)malloc(sizeof(int32_t) * (size_t)A);
+    int n_e = oracle_moe_plan(ids, T, k, E, experts, off, tok, slot);
+    if (n_e < 0) {
+        free(experts); free(off); free(tok); free(slot);
+        return -1;
+    }
+    const uint8_t** recs = (const uint8_t**)malloc(sizeof(void*) * (size_t)(n_e ? n_e : 1));
+    for (int i = 0; i < n_e; i++) recs[i] = all_recs[experts[i]];
+    float* h = (float*)malloc(sizeof(float) * (size_t)A * (size_t)I);
+    float* y = (float*)malloc(sizeof(float) * (size_t)A * (size_t)H);
+    oracle_moe_gate_up_fp8(recs, off, tok, n_e, x, h, geo);
+    oracle_moe_down_fp8(recs, off, n_e, h, y, geo);
+    oracle_moe_combine_slots(y, slot, weights, out, T, (int)H, k);
+    free(h); free(y); free(recs); free(experts); free(off); free(tok); free(slot);
+    return 0;
+}
+
+/* ---- prefill grouped GEMM (FP8 x FP8) ---------------------------------------- */
+
+void oracle_grouped_gemm_fp8(const uint8_t* const* recs, const int32_t* off, const int32_t* rows, int n_e,
+                             const uint8_t* xq, const float* x_scale, int x_group, float* y, int64_t N, int64_t K,
+                             int64_t w_off, int64_t s_off) {
+    int64_t nkb = cdiv(K, 128);
+    float* xd = (float*)malloc(sizeof(float) * (size_t)K);
+    for (int i = 0; i < n_e; i++) {
+        const uint8_t* W = recs[i] + w_off;
+        const float* S = (const float*)(recs[i] + s_off);
+        for (int a = off[i]; a < off[i + 1]; a++) {
+            int64_t row = rows ? rows[a] : a;
+            for (int64_t c = 0; c < K; c++) xd[c] = oracle_e4m3_to_f32(xq[row * K + c]);
+            for (int64_t r = 0; r < N; r++) {
+                float acc = 0.0f;
+                for (int64_t kb = 0; kb < nkb; kb++) {
+                    float blk = 0.0f;
+                    for (int64_t c = kb * 128; c < K && c < (kb + 1) * 128; c++)
+                        blk += xd[c] * oracle_e4m3_to_f32(W[r * K + c]);
+                    float ws = S[(r / 128) * nkb + kb];
+                    if (x_group) acc += blk * (ws * x_scale[row * nkb + kb]);
+                    else acc += blk * ws;
+                }
+                y[(size_t)a * N + r] = x_group ? acc : acc * x_scale[row];
+            }
+        }
+    }
+    free(xd);
+}
+
+int oracle_moe_prefill_fp8(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
+                           const OomFp8Record* geo, int32_t* ids, float* weights, float* out) {
+    int A = T * k;
+    int64_t H = geo->hidden, I = geo->inter;
+    oracle_router_topk(logits, T, E, k, ids, weights);
+    int32_t* experts = (int32_t*)malloc(sizeof(int32_t) * (size_t)(A + 1));
+    int32_t* off = (int32_t*)malloc(sizeof(int32_t) * (size_t)(A + 2));
+    int32_t* tok = (int32_t*)malloc(sizeof(int32_t) * (size_t)A);
+    int32_t* slot = (int32_t*)malloc(sizeof(int32_t) * (size_t)A);
+    int n_e = oracle_moe_plan(ids, T, k, E, experts, off, tok, slot);
+    if (n_e < 0) {
+        free(experts); free(off); free(tok); free(slot);
+        return -1;
+    }
+    const uint8_t** recs = (const uint8_t**)malloc(sizeof(void*) * (size_t)(n_e ? n_e : 1));
+    for (int i = 0; i < n_e; i++) recs[i] = all_recs[experts[i]];
+    uint8_t* xq = (uint8_t*)malloc((size_t)T * (size_t)H);
+    float* xs = (float*)malloc(sizeof(float) * (size_t)T);
+    oracle_quantize_act(x, T, H, 0, xq, xs);
+    float* g = (float*)malloc(sizeof(float) * (size_t)A * (size_t)I);
+    float* u = (float*)malloc(sizeof(float) * (size_t)A * (size_t)I);
+    oracle_grouped_gemm_fp8(recs, off, tok, n_e, xq, xs, 0, g, I, H, geo->gate_weight, geo->gate_scale);
+    oracle_grouped_gemm_fp8(recs, off, tok, n_e, xq, xs, 0, u, I, H, geo->up_weight, geo->up_scale);
+    for (size_t i = 0; i < (size_t)A * (size_t)I; i++) g[i] = siluf(g[i]) * u[i];
+    int64_t nib = cdiv(I, 128);
+    uint8_t* hq = (uint8_t*)malloc((size_t)A * (size_t)I);
+    float* hs = (float*)malloc(sizeof(float) * (size_t)A * (size_t)nib);
+    oracle_quantize_act(g, A, I, 128, hq, hs);
+    float* y = (float*)malloc(sizeof(float) * (size_t)A * (size_t)H);
+    oracle_grouped_gemm_fp8(recs, off, NULL, n_e, hq, hs, 128, y, H, I, geo->down_weight, geo->down_scale);
+    oracle_moe_combine_slots(y, slot, weights, out, T, (int)H, k);
+    free(y); free(hq); free(hs); free(g); free(u); free(xq); free(xs);
+    free(recs); free(experts); free(off); free(tok); free(slot);
+    return n_e;
+}
+
+/* ---- paged GQA decode attention ---------------------------------------------- */
+
+/* attention.cu:449-548 for one query token: key tiles of 16; per row the tile's
+ * scores s = (q . k) * scale (dot in d order), tile max by a 16-lane xor tree,
+ * e = exp(s - m_new), tile sum by the same tree, l = l * exp(m_old - m_new) + sum,
+ * acc = acc * corr + sum_j e_j v_j in key order; out = acc / l. */
+static float tree16_sum(const float* v) {
+    float a[16];
+    memcpy(a, v, sizeof(a));
+    for (int o = 8; o > 0; o >>= 1) {
+        float n[16];
+        for (int i = 0; i < 16; i++) n[i] = a[i] + a[i ^ o];
+        memcpy(a, n, sizeof(a));
+    }
+    return a[0];
+}
+
+void oracle_attn_decode_paged(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                              const int32_t* page_table, int page_size, int kv_len, int H, int Hkv, int D,
+                              float scale, float* out) {
+    int G = H / Hkv;
+    float* qf = (float*)malloc(sizeof(float) * (size_t)D);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)D);
+    float* vrow = (float*)malloc(sizeof(float) * 16 * (size_t)D);
+    for (int h = 0; h < H; h++) {
+        int kvh = h / G;
+        for (int d = 0; d < D; d++) qf[d] = oracle_bf16_to_f32(q[(size_t)h * D + d]);
+        for (int d = 0; d < D; d++) acc[d] = 0.0f;
+        float m = -INFINITY, l = 0.0f;
+        for (int j0 = 0; j0 < kv_len; j0 += 16) {
+            float s[16], e[16];
+            for (int jj = 0; jj < 16; jj++) {
+                int j = j0 + jj;
+                if (j >= kv_len) {
+                    s[jj] = -INFINITY;
+                    continue;
+                }
+                size_t row = ((size_t)page_table[j / page_size] * page_size + (size_t)(j % page_size)) * Hkv + kvh;
+                const uint16_t* kr = k_pages + row * D;
+                const uint16_t* vr = v_pages + row * D;
+                float dot = 0.0f;
+                for (int d = 0; d < D; d++) dot += qf[d] * oracle_bf16_to_f32(kr[d]);
+                s[jj] = dot * scale;
+                for (int d = 0; d < D; d++) vrow[jj * D + d] = oracle_bf16_to_f32(vr[d]);
+            }
+            float mt = -INFINITY;
+            for (int jj = 0; jj < 16; jj++) mt = fmaxf(mt, s[jj]);
+            float mn = fmaxf(m, mt);
+            for (int jj = 0; jj < 16; jj++) e[jj] = (mn == -INFINITY || s[jj] == -INFINITY) ? 0.0f : expf(s[jj] - mn);
+            float sum = tree16_sum(e);
+            float corr = mn == -INFINITY ? 1.0f : expf(m - mn);
+            l = l * corr + sum;
+            m = mn;
+            for (int d = 0; d < D; d++) {
+                float a = acc[d] * corr;
+                for (int jj = 0; jj < 16; jj++)
+                    if (j0 + jj < kv_len) a += e[jj] * vrow[jj * D + d];
+                acc[d] = a;
+            }
+        }
+        for (int d = 0; d < D; d++) out[(size_t)h * D + d] = acc[d] / l;
+    }
+    free(qf);
+    free(acc);
+    free(vrow);
+}

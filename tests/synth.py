@@ -1,0 +1,98 @@
+"""Seeded synthetic inputs for the hot path's configurations (shared by tests and bench).
+
+Weights are drawn from N(0, 0.02) (xorshift64* + Box-Muller, as the reference's
+tests draw them: crates/oominf-cuda/tests/kv_cache.rs:10-24), rounded to bf16 and
+quantised to e4m3 with fp32 block scales on the host, as the reference's loader
+quantises dense FP8 weights (crates/oominf-core/src/fp8.rs:52-88).
+Expert e's part p (0 gate, 1 up, 2 down) comes from stream oracle.seed(seed, 3 e + p).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+WEIGHT_STD = 0.02
+
+
+def expert_record(geo: oracle.Fp8Record, seed: int, e: int, stride: int | None = None) -> np.ndarray:
+    """One fp8-e4m3-b128 expert record (uint8, `stride` bytes) of expert e."""
+    stride = stride or oracle.record_stride(geo)
+    rec = np.zeros(stride, dtype=np.uint8)
+    H, I = geo.hidden, geo.inter
+    parts = [(geo.gate_weight, geo.gate_scale, I, H), (geo.up_weight, geo.up_scale, I, H),
+             (geo.down_weight, geo.down_scale, H, I)]
+    for p, (wo, so, n, k) in enumerate(parts):
+        w = oracle.gaussian_bf16((n, k), oracle.seed(seed, 3 * e + p), WEIGHT_STD)
+        q, s = oracle.quantize(w, oracle.SCALE_128X128)
+        rec[wo:wo + n * k] = q.reshape(-1)
+        rec[so:so + s.size * 4] = s.view(np.uint8)
+    return rec
+
+
+def expert_records(geo: oracle.Fp8Record, seed: int, E: int, only=None) -> list[np.ndarray]:
+    """Records of E experts; experts outside `only` (when given) are left zero."""
+    stride = oracle.record_stride(geo)
+    return [expert_record(geo, seed, e, stride) if only is None or e in only else np.zeros(stride, np.uint8)
+            for e in range(E)]
+
+
+def constant_record(geo: oracle.Fp8Record, code: int = 0x38, scale: float = 1.0) -> np.ndarray:
+    """A record whose every weight is e4m3 `code` and every scale `scale`."""
+    rec = np.zeros(oracle.record_stride(geo), dtype=np.uint8)
+    H, I = geo.hidden, geo.inter
+    for wo, so, n, k in [(geo.gate_weight, geo.gate_scale, I, H), (geo.up_weight, geo.up_scale, I, H),
+                         (geo.down_weight, geo.down_scale, H, I)]:
+        rec[wo:wo + n * k] = code
+        nb = ((n + 127) // 128) * ((k + 127) // 128)
+        rec[so:so + nb * 4] = np.full(nb, scale, dtype=np.float32).view(np.uint8)
+    return rec
+
+
+def record_weights(rec: np.ndarray, geo: oracle.Fp8Record):
+    """Dequantised (gate [I, H], up [I, H], down [H, I]) fp32 weights of a record,
+    decoded with torch's float8_e4m3fn (a library decode independent of the oracle)."""
+    import torch
+
+    H, I = geo.hidden, geo.inter
+    out = []
+    for wo, so, n, k in [(geo.gate_weight, geo.gate_scale, I, H), (geo.up_weight, geo.up_scale, I, H),
+                         (geo.down_weight, geo.down_scale, H, I)]:
+        q = torch.from_numpy(rec[wo:wo + n * k].copy()).view(torch.float8_e4m3fn).float().numpy().reshape(n, k)
+        nb = ((n + 127) // 128) * ((k + 127) // 128)
+        s = rec[so:so + nb * 4].view(np.float32).reshape((n + 127) // 128, (k + 127) // 128)
+        out.append(q * s[np.arange(n) // 128][:, np.arange(k) // 128])
+    return out
+
+
+def decode_logits(seed: int, T: int, E: int, zipf: float | None = None) -> np.ndarray:
+    """Router logits [T, E] from N(0, 1), plus a Zipf(s) popularity bias when given."""
+    logits = oracle.gaussian(T * E, oracle.seed(seed, 1 << 40)).reshape(T, E)
+    if zipf is not None:
+        logits = logits + oracle.zipf_bias(E, zipf, oracle.seed(seed, (1 << 40) + 1))[None, :]
+    return np.ascontiguousarray(logits, dtype=np.float32)
+
+
+def activations_bf16(seed: int, T: int, H: int) -> np.ndarray:
+    """x [T, H] bf16 bits from N(0, 1)."""
+    return oracle.gaussian_bf16((T, H), oracle.seed(seed, (1 << 40) + 2), 1.0)
+
+
+def f64_moe(logits_ids_w, x: np.ndarray, recs, geo: oracle.Fp8Record) -> np.ndarray:
+    """f64 evaluation of the routed MoE FFN over dequantised weights: per token,
+    sum_s w_s down(silu(g) * u) with the given ids and weights."""
+    ids, w = logits_ids_w
+    T, k = ids.shape
+    out = np.zeros((T, geo.hidden))
+    cache = {}
+    for t in range(T):
+        xt = x[t].astype(np.float64)
+        for s in range(k):
+            e = int(ids[t, s])
+            if e not in cache:
+                cache[e] = [m.astype(np.float64) for m in record_weights(recs[e], geo)]
+            g, u, d = cache[e]
+            gv, uv = g @ xt, u @ xt
+            h = gv / (1.0 + np.exp(-gv)) * uv
+            out[t] += float(w[t, s]) * (d @ h)
+    return out
