@@ -1,0 +1,217 @@
+"""Benchmark of the MI355X decode hot path (one GPU).
+
+Default workload: one FP8 MoE FFN decode step at batch 1 -- router top-8 over 128
+experts from fresh N(0, 1) logits, fused gate/up + SiLU*mul, down projection and
+slot-order weighted combine, hidden 4096, expert intermediate 1536, e4m3 weights with
+128x128-block fp32 scales quantised from N(0, 0.02) -- run through
+oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
+(2 x 2.42 GB) alternate between steps so weights stream from HBM, not from the
+256 MB Infinity Cache.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config decode1|decode16|gemv]
+
+Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
+kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
+this host's cores over a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "MoE FP8 decode layer µs/token + achieved HBM GB/s (% of MI355X peak), 1 GPU"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def quantize_blocks_dev(w, torch):
+    """e4m3 codes and 128x128 fp32 scales of a bf16-valued [n, k] tensor on the device:
+    scale = block absmax / 448 (1 for a zero block), q = e4m3(w / scale) rounded to
+    nearest even and saturated at +-448 (crates/oominf-core/src/fp8.rs:52-88 per block)."""
+    n, k = w.shape
+    b = w.reshape(n // 128, 128, k // 128, 128)
+    amax = b.abs().amax(dim=(1, 3))
+    s = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    q = (b / s[:, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).reshape(n, k)
+    return q, s.contiguous()
+
+
+def make_expert_set(E, geo, stride, seed, torch):
+    """[E, stride] uint8 records of E experts, weights N(0, 0.02) rounded to bf16."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    buf = torch.zeros((E, stride), dtype=torch.uint8, device="cuda")
+    H, I = geo.hidden, geo.inter
+    parts = [(geo.gate_weight, geo.gate_scale, I, H), (geo.up_weight, geo.up_scale, I, H),
+             (geo.down_weight, geo.down_scale, H, I)]
+    for e in range(E):
+        for wo, so, n, k in parts:
+            w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16).float()
+            q, s = quantize_blocks_dev(w, torch)
+            buf[e, wo:wo + n * k] = q.reshape(-1)
+            buf[e, so:so + s.numel() * 4] = s.reshape(-1).view(torch.uint8)
+    return buf
+
+
+def usable_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_decode(host_recs, geo, E, k, T, budget_s=10.0):
+    """The reference CPU path (oracle restatement of crates/oominf-cpu) on this host:
+    router -> plan -> HostExperts -> slot-order combine per step, fresh logits each
+    step, for about `budget_s` seconds. Returns (us_per_token, cores, steps)."""
+    import numpy as np
+
+    import oracle
+
+    cores = usable_cores()
+    rng = np.random.default_rng(5)
+    x = oracle.bf16_to_f32(oracle.bf16_from_f32(rng.standard_normal((T, geo.hidden)).astype(np.float32)))
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        logits = rng.standard_normal((T, E)).astype(np.float32)
+        ids, w = oracle.router_topk(logits, k)
+        experts, off, tok, slot = oracle.moe_plan(ids, E)
+        jobs = [tok[off[i]:off[i + 1]] for i in range(len(experts))]
+        y = oracle.host_experts(geo, [host_recs[e] for e in experts], jobs, x, cores)
+        oracle.moe_combine_slots(y, slot, w)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and steps >= 3:
+            break
+    return el / steps / T * 1e6, cores, steps
+
+
+def bench_decode(args, T, zipf):
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    E, k, H, I = 128, 8, 4096, 1536
+    geo = hip.record_geometry(H, I)
+    stride = hip.record_stride(geo)
+    log(f"bench: decode T={T} E={E} k={k} H={H} I={I}; building 2 expert sets of {E * stride / 1e9:.2f} GB")
+    sets = [make_expert_set(E, geo, stride, 1234 + s, torch) for s in range(2)]
+    addrs = [torch.tensor([b.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
+             for b in sets]
+    n = args.warmup + args.steps
+    g = torch.Generator(device="cuda")
+    g.manual_seed(99)
+    logits = torch.randn((n, T, E), generator=g, device="cuda")
+    if zipf is not None:
+        import oracle
+
+        bias = torch.from_numpy(oracle.zipf_bias(E, zipf, 7)).cuda()
+        logits = logits + bias
+    logits = logits.contiguous()
+    x = (torch.randn((T, H), generator=g, device="cuda")).to(torch.bfloat16)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ids = torch.empty((n, T, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n, T, k), dtype=torch.float32, device="cuda")
+    ws = torch.zeros(hip.moe_decode_fp8_workspace_size(T, E, k, geo), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        hip.moe_decode_fp8(logits[i], x, addrs[i % 2], k, geo, ids[i], wts[i], out, ws, stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(args.warmup, n):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    # algorithmic bytes: each distinct routed expert's weights and scales once, x and out
+    idn = ids[args.warmup:].cpu().numpy()
+    distinct = np.array([len(np.unique(s)) for s in idn])
+    per_expert = 3 * H * I + 3 * ((H + 127) // 128) * ((I + 127) // 128) * 4
+    bytes_step = float(distinct.mean()) * per_expert + 2 * T * H * 2
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": ms * 1e3 / T,
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 weights, bf16 activations, fp32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": f"MoE FFN decode step, batch {T}: 128 experts top-8, hidden 4096, inter 1536, "
+                               "e4m3 128x128-block-scaled weights from N(0,0.02), bf16 x, fresh N(0,1) logits"
+                               + (f" + Zipf({zipf}) bias" if zipf else "") + "; 2 expert sets alternate past the MALL",
+                   "batch": T, "experts": E, "top_k": k, "hidden": H, "inter": I,
+                   "distinct_experts_per_step": float(distinct.mean())},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": None, "kernel": "oom_moe_decode_fp8 step (all its kernels)",
+                     "algorithmic_bytes_per_step": bytes_step},
+    }
+    if not args.no_cpu:
+        host = sets[0].cpu().numpy()
+        import oracle
+
+        ogeo = oracle.record_geometry(H, I)
+        us, cores, nsteps = cpu_baseline_decode([host[e] for e in range(E)], ogeo, E, k, T, args.cpu_seconds)
+        res["cpu_baseline"] = {"value": us, "unit": "us/token", "cores": cores, "kind": "port",
+                               "sample": f"{nsteps} steps of the same batch-{T} decode MoE layer (fresh logits), "
+                                         f"oracle restatement of crates/oominf-cpu HostExperts on {cpu_model()}"}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build measures one MI355X (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.config == "decode1":
+        res = bench_decode(args, 1, None)
+    else:
+        res = bench_decode(args, 16, 1.1)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,177 @@
+"""homelab_amd: MI355X (gfx950) kernels for oom-inference's decode hot path.
+
+The product is liboom_hip.so, a C ABI (include/oom_hip.h) that an `oominf-rocm`
+backend crate binds. This module loads that library with ctypes so tests and the
+bench call exactly the entry points the engine would; torch provides device memory
+and streams only. There is no fallback: without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboom_hip.so")
+
+OK = 0
+F32, BF16 = 0, 1
+SCALE_ROW, SCALE_1X128, SCALE_128X128 = 0, 1, 2
+
+_lib = None
+
+
+class OomError(RuntimeError):
+    pass
+
+
+class Fp8Record(ctypes.Structure):
+    """OomFp8Record: byte offsets of an FP8 expert record's parts."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "hidden", "inter", "gate_weight", "gate_scale", "up_weight", "up_scale", "down_weight", "down_scale")]
+
+
+# entry point -> (restype, argtypes); every symbol include/oom_hip.h declares
+P, I32, I64, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+SIGNATURES = {
+    "oom_last_error": (ctypes.c_char_p, []),
+    "oom_workspace_init": (I32, [P, SZ, P]),
+    "oom_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
+    "oom_gemv_fp8_workspace_size": (SZ, [I32, I64, I64]),
+    "oom_gemv_fp8": (I32, [P, I32, P, P, I32, P, I32, I32, I64, I64, P, SZ, P]),
+    "oom_moe_gate_up_fp8": (I32, [P, P, P, I32, P, I32, P, P, P]),
+    "oom_moe_down_fp8": (I32, [P, P, I32, P, P, P, P]),
+    "oom_moe_combine_slots": (I32, [P, P, P, P, I32, I32, I32, I32, P]),
+    "oom_moe_plan_size": (SZ, [I32, I32, I32]),
+    "oom_moe_plan": (I32, [P, I32, I32, I32, P, P, P, P]),
+    "oom_moe_decode_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
+    "oom_moe_decode_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded product library; raises if it was not built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OomError(f"{LIB_PATH} is missing: build it with `python -m homelab_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise OomError(f"status {rc}: {lib().oom_last_error().decode()}")
+
+
+def _ptr(t) -> ctypes.c_void_p | None:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return ctypes.c_void_p(t)
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None) -> ctypes.c_void_p:
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dtype_code(t) -> int:
+    import torch
+
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise OomError(f"unsupported activation dtype {t.dtype}")
+
+
+def record_geometry(hidden: int, inter: int) -> Fp8Record:
+    """The fp8-e4m3-b128 record layout (gate.weight, gate.scale, up.weight, up.scale,
+    down.weight, down.scale; parts 256-byte aligned)."""
+    def al(v):
+        return (v + 255) // 256 * 256
+
+    def nb(n, k):
+        return ((n + 127) // 128) * ((k + 127) // 128) * 4
+    o = 0
+    gw = o; o = al(o + inter * hidden)
+    gs = o; o = al(o + nb(inter, hidden))
+    uw = o; o = al(o + inter * hidden)
+    us = o; o = al(o + nb(inter, hidden))
+    dw = o; o = al(o + hidden * inter)
+    ds = o
+    return Fp8Record(hidden, inter, gw, gs, uw, us, dw, ds)
+
+
+def record_stride(geo: Fp8Record) -> int:
+    end = geo.down_scale + ((geo.hidden + 127) // 128) * ((geo.inter + 127) // 128) * 4
+    return (end + 4095) // 4096 * 4096
+
+
+# ---- entry points (torch tensors in, results in the given output tensors) ----------
+
+def workspace_init(ws, stream=None) -> None:
+    check(lib().oom_workspace_init(_ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
+
+
+def router_topk(logits, ids, weights, k: int, stream=None) -> None:
+    T, E = logits.shape
+    check(lib().oom_router_topk(_ptr(logits), _ptr(ids), _ptr(weights), T, E, k, _stream(stream)))
+
+
+def gemv_fp8_workspace_size(T: int, N: int, K: int) -> int:
+    return int(lib().oom_gemv_fp8_workspace_size(T, N, K))
+
+
+def gemv_fp8(x, q, scale, scale_layout: int, y, ws=None, stream=None) -> None:
+    T, K = x.shape
+    N = q.shape[0]
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().oom_gemv_fp8(_ptr(x), _dtype_code(x), _ptr(q), _ptr(scale), scale_layout, _ptr(y), _dtype_code(y),
+                             T, N, K, _ptr(ws), ws_bytes, _stream(stream)))
+
+
+def moe_gate_up_fp8(recs, off, assign_tok, n_experts: int, x, h, geo: Fp8Record, stream=None) -> None:
+    check(lib().oom_moe_gate_up_fp8(_ptr(recs), _ptr(off), _ptr(assign_tok), n_experts, _ptr(x), _dtype_code(x),
+                                    _ptr(h), ctypes.byref(geo), _stream(stream)))
+
+
+def moe_down_fp8(recs, off, n_experts: int, h, y, geo: Fp8Record, stream=None) -> None:
+    check(lib().oom_moe_down_fp8(_ptr(recs), _ptr(off), n_experts, _ptr(h), _ptr(y), ctypes.byref(geo),
+                                 _stream(stream)))
+
+
+def moe_combine_slots(y, slot_assign, w, out, stream=None) -> None:
+    T, k = w.shape
+    H = y.shape[1]
+    check(lib().oom_moe_combine_slots(_ptr(y), _ptr(slot_assign), _ptr(w), _ptr(out), _dtype_code(out), T, H, k,
+                                      _stream(stream)))
+
+
+def moe_plan_size(T: int, E: int, k: int) -> int:
+    return int(lib().oom_moe_plan_size(T, E, k))
+
+
+def moe_plan(ids, E: int, all_recs, plan, recs, stream=None) -> None:
+    T, k = ids.shape
+    check(lib().oom_moe_plan(_ptr(ids), T, E, k, _ptr(all_recs), _ptr(plan), _ptr(recs), _stream(stream)))
+
+
+def moe_decode_fp8_workspace_size(T: int, E: int, k: int, geo: Fp8Record) -> int:
+    return int(lib().oom_moe_decode_fp8_workspace_size(T, E, k, ctypes.byref(geo)))
+
+
+def moe_decode_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, out, ws, stream=None) -> None:
+    T, E = logits.shape
+    check(lib().oom_moe_decode_fp8(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k, ctypes.byref(geo),
+                                   _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
+                                   ws.numel() * ws.element_size(), _stream(stream)))

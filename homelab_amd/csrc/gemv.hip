@@ -1,0 +1,227 @@
+// Decode GEMV over e4m3 weights: y[t, n] = sum_k x[t, k] * e4m3(q[n, k]) * scale(n, k).
+//
+// Layout of the work (gfx950, wave64):
+//   - a block is 4 waves; each wave owns R consecutive rows; a split owns
+//     KCH * 1024 columns (the last split may be shorter);
+//   - lane l reads 16 e4m3 bytes (one 128-bit load) at columns c * 1024 + 16 l of
+//     chunk c, so a wave-wide load is one contiguous 1 KiB run of a row and all R x
+//     KCH loads of a wave are in flight before the first use;
+//   - the split's activations sit in LDS as fp32 in lane order (float4 i of chunk c
+//     of lane l at ((t * KCH + c) * 4 + i) * 64 + l), so a lane's ds_read_b128s are
+//     conflict-free and each feeds all R rows;
+//   - per (row, chunk) a lane's 16 products sum in fp32, are scaled by the weight
+//     block's scale (one per lane: 16 columns never straddle a 128 block) and
+//     accumulate; the R * T per-lane sums reduce over the wave in one multi-value
+//     butterfly (R * T - 1 + log2(64 / (R * T)) exchanges);
+//   - splits > 1 write fp32 partials [splits, T, N]; the last block of a row tile
+//     (a ticket per tile, reset after use) adds them in split order, so the result
+//     does not depend on block timing (crates/oominf-cuda/kernels/ops.cu:421-439).
+#include "common.hpp"
+
+namespace oom {
+
+constexpr int GEMV_WAVES = 4;
+
+template <int T, int R, int KCH, int SL, int XDT, int YDT>
+__global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ x, const uint8_t* __restrict__ q,
+                                                       const float* __restrict__ scale, void* __restrict__ y,
+                                                       float* __restrict__ partial, uint32_t* __restrict__ tickets,
+                                                       int tn, int N, int K) {
+    extern __shared__ float4 xs4[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int split = blockIdx.y, splits = gridDim.y;
+    const int klen = KCH * 1024;
+    const int k0 = split * klen;
+    const int kl = min(K, k0 + klen) - k0;
+    // stage x[t, k0 .. k0 + kl) in lane order (zeros past kl and for padded tokens)
+    float* xs = reinterpret_cast<float*>(xs4);
+    for (int i = threadIdx.x; i < T * klen; i += blockDim.x) {
+        int t = i / klen, kk = i - t * klen;
+        int c = kk >> 10, w = kk & 1023, l = w >> 4, j = w & 15;
+        float v = (t < tn && kk < kl) ? load_act<XDT>(x, (size_t)t * K + k0 + kk) : 0.0f;
+        xs[(((t * KCH + c) * 4 + (j >> 2)) * 64 + l) * 4 + (j & 3)] = v;
+    }
+    __syncthreads();
+
+    const int row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
+    const int nkb = (K + 127) >> 7;
+    float acc[T * R];
+#pragma unroll
+    for (int i = 0; i < T * R; i++) acc[i] = 0.0f;
+
+    uint4 w[R][KCH];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int row = min(row0 + r, N - 1);
+#pragma unroll
+        for (int c = 0; c < KCH; c++) {
+            int col = c * 1024 + lane * 16;
+            w[r][c] = col < kl ? *reinterpret_cast<const uint4*>(q + (size_t)row * K + k0 + col) : make_uint4(0, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        int col = k0 + c * 1024 + lane * 16;
+        float sc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int row = min(row0 + r, N - 1);
+            if constexpr (SL == OOM_SCALE_ROW) sc[r] = 1.0f;
+            else if constexpr (SL == OOM_SCALE_1X128) sc[r] = col < K ? scale[(size_t)row * nkb + (col >> 7)] : 0.0f;
+            else sc[r] = col < K ? scale[(size_t)(row >> 7) * nkb + (col >> 7)] : 0.0f;
+        }
+        float wf[R][16];
+#pragma unroll
+        for (int r = 0; r < R; r++) e4m3x16(w[r][c], wf[r]);
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            float xv[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float4 a = xs4[((t * KCH + c) * 4 + i) * 64 + lane];
+                xv[4 * i] = a.x;
+                xv[4 * i + 1] = a.y;
+                xv[4 * i + 2] = a.z;
+                xv[4 * i + 3] = a.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) p = fmaf(wf[r][i], xv[i], p);
+                acc[t * R + r] = fmaf(p, sc[r], acc[t * R + r]);
+            }
+        }
+    }
+    float tot = wave_sum_multi<T * R>(acc, lane);
+    const int g = lane / (64 / (T * R));  // value g of the butterfly: t = g / R, r = g % R
+    const bool writer = (lane % (64 / (T * R))) == 0;
+    const int t = g / R, r = g % R, row = row0 + r;
+    if (writer && row < N && t < tn) {
+        if constexpr (SL == OOM_SCALE_ROW) tot *= scale[row];
+        if (splits == 1) store_out<YDT>(y, (size_t)t * N + row, tot);
+        else partial[((size_t)split * T + t) * N + row] = tot;
+    }
+    if (splits == 1) return;
+    __shared__ bool last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(&tickets[blockIdx.x], 1u) == (unsigned)splits - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    const int tile = GEMV_WAVES * R, first = blockIdx.x * tile;
+    for (int i = threadIdx.x; i < tn * tile; i += blockDim.x) {
+        int tt = i / tile, n = first + i % tile;
+        if (n >= N) continue;
+        float sum = 0.0f;
+        for (int s = 0; s < splits; s++) sum += __builtin_nontemporal_load(&partial[((size_t)s * T + tt) * N + n]);
+        store_out<YDT>(y, (size_t)tt * N + n, sum);
+    }
+    if (threadIdx.x == 0) tickets[blockIdx.x] = 0;
+}
+
+// Launch geometry of one call (shared by the workspace query and the launch).
+struct GemvPlan {
+    int tp, R, kch, splits, tiles;
+    size_t lds;
+};
+
+static GemvPlan gemv_plan(int T, int64_t N, int64_t K) {
+    GemvPlan p;
+    p.tp = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16;
+    p.R = p.tp >= 8 ? 2 : 4;
+    // x of one split in LDS: tp * kch * 4 KiB <= 64 KiB
+    int kch_max = std::max(1, 16 / p.tp);
+    kch_max = std::min(kch_max, 4);
+    int kchunks = (int)cdiv(K, 1024);
+    p.tiles = (int)cdiv(N, (int64_t)GEMV_WAVES * p.R);
+    // enough blocks to cover the CUs (>= 512 blocks), but a split never shorter than 1 KiB
+    int want = (int)std::max<int64_t>(1, cdiv(512, p.tiles));
+    int splits = std::max<int>((int)cdiv(kchunks, kch_max), std::min(want, kchunks));
+    p.kch = (int)cdiv(kchunks, splits);
+    p.kch = p.kch <= 1 ? 1 : p.kch <= 2 ? 2 : 4;
+    p.splits = (int)cdiv(kchunks, p.kch);
+    p.lds = (size_t)p.tp * p.kch * 1024 * sizeof(float);
+    return p;
+}
+
+template <int T, int R, int KCH>
+static void launch_gemv(const GemvPlan& p, int sl, int xdt, int ydt, const void* x, const uint8_t* q, const float* s,
+                        void* y, float* part, uint32_t* tk, int tn, int N, int K, hipStream_t st) {
+    dim3 grid(p.tiles, p.splits), block(256);
+#define GEMV_CASE(SL, XD, YD)                                                                                     \
+    if (sl == SL && xdt == XD && ydt == YD) {                                                                     \
+        hipLaunchKernelGGL((gemv_fp8_kernel<T, R, KCH, SL, XD, YD>), grid, block, p.lds, st, x, q, s, y, part, tk, tn, \
+                           N, K);                                                                                 \
+        return;                                                                                                   \
+    }
+#define GEMV_DT(SL)                   \
+    GEMV_CASE(SL, OOM_F32, OOM_F32)   \
+    GEMV_CASE(SL, OOM_F32, OOM_BF16)  \
+    GEMV_CASE(SL, OOM_BF16, OOM_F32)  \
+    GEMV_CASE(SL, OOM_BF16, OOM_BF16)
+    GEMV_DT(OOM_SCALE_ROW)
+    GEMV_DT(OOM_SCALE_1X128)
+    GEMV_DT(OOM_SCALE_128X128)
+#undef GEMV_DT
+#undef GEMV_CASE
+}
+
+template <int T, int R>
+static void launch_gemv_k(const GemvPlan& p, int sl, int xdt, int ydt, const void* x, const uint8_t* q,
+                          const float* s, void* y, float* part, uint32_t* tk, int tn, int N, int K, hipStream_t st) {
+    switch (p.kch) {
+        case 1: launch_gemv<T, R, 1>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
+        case 2: launch_gemv<T, R, 2>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
+        default:
+            if constexpr (T <= 4) launch_gemv<T, R, 4>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st);
+            break;
+    }
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+}  // namespace oom
+
+extern "C" size_t oom_gemv_fp8_workspace_size(int T, int64_t N, int64_t K) {
+    if (T < 1 || N < 1 || K < 1) return 0;
+    oom::GemvPlan p = oom::gemv_plan(T, N, K);
+    if (p.splits == 1) return 0;
+    return oom::align256((size_t)p.splits * p.tp * N * sizeof(float)) + (size_t)p.tiles * sizeof(uint32_t);
+}
+
+extern "C" int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const float* scale, int scale_layout,
+                            void* y, int y_dtype, int T, int64_t N, int64_t K, void* ws, size_t ws_bytes,
+                            void* stream) {
+    using namespace oom;
+    OOM_REQUIRE(T >= 1 && T <= 16, "oom_gemv_fp8: T must be 1..16");
+    OOM_REQUIRE(N >= 1 && K >= 16 && K % 16 == 0, "oom_gemv_fp8: K must be a positive multiple of 16");
+    OOM_REQUIRE(N <= INT32_MAX && K <= INT32_MAX && N * K <= ((int64_t)1 << 40), "oom_gemv_fp8: shape too large");
+    OOM_REQUIRE(x && q && scale && y, "oom_gemv_fp8: null buffer");
+    OOM_REQUIRE(aligned(q, 16), "oom_gemv_fp8: weights must be 16-byte aligned");
+    OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_gemv_fp8: x_dtype");
+    OOM_REQUIRE(y_dtype == OOM_F32 || y_dtype == OOM_BF16, "oom_gemv_fp8: y_dtype");
+    OOM_REQUIRE(scale_layout >= OOM_SCALE_ROW && scale_layout <= OOM_SCALE_128X128, "oom_gemv_fp8: scale_layout");
+    GemvPlan p = gemv_plan(T, N, K);
+    float* part = nullptr;
+    uint32_t* tk = nullptr;
+    if (p.splits > 1) {
+        size_t need = oom_gemv_fp8_workspace_size(T, N, K);
+        if (ws_bytes < need || ws == nullptr)
+            return fail(OOM_ERR_WORKSPACE, "oom_gemv_fp8: workspace smaller than oom_gemv_fp8_workspace_size()");
+        OOM_REQUIRE(aligned(ws, 16), "oom_gemv_fp8: workspace must be 16-byte aligned");
+        part = reinterpret_cast<float*>(ws);
+        tk = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(ws) + align256((size_t)p.splits * p.tp * N * 4));
+    }
+    hipStream_t st = as_stream(stream);
+    int n = (int)N, k = (int)K;
+    switch (p.tp) {
+        case 1: launch_gemv_k<1, 4>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
+        case 2: launch_gemv_k<2, 4>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
+        case 4: launch_gemv_k<4, 4>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
+        case 8: launch_gemv_k<8, 2>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
+        default: launch_gemv_k<16, 2>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
+    }
+    return launched("oom_gemv_fp8");
+}

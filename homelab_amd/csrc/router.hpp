@@ -1,0 +1,97 @@
+// Router top-k for one token on one wavefront, and the routing-plan layout.
+#pragma once
+
+#include "common.hpp"
+
+namespace oom {
+
+// Softmax over E logits, top k by probability (ties to the lower id), weights
+// renormalised over the picks in pick order, for one token on one wave64 whose
+// lanes are `lane` = 0..63. `probs` is E floats of LDS owned by this wave.
+// The arithmetic is the reference's (crates/oominf-cuda/kernels/ops.cu:230-294):
+// p_e = expf(l_e - max) / sum, where sum adds expf(l_e - max) per virtual thread
+// t = e mod 256 in e order, then over each 32-thread group by an xor butterfly,
+// then over the 8 group totals by the same butterfly: the reference's 256-thread
+// block_sum (ops.cu:15-31), so p has the reference's bits given the same expf.
+// Lane r < k ends with ids_out = the r-th pick and w_out = its weight.
+__device__ __forceinline__ void route_token_wave(const float* __restrict__ l, int E, int k, float* probs, int lane,
+                                                 int& id_out, float& w_out) {
+    float m = -INFINITY;
+    for (int e = lane; e < E; e += 64) m = fmaxf(m, l[e]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    // virtual thread vt = lane + 64 q (q = 0..3) of the reference's 256-thread block
+    float part[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        float s = 0.0f;
+        for (int e = lane + 64 * q; e < E; e += 256) s += expf(l[e] - m);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);  // within each 32-lane half
+        part[q] = s;
+    }
+    // group totals: group 2q is lanes 0..31 of slot q, group 2q + 1 lanes 32..63
+    float w8[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        w8[2 * q] = __shfl(part[q], 0, 64);
+        w8[2 * q + 1] = __shfl(part[q], 32, 64);
+    }
+    // the xor butterfly over lanes 0..7 (zeros above): ((g0+g4)+(g2+g6)) + ((g1+g5)+(g3+g7))
+    float sum = ((w8[0] + w8[4]) + (w8[2] + w8[6])) + ((w8[1] + w8[5]) + (w8[3] + w8[7]));
+    for (int e = lane; e < E; e += 64) probs[e] = expf(l[e] - m) / sum;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float picked = 0.0f;
+    for (int r = 0; r < k; r++) {
+        float bv = -3.0f;
+        int bi = 0x7fffffff;
+        for (int e = lane; e < E; e += 64) {
+            float p = probs[e];
+            if (p > bv || (p == bv && e < bi)) {
+                bv = p;
+                bi = e;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            float ov = __shfl_xor(bv, o, 64);
+            int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        // every lane holds the winner; picks sit below every probability from now on
+        if (lane == (bi & 63)) probs[bi] = -2.0f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        picked += bv;
+        if (lane == r) {
+            id_out = bi;
+            w_out = bv;
+        }
+    }
+    if (lane < k) w_out = w_out / picked;
+}
+
+// Routing-plan buffer (i32) of a step with T tokens, E experts and top k:
+//   [0]                     n_e, the number of distinct experts
+//   [1, 1 + E)              experts: distinct ids ascending, then -1
+//   [1 + E, 2 + 2E)         off: off[i] = first assignment of expert i; A past n_e
+//   [2 + 2E, 2 + 2E + A)    assign_tok: token of each assignment
+//   [2 + 2E + A, 2 + 2E + 2A) slot_assign: assignment of slot t * k + s
+struct PlanView {
+    int32_t* base;
+    int E, A;
+    __host__ __device__ int32_t* n_e() const { return base; }
+    __host__ __device__ int32_t* experts() const { return base + 1; }
+    __host__ __device__ int32_t* off() const { return base + 1 + E; }
+    __host__ __device__ int32_t* assign_tok() const { return base + 2 + 2 * E; }
+    __host__ __device__ int32_t* slot_assign() const { return base + 2 + 2 * E + A; }
+    static size_t size(int E, int A) { return size_t(2 + 2 * E + 2 * A); }
+};
+
+}  // namespace oom
