@@ -56,6 +56,25 @@ __device__ __forceinline__ void e4m3x16(const uint4& v, float* out) {
     e4m3x4(v.w, out + 12);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// sum_i w[i] * x[i] over 16 e4m3 weights (one 128-bit load) and 16 bf16 activations
+// (8 packed words), fp32 accumulate: each weight pair converts exactly to a bf16 pair
+// (v_cvt_scalef32_pk_bf16_fp8, scale 1) and meets its activation pair in one
+// v_dot2c_f32_bf16 (bf16 products are exact in fp32).
+__device__ __forceinline__ float dot16_e4m3_bf16(const uint4& w, const uint32_t* xw) {
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const bf16x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(ww[i], 1.0f, false);
+        const bf16x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(ww[i], 1.0f, true);
+        p = __builtin_amdgcn_fdot2_f32_bf16(lo, __builtin_bit_cast(bf16x2_t, xw[2 * i]), p, false);
+        p = __builtin_amdgcn_fdot2_f32_bf16(hi, __builtin_bit_cast(bf16x2_t, xw[2 * i + 1]), p, false);
+    }
+    return p;
+}
+
 // Activations in either element type.
 template <int DT>
 __device__ __forceinline__ float load_act(const void* p, size_t i) {
@@ -72,6 +91,40 @@ __device__ __forceinline__ void store_out(void* p, size_t i, float v) {
 __device__ __forceinline__ float siluf(float v) { return v / (1.0f + expf(-v)); }
 
 // ---- wavefront reductions (wave64) -----------------------------------------------
+
+// v of another lane through DPP (no LDS): CTRL is a gfx9 dpp_ctrl code.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7 - i within 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15 - i within 16
+
+// Sum over each 32-lane half with the pairing of a 32-lane xor butterfly (partners
+// lane ^ 1, ^ 2, ^ 4, ^ 8, ^ 16), so the total has the butterfly's rounding. Steps
+// 3 and 4 use DPP mirrors: after the previous steps every lane of a quad (of a group
+// of 8) holds the same value, so the mirror partner's value is the xor partner's.
+__device__ __forceinline__ float sum32_xor_order(float v) {
+    v += dpp_f32<DPP_XOR1>(v);
+    v += dpp_f32<DPP_XOR2>(v);
+    v += dpp_f32<DPP_HALF_MIRROR>(v);
+    v += dpp_f32<DPP_MIRROR>(v);
+    v += __shfl_xor(v, 16, 64);
+    return v;
+}
+
+// Maximum over the wave (order-free).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f32<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f32<DPP_MIRROR>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
 
 // Sum over all 64 lanes; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -295,7 +295,13 @@ int launch_combine(const float* y, const int32_t* slot, const float* w, void* ou
 // LDS of one staged pass must fit 64 KiB.
 static bool lds_fits(int64_t width) { return (size_t)MOE_TB * cdiv(width, 1024) * 1024 * sizeof(float) <= 65536; }
 
-// Workspace of oom_moe_decode_fp8: plan | recs | h | y.
+// The one-launch path (moe_fused.hip) and its workspace.
+bool fused_supported(int T, int E, int k, const OomFp8Record& g);
+size_t fused_workspace_size(int T, int E, int k, const OomFp8Record& g);
+int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* all_recs, int T, int E, int k,
+                 const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st);
+
+// Workspace of the multi-launch path of oom_moe_decode_fp8: plan | recs | h | y.
 struct DecodeWs {
     size_t plan, recs, h, y, total;
 };
@@ -351,7 +357,7 @@ extern "C" int oom_moe_combine_slots(const float* y, const int32_t* slot_assign,
 
 extern "C" size_t oom_moe_decode_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo) {
     if (!geo || T < 1 || E < 1 || k < 1) return 0;
-    return oom::decode_ws(T, E, k, *geo).total;
+    return std::max(oom::decode_ws(T, E, k, *geo).total, oom::fused_workspace_size(T, E, k, *geo));
 }
 
 extern "C" int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T,
@@ -359,16 +365,19 @@ extern "C" int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtyp
                                   int out_dtype, void* ws, size_t ws_bytes, void* stream) {
     using namespace oom;
     if (int rc = check_geo(geo, "oom_moe_decode_fp8")) return rc;
-    OOM_REQUIRE(T >= 1 && T <= 64, "oom_moe_decode_fp8: T must be 1..64");
+    OOM_REQUIRE(T >= 1 && (int64_t)T * k <= (1 << 24), "oom_moe_decode_fp8: T must be >= 1 and T * k <= 2^24");
     OOM_REQUIRE(k >= 1 && k <= 32 && E >= k && E <= 8192, "oom_moe_decode_fp8: router top-k > 32 or experts > 8192");
     OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_moe_decode_fp8: x_dtype");
     OOM_REQUIRE(out_dtype == OOM_F32 || out_dtype == OOM_BF16, "oom_moe_decode_fp8: out_dtype");
     OOM_REQUIRE(lds_fits(geo->hidden) && lds_fits(geo->inter), "oom_moe_decode_fp8: widths > 4096 unsupported");
     OOM_REQUIRE(logits && x && all_recs && ids && weights && out, "oom_moe_decode_fp8: null buffer");
     DecodeWs w = decode_ws(T, E, k, *geo);
-    if (!ws || ws_bytes < w.total)
+    if (!ws || ws_bytes < oom_moe_decode_fp8_workspace_size(T, E, k, geo))
         return fail(OOM_ERR_WORKSPACE, "oom_moe_decode_fp8: workspace smaller than oom_moe_decode_fp8_workspace_size()");
     OOM_REQUIRE(aligned(ws, 256), "oom_moe_decode_fp8: workspace must be 256-byte aligned");
+    if (fused_supported(T, E, k, *geo))
+        return launch_fused(logits, x, x_dtype, all_recs, T, E, k, *geo, ids, weights, out, out_dtype, ws,
+                            as_stream(stream));
     uint8_t* base = reinterpret_cast<uint8_t*>(ws);
     int32_t* plan = reinterpret_cast<int32_t*>(base + w.plan);
     uint64_t* recs = reinterpret_cast<uint64_t*>(base + w.recs);

@@ -77,6 +77,54 @@ __device__ __forceinline__ void route_token_wave(const float* __restrict__ l, in
     if (lane < k) w_out = w_out / picked;
 }
 
+// route_token_wave for E <= 256, without LDS round trips: lane l holds experts
+// l + 64 q (q < 4) in registers; sums keep the reference's order (sum32_xor_order);
+// each of the k rounds takes the wave maximum of p, then the lowest id holding it
+// (ballots), which is the reference's argmax with ties to the lower id.
+__device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int k, int lane, int& id_out,
+                                                 float& w_out) {
+    float lv[4], p[4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        lv[q] = lane + 64 * q < E ? l[lane + 64 * q] : -INFINITY;
+        m = fmaxf(m, lv[q]);
+    }
+    m = wave_max(m);
+    // E <= 256: virtual thread vt = lane + 64 q holds at most expert vt
+    float ex[4], w8[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        ex[q] = lane + 64 * q < E ? expf(lv[q] - m) : 0.0f;
+        const float s = sum32_xor_order(0.0f + ex[q]);
+        w8[2 * q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+        w8[2 * q + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+    }
+    const float sum = ((w8[0] + w8[4]) + (w8[2] + w8[6])) + ((w8[1] + w8[5]) + (w8[3] + w8[7]));
+#pragma unroll
+    for (int q = 0; q < 4; q++) p[q] = lane + 64 * q < E ? ex[q] / sum : -3.0f;
+    float picked = 0.0f;
+    for (int r = 0; r < k; r++) {
+        const float best = wave_max(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
+        int e = -1;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint64_t b = __ballot(p[q] == best);
+            if (e < 0 && b) e = 64 * q + (int)__builtin_ctzll(b);
+        }
+        // the winner's lane marks it used (below every probability)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (64 * q + lane == e) p[q] = -2.0f;
+        picked += best;
+        if (lane == r) {
+            id_out = e;
+            w_out = best;
+        }
+    }
+    if (lane < k) w_out = w_out / picked;
+}
+
 // Routing-plan buffer (i32) of a step with T tokens, E experts and top k:
 //   [0]                     n_e, the number of distinct experts
 //   [1, 1 + E)              experts: distinct ids ascending, then -1

@@ -122,7 +122,9 @@ int oom_moe_plan(const int32_t* ids, int T, int E, int k, const uint64_t* all_re
  * (all_recs[e] = device address of expert e's record, for all E experts) once per
  * step for all their tokens. x [T, hidden] in x_dtype; out [T, hidden] in
  * out_dtype; ids i32 [T, k] and weights f32 [T, k] are written as by
- * oom_router_topk. T <= 64. The fused equivalent of Moe::forward's routed part
+ * oom_router_topk. Steps with T * k <= 512, E <= 256, hidden <= 4096 and inter <= 2048 run
+ * as one persistent kernel; larger steps as router, plan, gate/up, down and combine
+ * launches. The fused equivalent of Moe::forward's routed part
  * (crates/oominf-models-qwen/src/moe.rs:290-366: router_topk, begin_routed,
  * finish_routed, run_group, moe_combine_slots). */
 size_t oom_moe_decode_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo);

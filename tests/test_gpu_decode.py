@@ -251,14 +251,22 @@ def decode_case(T, E, k, zipf, seed, H=4096, I=1536):
     return geo, logits, recs, xb
 
 
-@pytest.mark.parametrize("T,E,k,zipf", [(1, 128, 8, None), (16, 128, 8, 1.1), (4, 128, 8, None)])
-def test_fused_decode_full_size(hip, T, E, k, zipf):
-    """The whole decode MoE step at the benchmark's shapes (hidden 4096, inter 1536,
-    128 experts, top-8) on the device with no host sync, against the oracle."""
+@pytest.mark.parametrize("T,E,k,zipf,H,I", [(1, 128, 8, None, 4096, 1536), (16, 128, 8, 1.1, 4096, 1536),
+                                            (4, 128, 8, None, 4096, 1536), (64, 128, 8, 1.1, 1024, 512),
+                                            (3, 16, 4, None, 256, 128), (80, 64, 8, None, 1024, 512),
+                                            pytest.param(2, 300, 6, None, 512, 256, marks=pytest.mark.skip(
+                                                reason="left the GPU faulted once with the one-launch kernel's "
+                                                       "E > 256 router (cause not found on the CPU); that path is "
+                                                       "off and this case stays off the GPU until a cause is shown"))])
+def test_fused_decode_full_size(hip, T, E, k, zipf, H, I):
+    """The whole decode MoE step on the device with no host sync, against the oracle:
+    the benchmark's shapes (hidden 4096, inter 1536, 128 experts, top-8) at batch 1,
+    4 and 16, small shapes with masked lanes, and a step past the one-launch kernel's
+    limit (T * k > 512) that takes the multi-launch path."""
     import torch
 
-    print(f"case: fused decode T={T} E={E} k={k} zipf={zipf}", flush=True)
-    geo, logits, recs, xb = decode_case(T, E, k, zipf, 1000 + T)
+    print(f"case: fused decode T={T} E={E} k={k} zipf={zipf} H={H} I={I}", flush=True)
+    geo, logits, recs, xb = decode_case(T, E, k, zipf, 1000 + T, H, I)
     x = oracle.bf16_to_f32(xb)
     want_ids, want_w, want = oracle.moe_decode(logits, x, recs, k, geo)
     hgeo = hip.record_geometry(geo.hidden, geo.inter)
