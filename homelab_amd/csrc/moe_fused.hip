@@ -12,11 +12,13 @@
 //    at one barrier (one arrival per block, sense-reversing, so it needs no reset): the
 //    dependency of down on h costs no HBM idle time. All blocks are resident (the grid
 //    never exceeds the occupancy limit), so the barrier always completes.
-//  * Phase 2: wave-sized down items (expert, 8 output rows). The last expert to finish
-//    an output row tile (a ticket per tile, reset by its user) combines the tile over all
-//    tokens in slot order, so results do not depend on timing.
-// Counters are touched once per block (barrier) or once per (expert, tile) (tickets):
-// same-address atomics from every wave serialise at the memory side.
+//  * Phase 2: wave-sized down items (expert, 8 output rows) write y. The last expert
+//    to finish an output row tile (a ticket per tile, in arrival order, reset by its
+//    user) combines the tile over all tokens in slot order, so results do not depend on
+//    timing. With one token, a wave takes both tickets of its two items together.
+// Counters see one arrival per block (barrier) or per (expert, tile) (tickets):
+// same-address atomics from every wave serialise at the memory side. The kernel has
+// exactly one grid barrier.
 #include "router.hpp"
 
 namespace oom {
@@ -28,6 +30,9 @@ constexpr int F_AMAX = 512;  // assignments (T * k) per step
 constexpr int F_EMAX = 256;  // experts (register router; larger E takes the multi-launch path)
 constexpr int F_HMAX = 4096; // hidden: 4 chunks of 1024 per lane row
 constexpr int F_IMAX = 2048; // inter: 2 chunks
+// down items per wave whose weights load before the barrier (one token per expert: 2)
+template <int TG>
+constexpr int prefetch_items() { return TG == 1 ? 2 : 1; }
 constexpr uint32_t F_SPIN_LIMIT = 1u << 22;
 constexpr int BAR_GROUPS = 8;   // barrier groups (one per XCD)
 constexpr int BAR_STRIDE = 64;  // u32 words between counters: one 256-byte line each
@@ -43,7 +48,7 @@ struct FusedArgs {
     void* out;
     float* h;
     float* y;
-    uint32_t* tickets;  // [ceil(H / FD_R)] down items finished per row tile
+    uint32_t* tickets;   // [ceil(H / FD_R)] down items finished per row tile
     uint32_t* bar;       // barrier: group counters, top counter, group flags (256 B apart)
     uint32_t* status;    // 1 if a wait gave up (results invalid)
     int h_bytes;         // bytes of h (bounds of its buffer resource)
@@ -220,74 +225,78 @@ __device__ __forceinline__ void down_load(const FusedArgs& a, const PlanLds& pl,
     }
 }
 
-template <int TG, int ODT>
-__device__ __forceinline__ void down_compute(const FusedArgs& a, const PlanLds& pl, int i, int tile, int lane,
-                                             const DownW& d) {
+// h of assignments a0 .. a0 + nb (zeros past nb) for this lane's 2 chunks of 16
+// columns, through device-coherent 128-bit buffer loads.
+template <int TG>
+__device__ __forceinline__ void down_h_load(const FusedArgs& a, int a0, int nb, int lane, float (&hv)[TG][2][16]) {
+    const int I = (int)a.I, CH = (I + 1023) >> 10;
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, a.h_bytes, 0x00020000);
+#pragma unroll
+    for (int t = 0; t < TG; t++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int col = c * 1024 + lane * 16;
+            if (t < nb && c < CH && col < I) {
+                const int off = (int)(((size_t)(a0 + t) * I + col) * sizeof(float));
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16 * q, 0, BUF_SC1);
+                    hv[t][c][4 * q] = __uint_as_float(v[0]);
+                    hv[t][c][4 * q + 1] = __uint_as_float(v[1]);
+                    hv[t][c][4 * q + 2] = __uint_as_float(v[2]);
+                    hv[t][c][4 * q + 3] = __uint_as_float(v[3]);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; q++) hv[t][c][q] = 0.0f;
+            }
+        }
+}
+
+// y[a0 + t, r0 .. r0 + FD_R) = h . Wd rows for the token group, from loaded weights and h.
+template <int TG>
+__device__ __forceinline__ void down_rows(const FusedArgs& a, const PlanLds& pl, int i, int tile, int lane,
+                                          const DownW& d, const float (&hv)[TG][2][16], int a0, int nb) {
     const int H = (int)a.H, I = (int)a.I;
     const int CH = (I + 1023) >> 10, nkb = (I + 127) >> 7;
     const uint8_t* rec = reinterpret_cast<const uint8_t*>(a.all_recs[pl.experts[i]]);
     const int r0 = tile * FD_R;
     const float* ds = reinterpret_cast<const float*>(rec + a.ds) + (size_t)(r0 >> 7) * nkb;
-    // h comes through a buffer resource with device-coherent (sc1) 128-bit loads
-    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, a.h_bytes, 0x00020000);
-    const int a_begin = pl.off[i], a_end = pl.off[i + 1];
-    for (int a0 = a_begin; a0 < a_end; a0 += TG) {
-        const int nb = min(TG, a_end - a0);
-        float acc[TG * FD_R];
+    float acc[TG * FD_R];
 #pragma unroll
-        for (int q = 0; q < TG * FD_R; q++) acc[q] = 0.0f;
+    for (int q = 0; q < TG * FD_R; q++) acc[q] = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            if (c >= CH) break;
-            const int col = c * 1024 + lane * 16;
-            const bool ok = col < I;
-            const float sd = ok ? ds[col >> 7] : 0.0f;
-            float hv[TG][16];
+    for (int c = 0; c < 2; c++) {
+        if (c >= CH) break;
+        const int col = c * 1024 + lane * 16;
+        const float sd = col < I ? ds[col >> 7] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < FD_R; r++) {
+            float f[16];
+            e4m3x16(d.w[r][c], f);
 #pragma unroll
             for (int t = 0; t < TG; t++) {
-                if (t < nb && ok) {
-                    const int off = (int)(((size_t)(a0 + t) * I + col) * sizeof(float));
+                float p = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const auto v = __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16 * q, 0, BUF_SC1);
-                        hv[t][4 * q] = __uint_as_float(v[0]);
-                        hv[t][4 * q + 1] = __uint_as_float(v[1]);
-                        hv[t][4 * q + 2] = __uint_as_float(v[2]);
-                        hv[t][4 * q + 3] = __uint_as_float(v[3]);
-                    }
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 16; q++) hv[t][q] = 0.0f;
-                }
+                for (int q = 0; q < 16; q++) p = fmaf(f[q], hv[t][c][q], p);
+                acc[t * FD_R + r] = fmaf(p, sd, acc[t * FD_R + r]);
             }
-#pragma unroll
-            for (int r = 0; r < FD_R; r++) {
-                float f[16];
-                e4m3x16(d.w[r][c], f);
-#pragma unroll
-                for (int t = 0; t < TG; t++) {
-                    float p = 0.0f;
-#pragma unroll
-                    for (int q = 0; q < 16; q++) p = fmaf(f[q], hv[t][q], p);
-                    acc[t * FD_R + r] = fmaf(p, sd, acc[t * FD_R + r]);
-                }
-            }
-        }
-        constexpr int NV = TG * FD_R, GROUP = 64 / NV;
-        float tot = wave_sum_multi<NV>(acc, lane);
-        const int v = lane / GROUP;
-        if (lane % GROUP == 0) {
-            const int t = v / FD_R, r = r0 + v % FD_R;
-            if (t < nb && r < H) st_dev(&a.y[(size_t)(a0 + t) * H + r], tot);
         }
     }
-    // the last expert to finish this row tile combines it for every token, in slot order
-    wait_mem();
-    uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(&a.tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0, 64);
-    if (old != (uint32_t)pl.n_e - 1) return;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    constexpr int NV = TG * FD_R, GROUP = 64 / NV;
+    float tot = wave_sum_multi<NV>(acc, lane);
+    const int v = lane / GROUP;
+    if (lane % GROUP == 0) {
+        const int t = v / FD_R, r = r0 + v % FD_R;
+        if (t < nb && r < H) st_dev(&a.y[(size_t)(a0 + t) * H + r], tot);
+    }
+}
+
+// Combine of output row tile `tile` for every token, in slot order, by the wave that
+// took the tile's last ticket; it then resets the ticket.
+template <int ODT>
+__device__ __forceinline__ void combine_tile(const FusedArgs& a, const PlanLds& pl, int tile, int lane) {
+    const int H = (int)a.H, r0 = tile * FD_R;
     for (int idx = lane; idx < a.T * FD_R; idx += 64) {
         const int t = idx / FD_R, r = r0 + idx % FD_R;
         if (r >= H) continue;
@@ -299,22 +308,47 @@ __device__ __forceinline__ void down_compute(const FusedArgs& a, const PlanLds& 
     if (lane == 0) __hip_atomic_store(&a.tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Takes a ticket of row tile `tile` (after this wave's y stores completed); true if it
+// was the tile's last (every expert's rows of the tile are in y).
+__device__ __forceinline__ uint32_t take_ticket(const FusedArgs& a, int tile, int lane) {
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(&a.tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return old;
+}
+
+// Down item (i, tile) over all of the expert's tokens, weights already loaded.
+template <int TG>
+__device__ __forceinline__ void down_item(const FusedArgs& a, const PlanLds& pl, int i, int tile, int lane,
+                                          const DownW& d) {
+    const int a_begin = pl.off[i], a_end = pl.off[i + 1];
+    for (int a0 = a_begin; a0 < a_end; a0 += TG) {
+        const int nb = min(TG, a_end - a0);
+        float hv[TG][2][16];
+        down_h_load<TG>(a, a0, nb, lane, hv);
+        down_rows<TG>(a, pl, i, tile, lane, d, hv, a0, nb);
+    }
+}
+
 // Grid-wide barrier, one arrival per block, in two levels so no counter sees more
 // than 64 arrivals: block b arrives at group b % G (G = 8, one group per XCD under
-// round-robin dispatch); the last of a group arrives at the top counter; the last
-// of those flips every group's flag, which that group's blocks poll. A block reads
-// its flag (the sense) before it arrives; counters are reset by their last arrival,
-// so nothing needs clearing between calls.
+// round-robin dispatch); the last of a group arrives at the top counter; the last of
+// those publishes the next generation in every group's generation word, which that
+// group's blocks poll. Counters are reset by their last arrival and generations only
+// grow, so nothing needs clearing between calls. Used once per kernel.
 __device__ __forceinline__ void grid_barrier(const FusedArgs& a) {
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t G = min(gridDim.x, (uint32_t)BAR_GROUPS), g = blockIdx.x % G;
         const uint32_t n_g = (gridDim.x - g + G - 1) / G;
         uint32_t* cnt = a.bar + g * BAR_STRIDE;
-        uint32_t* flag = a.bar + (BAR_GROUPS + 1 + g) * BAR_STRIDE;
+        uint32_t* genw = a.bar + (BAR_GROUPS + 1 + g) * BAR_STRIDE;
         uint32_t* top = a.bar + BAR_GROUPS * BAR_STRIDE;
-        const uint32_t sense = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        // the generation is read before this block arrives, and waited for: memory
+        // operations to different addresses may be performed out of order, and a read
+        // after the last arrival would see the next generation and wait for one more
+        const uint32_t gen = __hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_mem();
+        const uint32_t target = gen + 1u;
         bool released = false;
         if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_g - 1) {
             __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -323,14 +357,15 @@ __device__ __forceinline__ void grid_barrier(const FusedArgs& a) {
                 __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 wait_mem();
                 for (uint32_t q = 0; q < G; q++)
-                    __hip_atomic_store(a.bar + (BAR_GROUPS + 1 + q) * BAR_STRIDE, sense ^ 1u, __ATOMIC_RELAXED,
+                    __hip_atomic_store(a.bar + (BAR_GROUPS + 1 + q) * BAR_STRIDE, target, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
+                wait_mem();
                 released = true;
             }
         }
         if (!released) {
             uint32_t spins = 0;
-            while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sense) {
+            while ((int32_t)(__hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
                 __builtin_amdgcn_s_sleep(4);
                 if (++spins > F_SPIN_LIMIT) {
                     __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -360,30 +395,65 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
     }
     __syncthreads();
     // ---- plan: slots sorted by (expert, slot); experts in id order ----
-    for (int s = tid; s < A; s += blockDim.x) {
-        const int e = pl.ids[s];
-        int pos = 0;
-        for (int s2 = 0; s2 < A; s2++) {
-            const int e2 = pl.ids[s2];
-            pos += (e2 < e) || (e2 == e && s2 < s);
+    if (A <= 64) {
+        // one wave, lane s = slot s: ranks by readlane broadcast, no LDS round trips
+        if (wave == 0) {
+            const int e = lane < A ? pl.ids[lane] : 0x7fffffff;
+            int pos = 0, below = 0, first = 1;
+            for (int j = 0; j < A; j++) {
+                const int ej = __builtin_amdgcn_readlane(e, j);
+                pos += (ej < e) || (ej == e && j < lane);
+                below += ej < e;
+                first &= !(ej == e && j < lane);
+            }
+            const uint64_t firsts = __ballot(lane < A && first);
+            if (lane < A) {
+                pl.slot_assign[lane] = pos;
+                pl.assign_tok[pos] = lane / k;
+                if (first) {
+                    // experts in id order: the rank of this first slot among first slots by id
+                    int eidx = 0;
+                    for (int j = 0; j < A; j++) {
+                        const int ej = __builtin_amdgcn_readlane(e, j);
+                        const int fj = (int)((firsts >> j) & 1ull);
+                        eidx += fj && ej < e;
+                    }
+                    pl.experts[eidx] = e;
+                    pl.off[eidx] = below;
+                }
+            }
+            if (lane == 0) {
+                const int n = (int)__builtin_popcountll(firsts);
+                pl.n_e = n;
+                pl.off[n] = A;
+            }
         }
-        pl.sorted[pos] = e;
-        pl.slot_assign[s] = pos;
-        pl.assign_tok[pos] = s / k;
-    }
-    __syncthreads();
-    for (int p = tid; p < A; p += blockDim.x) {
-        if (p == 0 || pl.sorted[p - 1] != pl.sorted[p]) {
-            int idx = 0;
-            for (int q = 1; q <= p; q++) idx += pl.sorted[q - 1] != pl.sorted[q];
-            pl.experts[idx] = pl.sorted[p];
-            pl.off[idx] = p;
+    } else {
+        for (int s = tid; s < A; s += blockDim.x) {
+            const int e = pl.ids[s];
+            int pos = 0;
+            for (int s2 = 0; s2 < A; s2++) {
+                const int e2 = pl.ids[s2];
+                pos += (e2 < e) || (e2 == e && s2 < s);
+            }
+            pl.sorted[pos] = e;
+            pl.slot_assign[s] = pos;
+            pl.assign_tok[pos] = s / k;
         }
-        if (p == A - 1) {
-            int n = 1;
-            for (int q = 1; q < A; q++) n += pl.sorted[q - 1] != pl.sorted[q];
-            pl.n_e = n;
-            pl.off[n] = A;
+        __syncthreads();
+        for (int p = tid; p < A; p += blockDim.x) {
+            if (p == 0 || pl.sorted[p - 1] != pl.sorted[p]) {
+                int idx = 0;
+                for (int q = 1; q <= p; q++) idx += pl.sorted[q - 1] != pl.sorted[q];
+                pl.experts[idx] = pl.sorted[p];
+                pl.off[idx] = p;
+            }
+            if (p == A - 1) {
+                int n = 1;
+                for (int q = 1; q < A; q++) n += pl.sorted[q - 1] != pl.sorted[q];
+                pl.n_e = n;
+                pl.off[n] = A;
+            }
         }
     }
     __syncthreads();
@@ -399,14 +469,60 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
     // ---- phase 1: gate/up + SwiGLU -> h ----
     for (int it = gwave; it < NG; it += NW) gate_up_item<TG, XDT>(a, pl, it / tiles_g, it % tiles_g, lane);
     wait_mem();  // this wave's h stores are complete before its block arrives
-    // ---- the first down item's weights stream while the grid meets ----
-    DownW d;
-    if (gwave < ND) down_load(a, pl, gwave / tiles_d, gwave % tiles_d, lane, d);
+    // ---- the first down items' weights stream while the grid meets ----
+    constexpr int PF = prefetch_items<TG>();
+    DownW d[PF];
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+        const int it = gwave + p * NW;
+        if (it < ND) down_load(a, pl, it / tiles_d, it % tiles_d, lane, d[p]);
+    }
     grid_barrier(a);
-    // ---- phase 2: down projection + slot-order combine ----
-    for (int it = gwave; it < ND; it += NW) {
-        if (it != gwave) down_load(a, pl, it / tiles_d, it % tiles_d, lane, d);
-        down_compute<TG, ODT>(a, pl, it / tiles_d, it % tiles_d, lane, d);
+    // ---- phase 2: down projection -> y, then the ticketed slot-order combine ----
+    if constexpr (TG == 1) {
+        // one token: h of both prefetched items in flight together, tickets taken together
+        float hv[PF][1][2][16];
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int it = gwave + p * NW;
+            const int i = it < ND ? it / tiles_d : 0;
+            down_h_load<1>(a, pl.off[i], it < ND ? 1 : 0, lane, hv[p]);
+        }
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int it = gwave + p * NW;
+            if (it < ND) down_rows<1>(a, pl, it / tiles_d, it % tiles_d, lane, d[p], hv[p], pl.off[it / tiles_d], 1);
+        }
+        wait_mem();
+        uint32_t old[PF];
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int it = gwave + p * NW;
+            old[p] = it < ND ? take_ticket(a, it % tiles_d, lane) : 0u;
+        }
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int it = gwave + p * NW;
+            if (it < ND && __shfl(old[p], 0, 64) == (uint32_t)n_e - 1) combine_tile<ODT>(a, pl, it % tiles_d, lane);
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < PF; p++) {
+            const int it = gwave + p * NW;
+            if (it < ND) {
+                down_item<TG>(a, pl, it / tiles_d, it % tiles_d, lane, d[p]);
+                wait_mem();
+                if (__shfl(take_ticket(a, it % tiles_d, lane), 0, 64) == (uint32_t)n_e - 1)
+                    combine_tile<ODT>(a, pl, it % tiles_d, lane);
+            }
+        }
+    }
+    for (int it = gwave + PF * NW; it < ND; it += NW) {
+        down_load(a, pl, it / tiles_d, it % tiles_d, lane, d[0]);
+        down_item<TG>(a, pl, it / tiles_d, it % tiles_d, lane, d[0]);
+        wait_mem();
+        if (__shfl(take_ticket(a, it % tiles_d, lane), 0, 64) == (uint32_t)n_e - 1)
+            combine_tile<ODT>(a, pl, it % tiles_d, lane);
     }
 }
 
@@ -500,12 +616,11 @@ int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* al
     if (xdt == OOM_BF16 && odt == OOM_F32) return launch_fused_t<TG, OOM_BF16, OOM_F32>(a, lds, st);   \
     if (xdt == OOM_F32 && odt == OOM_BF16) return launch_fused_t<TG, OOM_F32, OOM_BF16>(a, lds, st);   \
     return launch_fused_t<TG, OOM_F32, OOM_F32>(a, lds, st);
+    // one token: TG 1; more: groups of 4 tokens per pass over an item's weights
     if (T == 1) {
         FUSED_CASE(1)
-    } else if (T <= 4) {
-        FUSED_CASE(4)
     } else {
-        FUSED_CASE(8)
+        FUSED_CASE(4)
     }
 #undef FUSED_CASE
 }
