@@ -46,20 +46,63 @@ def quantize_blocks_dev(w, torch):
 
 
 def make_expert_set(E, geo, stride, seed, torch):
-    """[E, stride] uint8 records of E experts, weights N(0, 0.02) rounded to bf16."""
+    """[E, stride] uint8 records of E experts, weights N(0, 0.02) rounded to bf16, built
+    a few experts at a time on the device."""
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     buf = torch.zeros((E, stride), dtype=torch.uint8, device="cuda")
     H, I = geo.hidden, geo.inter
     parts = [(geo.gate_weight, geo.gate_scale, I, H), (geo.up_weight, geo.up_scale, I, H),
              (geo.down_weight, geo.down_scale, H, I)]
-    for e in range(E):
+    chunk = 16
+    for e0 in range(0, E, chunk):
+        ne = min(chunk, E - e0)
         for wo, so, n, k in parts:
-            w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16).float()
+            w = (torch.randn((ne * n, k), generator=g, device="cuda") * 0.02).to(torch.bfloat16).float()
             q, s = quantize_blocks_dev(w, torch)
-            buf[e, wo:wo + n * k] = q.reshape(-1)
-            buf[e, so:so + s.numel() * 4] = s.reshape(-1).view(torch.uint8)
+            buf[e0:e0 + ne, wo:wo + n * k] = q.reshape(ne, n * k)
+            buf[e0:e0 + ne, so:so + (n // 128) * (k // 128) * 4] = s.reshape(ne, -1).contiguous().view(torch.uint8)
     return buf
+
+
+def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
+    """GB/s of a plain device copy of `nbytes` (read + write counted), the STREAM-like
+    figure quoted beside the 8 TB/s peak; also the calibration kernel of the PMC runs."""
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes nbytes
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        torch.mul(src, 1.0, out=dst)
+    b.record()
+    torch.cuda.synchronize()
+    return 2 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of the step's kernel from the committed rocprofv3 PMC
+    summary (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE per dispatch, each
+    scaled by what the counter reads for a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)[config]
+        return float(t["bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def zipf_bias(E, s, seed):
+    """Per-expert router-logit bias of a Zipf(s) popularity prior: the expert of
+    popularity rank r (a seeded permutation) gets ln p_r = -s ln(r + 1) + const."""
+    import numpy as np
+
+    perm = np.random.default_rng(seed).permutation(E)
+    bias = np.empty(E, dtype=np.float32)
+    bias[perm] = -s * np.log(np.arange(1, E + 1, dtype=np.float64))
+    return bias
 
 
 def usable_cores() -> int:
@@ -80,7 +123,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline_decode(host_recs, geo, E, k, T, budget_s=10.0):
+def cpu_baseline_decode(host_recs, geo, E, k, T, zipf, budget_s=10.0):
     """The reference CPU path (oracle restatement of crates/oominf-cpu) on this host:
     router -> plan -> HostExperts -> slot-order combine per step, fresh logits each
     step, for about `budget_s` seconds. Returns (us_per_token, cores, steps)."""
@@ -95,6 +138,8 @@ def cpu_baseline_decode(host_recs, geo, E, k, T, budget_s=10.0):
     steps = 0
     while True:
         logits = rng.standard_normal((T, E)).astype(np.float32)
+        if zipf is not None:
+            logits += zipf_bias(E, zipf, 7)
         ids, w = oracle.router_topk(logits, k)
         experts, off, tok, slot = oracle.moe_plan(ids, E)
         jobs = [tok[off[i]:off[i + 1]] for i in range(len(experts))]
@@ -107,7 +152,7 @@ def cpu_baseline_decode(host_recs, geo, E, k, T, budget_s=10.0):
     return el / steps / T * 1e6, cores, steps
 
 
-def bench_decode(args, T, zipf):
+def bench_decode(args, T, zipf, config):
     import numpy as np
     import torch
 
@@ -125,10 +170,7 @@ def bench_decode(args, T, zipf):
     g.manual_seed(99)
     logits = torch.randn((n, T, E), generator=g, device="cuda")
     if zipf is not None:
-        import oracle
-
-        bias = torch.from_numpy(oracle.zipf_bias(E, zipf, 7)).cuda()
-        logits = logits + bias
+        logits = logits + torch.from_numpy(zipf_bias(E, zipf, 7)).cuda()
     logits = logits.contiguous()
     x = (torch.randn((T, H), generator=g, device="cuda")).to(torch.bfloat16)
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
@@ -175,15 +217,15 @@ def bench_decode(args, T, zipf):
                    "batch": T, "experts": E, "top_k": k, "hidden": H, "inter": I,
                    "distinct_experts_per_step": float(distinct.mean())},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
-                     "traffic": None, "kernel": "oom_moe_decode_fp8 step (all its kernels)",
-                     "algorithmic_bytes_per_step": bytes_step},
+                     "traffic": measured_traffic(config), "kernel": "moe_decode_fused_kernel (oom_moe_decode_fp8)",
+                     "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
     }
     if not args.no_cpu:
         host = sets[0].cpu().numpy()
         import oracle
 
         ogeo = oracle.record_geometry(H, I)
-        us, cores, nsteps = cpu_baseline_decode([host[e] for e in range(E)], ogeo, E, k, T, args.cpu_seconds)
+        us, cores, nsteps = cpu_baseline_decode([host[e] for e in range(E)], ogeo, E, k, T, zipf, args.cpu_seconds)
         res["cpu_baseline"] = {"value": us, "unit": "us/token", "cores": cores, "kind": "port",
                                "sample": f"{nsteps} steps of the same batch-{T} decode MoE layer (fresh logits), "
                                          f"oracle restatement of crates/oominf-cpu HostExperts on {cpu_model()}"}
@@ -195,7 +237,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16"])
+    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -206,10 +248,15 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    if args.config == "decode1":
-        res = bench_decode(args, 1, None)
+    if args.config == "copy":
+        # the PMC calibration run: copies of exactly 1 GiB, nothing else on the GPU
+        gbs = copy_bandwidth(torch, 1 << 30, args.steps)
+        res = {"metric": "device copy GB/s (read + write)", "value": gbs, "unit": "GB/s", "bytes_per_copy": 1 << 30,
+               "copies": args.steps + 1}
+    elif args.config == "decode1":
+        res = bench_decode(args, 1, None, args.config)
     else:
-        res = bench_decode(args, 16, 1.1)
+        res = bench_decode(args, 16, 1.1, args.config)
     print(json.dumps(res), flush=True)
 
 
