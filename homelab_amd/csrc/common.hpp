@@ -99,20 +99,57 @@ __device__ __forceinline__ float dpp_f32(float v) {
 }
 constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_XOR3 = 0x1B;         // quad_perm [3,2,1,0]
 constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7 - i within 8
 constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15 - i within 16
+constexpr int DPP_ROR8 = 0x128;        // row_ror:8, lane i <- i ^ 8 within 16
+
+// The value of lane ^ O for every lane of a fully active wave, without the LDS
+// crossbar: O = 1, 2 by quad permutes; 4 by a half-row mirror (i ^ 7) then a quad
+// reversal (^ 3); 8 by a row rotation; 16 and 32 by v_permlane16_swap /
+// v_permlane32_swap of the value with itself, which leaves the two rows (halves) of
+// each pair in the two results: a lane in an even row (lower half) finds its partner
+// in the second result, a lane in an odd row (upper half) in the first.
+template <int O>
+__device__ __forceinline__ float lane_xor(float v, int lane) {
+    if constexpr (O == 1) return dpp_f32<DPP_XOR1>(v);
+    else if constexpr (O == 2) return dpp_f32<DPP_XOR2>(v);
+    else if constexpr (O == 4) return dpp_f32<DPP_XOR3>(dpp_f32<DPP_HALF_MIRROR>(v));
+    else if constexpr (O == 8) return dpp_f32<DPP_ROR8>(v);
+    else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float((lane & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(O == 32, "lane_xor: O is a power of two <= 32");
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float((lane & 32) ? r[0] : r[1]);
+    }
+}
+
+// lane_xor with the offset as a value (folds to one case once loops over o unroll).
+__device__ __forceinline__ float lane_xor_n(float v, int o, int lane) {
+    switch (o) {
+        case 1: return lane_xor<1>(v, lane);
+        case 2: return lane_xor<2>(v, lane);
+        case 4: return lane_xor<4>(v, lane);
+        case 8: return lane_xor<8>(v, lane);
+        case 16: return lane_xor<16>(v, lane);
+        default: return lane_xor<32>(v, lane);
+    }
+}
 
 // Sum over each 32-lane half with the pairing of a 32-lane xor butterfly (partners
 // lane ^ 1, ^ 2, ^ 4, ^ 8, ^ 16), so the total has the butterfly's rounding. Steps
 // 3 and 4 use DPP mirrors: after the previous steps every lane of a quad (of a group
 // of 8) holds the same value, so the mirror partner's value is the xor partner's.
+// Step 5 adds the two rows of each pair (v_permlane16_swap), own + partner.
 __device__ __forceinline__ float sum32_xor_order(float v) {
     v += dpp_f32<DPP_XOR1>(v);
     v += dpp_f32<DPP_XOR2>(v);
     v += dpp_f32<DPP_HALF_MIRROR>(v);
     v += dpp_f32<DPP_MIRROR>(v);
-    v += __shfl_xor(v, 16, 64);
-    return v;
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Maximum over the wave (order-free).
@@ -121,30 +158,32 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_f32<DPP_XOR2>(v));
     v = fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
     v = fmaxf(v, dpp_f32<DPP_MIRROR>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
 // Sum over all 64 lanes; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v = sum32_xor_order(v);
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
-// Sums N per-lane values v[0..N) over the wave with N - 1 + log2(64/N) exchanges
-// instead of 6 N. Each round (lane offset o = 32, 16, ...) halves the values a lane
-// holds: a lane with bit o set keeps the upper half and sends the lower half to its
-// partner lane ^ o, which keeps the lower half. When one value is left the rest of
-// the rounds are a plain butterfly. Returns the total of value lane / (64 / N),
-// which every lane of that group of 64 / N lanes holds. N is a power of two <= 64.
-template <int N>
+// Sums N per-lane values v[0..N) over groups of 2 TOP lanes (TOP = 32: the whole wave;
+// 16: each half) with N - 1 + log2(2 TOP / N) exchanges instead of N log2(2 TOP). Each
+// round (lane offset o = TOP, TOP / 2, ...) halves the values a lane holds: a lane with
+// bit o set keeps the upper half and sends the lower half to its partner lane ^ o,
+// which keeps the lower half. When one value is left the rest of the rounds are a
+// plain butterfly. Value g's total ends in every lane of sub-group g of 2 TOP / N
+// lanes, g = (lane % (2 TOP)) / (2 TOP / N). N is a power of two <= 2 TOP.
+template <int N, int TOP = 32>
 __device__ __forceinline__ float wave_sum_multi(float (&v)[N], int lane) {
-    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
+    static_assert(N >= 1 && N <= 2 * TOP && (N & (N - 1)) == 0, "N must be a power of two <= 2 TOP");
     int count = N;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
+    for (int o = TOP; o >= 1; o >>= 1) {
         if (count > 1) {
             const int half = count / 2;
             const bool upper = (lane & o) != 0;
@@ -152,11 +191,11 @@ __device__ __forceinline__ float wave_sum_multi(float (&v)[N], int lane) {
             for (int i = 0; i < half; i++) {
                 float send = upper ? v[i] : v[i + half];
                 float keep = upper ? v[i + half] : v[i];
-                v[i] = keep + __shfl_xor(send, o, 64);
+                v[i] = keep + lane_xor_n(send, o, lane);
             }
             count = half;
         } else {
-            v[0] += __shfl_xor(v[0], o, 64);
+            v[0] += lane_xor_n(v[0], o, lane);
         }
     }
     return v[0];

@@ -5,20 +5,29 @@
 //    with the reference's arithmetic, picks by rank), so no block waits for another to
 //    route and there is no host round trip (the reference downloads the ids and waits,
 //    crates/oominf-models-qwen/src/moe.rs:308-316).
-//  * Phase 1: wave-sized gate/up items (expert, 2 intermediate rows), global wave w
-//    taking items w, w + NW, ...; each streams its gate and up rows (128-bit loads, all
-//    in flight before use) for all of the expert's tokens and writes h.
-//  * Each wave then issues the weight loads of its first down item, and the grid meets
-//    at one barrier (one arrival per block, sense-reversing, so it needs no reset): the
-//    dependency of down on h costs no HBM idle time. All blocks are resident (the grid
-//    never exceeds the occupancy limit), so the barrier always completes.
+//  * Phase 1: wave-sized gate/up items (expert, intermediate rows), global wave w taking
+//    items w, w + NW, ...; each streams its gate and up rows (128-bit loads) for all of
+//    the expert's tokens and writes h. With one token the item is one row of each, the
+//    token's activations stay in registers for the whole phase, and the loads of the
+//    wave's next item are in flight while the current one is reduced.
+//  * The weight loads of the wave's down items are issued early (with one token, right
+//    after its first gate/up item), and the grid meets at one barrier (one arrival per
+//    block): the dependency of down on h costs no HBM idle time. All blocks are
+//    resident (the grid never exceeds the occupancy limit), so the barrier completes.
 //  * Phase 2: wave-sized down items (expert, 8 output rows) write y. The last expert
 //    to finish an output row tile (a ticket per tile, in arrival order, reset by its
 //    user) combines the tile over all tokens in slot order, so results do not depend on
-//    timing. With one token, a wave takes both tickets of its two items together.
-// Counters see one arrival per block (barrier) or per (expert, tile) (tickets):
-// same-address atomics from every wave serialise at the memory side. The kernel has
-// exactly one grid barrier.
+//    timing. With one token and at most 8 experts, block b instead takes output tiles
+//    b, b + G, ... for every expert (two expert slots per wave), so a tile's expert rows
+//    meet in LDS and the slot-order combine needs no y buffer, ticket or second trip
+//    to memory.
+// Weights, scales and activations load through buffer resources: a lane or an item
+// past the end reads zeros (out-of-range offset, or an empty resource) without a
+// branch or a memory access. Counters see one arrival per block (barrier) or per
+// (expert, tile) (tickets), and each counter has a 256-byte line of its own: atomics
+// on one line serialise at the memory side. The kernel has exactly one grid barrier.
+#include <algorithm>
+
 #include "router.hpp"
 
 namespace oom {
@@ -30,12 +39,12 @@ constexpr int F_AMAX = 512;  // assignments (T * k) per step
 constexpr int F_EMAX = 256;  // experts (register router; larger E takes the multi-launch path)
 constexpr int F_HMAX = 4096; // hidden: 4 chunks of 1024 per lane row
 constexpr int F_IMAX = 2048; // inter: 2 chunks
-// down items per wave whose weights load before the barrier (one token per expert: 2)
-template <int TG>
-constexpr int prefetch_items() { return TG == 1 ? 2 : 1; }
 constexpr uint32_t F_SPIN_LIMIT = 1u << 22;
 constexpr int BAR_GROUPS = 8;   // barrier groups (one per XCD)
 constexpr int BAR_STRIDE = 64;  // u32 words between counters: one 256-byte line each
+constexpr int TICKET_STRIDE = 64;
+constexpr int BUF_FLAGS = 0x00020000;  // buffer resource word 3: 32-bit data format
+constexpr int OOB = 0x7ffffff0;        // an offset past every resource: loads read 0
 
 struct FusedArgs {
     const float* logits;
@@ -48,10 +57,11 @@ struct FusedArgs {
     void* out;
     float* h;
     float* y;
-    uint32_t* tickets;   // [ceil(H / FD_R)] down items finished per row tile
+    uint32_t* tickets;   // [ceil(H / FD_R)] down items finished per row tile, TICKET_STRIDE apart
     uint32_t* bar;       // barrier: group counters, top counter, group flags (256 B apart)
     uint32_t* status;    // 1 if a wait gave up (results invalid)
     int h_bytes;         // bytes of h (bounds of its buffer resource)
+    int rec_bytes;       // bytes of a record up to the end of its last part
 };
 
 // 16 consecutive activations of row `row` starting at column `col`, as fp32.
@@ -101,6 +111,7 @@ __device__ __forceinline__ void wait_mem() {
 }
 
 struct PlanLds {
+    uint64_t recs[F_EMAX];  // all_recs, read once per block
     int n_e;
     int experts[F_AMAX];
     int off[F_AMAX + 1];
@@ -115,7 +126,7 @@ template <int TG, int XDT>
 __device__ __forceinline__ void gate_up_item(const FusedArgs& a, const PlanLds& pl, int i, int tile, int lane) {
     const int H = (int)a.H, I = (int)a.I;
     const int CH = (H + 1023) >> 10, nkb = (H + 127) >> 7;
-    const uint8_t* rec = reinterpret_cast<const uint8_t*>(a.all_recs[pl.experts[i]]);
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(pl.recs[pl.experts[i]]);
     const int j0 = tile * FG_R;
     uint4 wg[FG_R][4], wu[FG_R][4];
 #pragma unroll
@@ -211,7 +222,7 @@ struct DownW {
 
 __device__ __forceinline__ void down_load(const FusedArgs& a, const PlanLds& pl, int i, int tile, int lane, DownW& d) {
     const int H = (int)a.H, I = (int)a.I, CH = (I + 1023) >> 10;
-    const uint8_t* rec = reinterpret_cast<const uint8_t*>(a.all_recs[pl.experts[i]]);
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(pl.recs[pl.experts[i]]);
     const int r0 = tile * FD_R;
 #pragma unroll
     for (int r = 0; r < FD_R; r++) {
@@ -259,7 +270,7 @@ __device__ __forceinline__ void down_rows(const FusedArgs& a, const PlanLds& pl,
                                           const DownW& d, const float (&hv)[TG][2][16], int a0, int nb) {
     const int H = (int)a.H, I = (int)a.I;
     const int CH = (I + 1023) >> 10, nkb = (I + 127) >> 7;
-    const uint8_t* rec = reinterpret_cast<const uint8_t*>(a.all_recs[pl.experts[i]]);
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(pl.recs[pl.experts[i]]);
     const int r0 = tile * FD_R;
     const float* ds = reinterpret_cast<const float*>(rec + a.ds) + (size_t)(r0 >> 7) * nkb;
     float acc[TG * FD_R];
@@ -305,14 +316,15 @@ __device__ __forceinline__ void combine_tile(const FusedArgs& a, const PlanLds& 
             acc = fmaf(pl.w[t * a.k + s], ld_dev(&a.y[(size_t)pl.slot_assign[t * a.k + s] * H + r]), acc);
         store_out<ODT>(a.out, (size_t)t * H + r, acc);
     }
-    if (lane == 0) __hip_atomic_store(&a.tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(&a.tickets[tile * TICKET_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Takes a ticket of row tile `tile` (after this wave's y stores completed); true if it
 // was the tile's last (every expert's rows of the tile are in y).
 __device__ __forceinline__ uint32_t take_ticket(const FusedArgs& a, int tile, int lane) {
     uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(&a.tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0)
+        old = __hip_atomic_fetch_add(&a.tickets[tile * TICKET_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return old;
 }
 
@@ -327,6 +339,201 @@ __device__ __forceinline__ void down_item(const FusedArgs& a, const PlanLds& pl,
         down_h_load<TG>(a, a0, nb, lane, hv);
         down_rows<TG>(a, pl, i, tile, lane, d, hv, a0, nb);
     }
+}
+
+// ---- one token (T == 1) ------------------------------------------------------------------
+
+// A record's parts through one buffer resource; an empty resource (bytes 0) reads zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rec_rsrc(const PlanLds& pl, int i, int bytes) {
+    const uint64_t r = pl.recs[pl.experts[i]];
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)r), hi = __builtin_amdgcn_readfirstlane((uint32_t)(r >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, bytes,
+                                             BUF_FLAGS);
+}
+
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float ldf(__amdgpu_buffer_rsrc_t r, int off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// The token's activations: lane l holds columns 1024 c + 16 l .. + 16 (c < 4), zeros
+// past hidden.
+template <int XDT>
+struct XRow;
+template <>
+struct XRow<OOM_BF16> {
+    uint32_t w[4][8];
+};
+template <>
+struct XRow<OOM_F32> {
+    float v[4][16];
+};
+
+template <int XDT>
+__device__ __forceinline__ void xrow_load(const void* x, int H, int lane, XRow<XDT>& xr) {
+    constexpr int ES = XDT == OOM_BF16 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, H * ES, BUF_FLAGS);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int col = c * 1024 + lane * 16;
+        const int off = col < H ? col * ES : OOB;
+        if constexpr (XDT == OOM_BF16) {
+            const uint4 a0 = ld16(r, off), a1 = ld16(r, off + 16);
+            xr.w[c][0] = a0.x; xr.w[c][1] = a0.y; xr.w[c][2] = a0.z; xr.w[c][3] = a0.w;
+            xr.w[c][4] = a1.x; xr.w[c][5] = a1.y; xr.w[c][6] = a1.z; xr.w[c][7] = a1.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 v = ld16(r, off + 16 * q);
+                xr.v[c][4 * q] = __uint_as_float(v.x);
+                xr.v[c][4 * q + 1] = __uint_as_float(v.y);
+                xr.v[c][4 * q + 2] = __uint_as_float(v.z);
+                xr.v[c][4 * q + 3] = __uint_as_float(v.w);
+            }
+        }
+    }
+}
+
+// Gate/up item `it` (expert it / I, row it % I): one gate row and one up row, 1024
+// columns per chunk, and their 128 x 128-block scales; an item past NG reads zeros.
+struct Gate1 {
+    uint4 g[4], u[4];
+    float sg[4], su[4];
+};
+
+__device__ __forceinline__ void gate1_load(const FusedArgs& a, const PlanLds& pl, int it, int NG, int lane, Gate1& w) {
+    const int H = (int)a.H, I = (int)a.I, nkb = (H + 127) >> 7;
+    const bool valid = it < NG;
+    const int i = valid ? it / I : 0, j = valid ? it % I : 0;
+    const __amdgpu_buffer_rsrc_t r = rec_rsrc(pl, i, valid ? a.rec_bytes : 0);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int col = c * 1024 + lane * 16;
+        const bool ok = col < H;
+        const int row = j * H + col, sc = ((j >> 7) * nkb + (col >> 7)) * 4;
+        w.g[c] = ld16(r, ok ? (int)a.gw + row : OOB);
+        w.u[c] = ld16(r, ok ? (int)a.uw + row : OOB);
+        w.sg[c] = ldf(r, ok ? (int)a.gs + sc : OOB);
+        w.su[c] = ldf(r, ok ? (int)a.us + sc : OOB);
+    }
+}
+
+// h[a(it), j(it)] = silu(x . gate row) * (x . up row).
+template <int XDT>
+__device__ __forceinline__ void gate1_compute(const FusedArgs& a, const PlanLds& pl, int it, int NG, const Gate1& w,
+                                              const XRow<XDT>& xr, int lane) {
+    float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        if constexpr (XDT == OOM_BF16) {
+            acc[0] = fmaf(dot16_e4m3_bf16(w.g[c], xr.w[c]), w.sg[c], acc[0]);
+            acc[1] = fmaf(dot16_e4m3_bf16(w.u[c], xr.w[c]), w.su[c], acc[1]);
+        } else {
+            float fg[16], fu[16];
+            e4m3x16(w.g[c], fg);
+            e4m3x16(w.u[c], fu);
+            float pg = 0.0f, pu = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                pg = fmaf(fg[q], xr.v[c][q], pg);
+                pu = fmaf(fu[q], xr.v[c][q], pu);
+            }
+            acc[0] = fmaf(pg, w.sg[c], acc[0]);
+            acc[1] = fmaf(pu, w.su[c], acc[1]);
+        }
+    }
+    // gate total in lanes 0..31, up total in lanes 32..63
+    const float tot = wave_sum_multi<2>(acc, lane);
+    const float up = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 32));
+    if (lane == 0 && it < NG) {
+        const int I = (int)a.I, i = it / I, j = it % I;
+        st_dev(&a.h[(size_t)pl.off[i] * I + j], siluf(tot) * up);
+    }
+}
+
+// Down item (expert i, output rows 8 t .. 8 t + 8) for one token: lanes 0..31 take rows
+// 8 t + 2 p, lanes 32..63 rows 8 t + 2 p + 1 (p < 4), each lane 16 columns of each
+// 512-column chunk c < DCH; one scale per chunk (the 8 rows share a 128-row block).
+template <int DCH>
+struct Down1 {
+    uint4 w[4][DCH];
+    float s[DCH];
+};
+
+template <int DCH>
+__device__ __forceinline__ void down1_load(const FusedArgs& a, const PlanLds& pl, int i, int tile, bool valid, int lane,
+                                           Down1<DCH>& d) {
+    const int H = (int)a.H, I = (int)a.I, nkb = (I + 127) >> 7;
+    const int r0 = valid ? tile * FD_R : 0;
+    const __amdgpu_buffer_rsrc_t r = rec_rsrc(pl, valid ? i : 0, valid ? a.rec_bytes : 0);
+    const int half = lane >> 5, l = lane & 31;
+#pragma unroll
+    for (int c = 0; c < DCH; c++) {
+        const int col = c * 512 + l * 16;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int row = r0 + 2 * p + half;
+            d.w[p][c] = ld16(r, row < H && col < I ? (int)a.dw + row * I + col : OOB);
+        }
+        d.s[c] = ldf(r, col < I ? (int)a.ds + ((r0 >> 7) * nkb + (col >> 7)) * 4 : OOB);
+    }
+}
+
+// h of assignment `as` at this lane's 16 columns of each chunk (zeros past inter, or
+// everywhere if !valid), through device-coherent loads. The two halves of the wave
+// need the same columns: each loads 8 of the 16 and v_permlane32_swap trades them
+// (the first result holds the lower half's values in every lane, the second the
+// upper half's).
+template <int DCH>
+__device__ __forceinline__ void down1_h(const FusedArgs& a, int as, bool valid, int lane, float (&hv)[DCH][16]) {
+    const int I = (int)a.I, l = lane & 31, half = lane >> 5;
+    const __amdgpu_buffer_rsrc_t hr =
+        __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, valid ? a.h_bytes : 0, BUF_FLAGS);
+#pragma unroll
+    for (int c = 0; c < DCH; c++) {
+        const int col = c * 512 + l * 16;
+        const int off = col < I ? (as * I + col) * 4 + half * 32 : OOB;
+        uint32_t mine[8];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16 * q, 0, BUF_SC1);
+            mine[4 * q] = v[0];
+            mine[4 * q + 1] = v[1];
+            mine[4 * q + 2] = v[2];
+            mine[4 * q + 3] = v[3];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const auto r = __builtin_amdgcn_permlane32_swap(mine[j], mine[j], false, false);
+            hv[c][j] = __uint_as_float(r[0]);
+            hv[c][j + 8] = __uint_as_float(r[1]);
+        }
+    }
+}
+
+// The item's 8 row totals: row pair p's total ends in lanes 8 p .. 8 p + 7 of each half
+// (lanes 0..31: row 2 p, lanes 32..63: row 2 p + 1 of the tile).
+template <int DCH>
+__device__ __forceinline__ float down1_rows(const Down1<DCH>& d, const float (&hv)[DCH][16], int lane) {
+    float acc[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DCH; c++) {
+            float f[16];
+            e4m3x16(d.w[p][c], f);
+            float q0 = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) q0 = fmaf(f[q], hv[c][q], q0);
+            s = fmaf(q0, d.s[c], s);
+        }
+        acc[p] = s;
+    }
+    return wave_sum_multi<4, 16>(acc, lane);
 }
 
 // Grid-wide barrier, one arrival per block, in two levels so no counter sees more
@@ -378,11 +585,16 @@ __device__ __forceinline__ void grid_barrier(const FusedArgs& a) {
     __syncthreads();
 }
 
-template <int TG, int XDT, int ODT>
+template <int TG, int DCH, int XDT, int ODT>
 __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
     __shared__ PlanLds pl;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int T = a.T, E = a.E, k = a.k, A = T * k;
+    // the record table and (one token) the activations load while the router runs
+    if (tid < E) pl.recs[tid] = a.all_recs[tid];
+    XRow<XDT> xr;
+    if constexpr (TG == 1) xrow_load<XDT>(a.x, (int)a.H, lane, xr);
     // ---- routing (every block) ----
     for (int t = wave; t < T; t += FW) {
         int id = 0;
@@ -463,66 +675,75 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
             a.weights[s] = pl.w[s];
         }
     const int n_e = pl.n_e;
-    const int tiles_g = (int)((a.I + FG_R - 1) / FG_R), tiles_d = (int)((a.H + FD_R - 1) / FD_R);
-    const int NG = n_e * tiles_g, ND = n_e * tiles_d;
     const int NW = gridDim.x * FW, gwave = blockIdx.x * FW + wave;
-    // ---- phase 1: gate/up + SwiGLU -> h ----
-    for (int it = gwave; it < NG; it += NW) gate_up_item<TG, XDT>(a, pl, it / tiles_g, it % tiles_g, lane);
-    wait_mem();  // this wave's h stores are complete before its block arrives
-    // ---- the first down items' weights stream while the grid meets ----
-    constexpr int PF = prefetch_items<TG>();
-    DownW d[PF];
-#pragma unroll
-    for (int p = 0; p < PF; p++) {
-        const int it = gwave + p * NW;
-        if (it < ND) down_load(a, pl, it / tiles_d, it % tiles_d, lane, d[p]);
-    }
-    grid_barrier(a);
-    // ---- phase 2: down projection -> y, then the ticketed slot-order combine ----
+    const int tiles_d = (int)((a.H + FD_R - 1) / FD_R), ND = n_e * tiles_d;
     if constexpr (TG == 1) {
-        // one token: h of both prefetched items in flight together, tickets taken together
-        float hv[PF][1][2][16];
-#pragma unroll
-        for (int p = 0; p < PF; p++) {
-            const int it = gwave + p * NW;
-            const int i = it < ND ? it / tiles_d : 0;
-            down_h_load<1>(a, pl.off[i], it < ND ? 1 : 0, lane, hv[p]);
+        // ---- phase 1, one token: item it = (expert it / I, row it % I); the next item's
+        // loads are in flight while the current one is reduced ----
+        const int NG = n_e * (int)a.I;
+        Gate1 w0, w1;
+        gate1_load(a, pl, gwave, NG, lane, w0);
+        // this block's first output tile for two expert slots streams behind the wave's
+        // first gate/up item: block b takes tiles b, b + G, ... for all (<= 8) experts,
+        // wave w the experts w and w + FW
+        const int s0 = wave, s1 = wave + FW, tb0 = blockIdx.x;
+        Down1<DCH> d0, d1;
+        down1_load<DCH>(a, pl, s0, tb0, s0 < n_e && tb0 < tiles_d, lane, d0);
+        down1_load<DCH>(a, pl, s1, tb0, s1 < n_e && tb0 < tiles_d, lane, d1);
+        for (int it = gwave; it < NG; it += 2 * NW) {
+            gate1_load(a, pl, it + NW, NG, lane, w1);
+            gate1_compute<XDT>(a, pl, it, NG, w0, xr, lane);
+            if (it + NW >= NG) break;
+            gate1_load(a, pl, it + 2 * NW, NG, lane, w0);
+            gate1_compute<XDT>(a, pl, it + NW, NG, w1, xr, lane);
         }
-#pragma unroll
-        for (int p = 0; p < PF; p++) {
-            const int it = gwave + p * NW;
-            if (it < ND) down_rows<1>(a, pl, it / tiles_d, it % tiles_d, lane, d[p], hv[p], pl.off[it / tiles_d], 1);
-        }
-        wait_mem();
-        uint32_t old[PF];
-#pragma unroll
-        for (int p = 0; p < PF; p++) {
-            const int it = gwave + p * NW;
-            old[p] = it < ND ? take_ticket(a, it % tiles_d, lane) : 0u;
-        }
-#pragma unroll
-        for (int p = 0; p < PF; p++) {
-            const int it = gwave + p * NW;
-            if (it < ND && __shfl(old[p], 0, 64) == (uint32_t)n_e - 1) combine_tile<ODT>(a, pl, it % tiles_d, lane);
+        wait_mem();  // this wave's h stores (and loads) are complete before its block arrives
+        grid_barrier(a);
+        // ---- phase 2, one token: the slots' h once, then per tile the 8 rows of each
+        // expert into LDS and the slot-order combine by wave 0 ----
+        __shared__ float ylds[2 * FW][FD_R];
+        float h0[DCH][16], h1[DCH][16];
+        down1_h<DCH>(a, pl.off[s0 < n_e ? s0 : 0], s0 < n_e, lane, h0);
+        down1_h<DCH>(a, pl.off[s1 < n_e ? s1 : 0], s1 < n_e, lane, h1);
+        const int prow = 2 * ((lane & 31) >> 3) + (lane >> 5);  // this lane group's row in the tile
+        for (int tb = tb0; tb < tiles_d; tb += gridDim.x) {
+            if (tb != tb0) {
+                down1_load<DCH>(a, pl, s0, tb, s0 < n_e, lane, d0);
+                down1_load<DCH>(a, pl, s1, tb, s1 < n_e, lane, d1);
+            }
+            const float y0 = down1_rows<DCH>(d0, h0, lane), y1 = down1_rows<DCH>(d1, h1, lane);
+            if ((lane & 7) == 0) {
+                ylds[s0][prow] = y0;
+                ylds[s1][prow] = y1;
+            }
+            __syncthreads();
+            // out[r] = sum over slots in order of w[s] * y[slot_assign[s]][r]; with one
+            // token, assignment i is expert slot i
+            const int r = tb * FD_R + lane;
+            if (wave == 0 && lane < FD_R && r < (int)a.H) {
+                float acc = 0.0f;
+                for (int s = 0; s < k; s++) acc = fmaf(pl.w[s], ylds[pl.slot_assign[s]][lane], acc);
+                store_out<ODT>(a.out, r, acc);
+            }
+            __syncthreads();
         }
     } else {
-#pragma unroll
-        for (int p = 0; p < PF; p++) {
-            const int it = gwave + p * NW;
-            if (it < ND) {
-                down_item<TG>(a, pl, it / tiles_d, it % tiles_d, lane, d[p]);
-                wait_mem();
-                if (__shfl(take_ticket(a, it % tiles_d, lane), 0, 64) == (uint32_t)n_e - 1)
-                    combine_tile<ODT>(a, pl, it % tiles_d, lane);
-            }
+        // ---- phase 1: gate/up + SwiGLU -> h, FG_R rows per item, tokens in groups of TG ----
+        const int tiles_g = (int)((a.I + FG_R - 1) / FG_R), NG = n_e * tiles_g;
+        for (int it = gwave; it < NG; it += NW) gate_up_item<TG, XDT>(a, pl, it / tiles_g, it % tiles_g, lane);
+        wait_mem();  // this wave's h stores are complete before its block arrives
+        // ---- the first down item's weights stream while the grid meets ----
+        DownW d;
+        if (gwave < ND) down_load(a, pl, gwave / tiles_d, gwave % tiles_d, lane, d);
+        grid_barrier(a);
+        // ---- phase 2: down projection -> y, then the ticketed slot-order combine ----
+        for (int it = gwave; it < ND; it += NW) {
+            if (it != gwave) down_load(a, pl, it / tiles_d, it % tiles_d, lane, d);
+            down_item<TG>(a, pl, it / tiles_d, it % tiles_d, lane, d);
+            wait_mem();
+            if ((uint32_t)__builtin_amdgcn_readlane((int)take_ticket(a, it % tiles_d, lane), 0) == (uint32_t)n_e - 1)
+                combine_tile<ODT>(a, pl, it % tiles_d, lane);
         }
-    }
-    for (int it = gwave + PF * NW; it < ND; it += NW) {
-        down_load(a, pl, it / tiles_d, it % tiles_d, lane, d[0]);
-        down_item<TG>(a, pl, it / tiles_d, it % tiles_d, lane, d[0]);
-        wait_mem();
-        if (__shfl(take_ticket(a, it % tiles_d, lane), 0, 64) == (uint32_t)n_e - 1)
-            combine_tile<ODT>(a, pl, it % tiles_d, lane);
     }
 }
 
@@ -540,45 +761,53 @@ static FusedWs fused_ws(int T, int E, int k, const OomFp8Record& g) {
     w.h = 0;
     w.y = al256(A * (size_t)g.inter * sizeof(float));
     w.tickets = w.y + al256(A * (size_t)g.hidden * sizeof(float));
-    w.bar = w.tickets + al256((size_t)cdiv(g.hidden, FD_R) * sizeof(uint32_t));
+    w.bar = w.tickets + (size_t)cdiv(g.hidden, FD_R) * TICKET_STRIDE * sizeof(uint32_t);
     w.status = w.bar + (2 * BAR_GROUPS + 1) * BAR_STRIDE * sizeof(uint32_t);
     w.total = w.status + 256;
     return w;
 }
 
+// Bytes of a record up to the end of its last part (the span its buffer resource covers).
+static int64_t record_span(const OomFp8Record& g) {
+    const int64_t nbg = cdiv(g.inter, 128) * cdiv(g.hidden, 128) * 4;
+    return std::max({g.gate_weight + g.inter * g.hidden, g.gate_scale + nbg, g.up_weight + g.inter * g.hidden,
+                     g.up_scale + nbg, g.down_weight + g.hidden * g.inter, g.down_scale + nbg});
+}
+
 bool fused_supported(int T, int E, int k, const OomFp8Record& g) {
-    return (int64_t)T * k <= F_AMAX && E <= F_EMAX && g.hidden <= F_HMAX && g.inter <= F_IMAX && T <= 64;
+    return (int64_t)T * k <= F_AMAX && E <= F_EMAX && g.hidden <= F_HMAX && g.inter <= F_IMAX && T <= 64 &&
+           record_span(g) < OOB;
 }
 
 size_t fused_workspace_size(int T, int E, int k, const OomFp8Record& g) { return fused_ws(T, E, k, g).total; }
 
 // Blocks of the fused kernel that fit on the device at once (all must be resident).
-template <int TG, int XDT, int ODT>
+template <int TG, int DCH, int XDT, int ODT>
 static int resident_blocks(int dev, size_t lds) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, XDT, ODT>, 256, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, DCH, XDT, ODT>, 256, lds) !=
         hipSuccess)
         return 0;
     return cus * per;
 }
 
-template <int TG, int XDT, int ODT>
+template <int TG, int DCH, int XDT, int ODT>
 static int launch_fused_t(const FusedArgs& a, size_t lds, hipStream_t st) {
     static thread_local int cached_dev = -1, cached_blocks = 0;
     static thread_local size_t cached_lds = 0;
     int dev = 0;
     (void)hipGetDevice(&dev);
     if (dev != cached_dev || lds != cached_lds) {
-        cached_blocks = resident_blocks<TG, XDT, ODT>(dev, lds);
+        cached_blocks = resident_blocks<TG, DCH, XDT, ODT>(dev, lds);
         cached_dev = dev;
         cached_lds = lds;
     }
     if (cached_blocks <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
     // never more waves than items (at most min(E, A) experts' worth)
-    const int64_t items = (int64_t)std::min(a.E, a.T * a.k) * (cdiv(a.I, FG_R) + cdiv(a.H, FD_R));
+    const int64_t items = (int64_t)std::min(a.E, a.T * a.k) * (cdiv(a.I, TG == 1 ? 1 : FG_R) + cdiv(a.H, FD_R));
     const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, cdiv(items, FW)));
-    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, XDT, ODT>), dim3(blocks), dim3(256), lds, st, a);
+    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, DCH, XDT, ODT>), dim3(blocks), dim3(256), lds, st, a);
     return launched("oom_moe_decode_fp8");
 }
 
@@ -610,17 +839,25 @@ int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* al
     a.bar = reinterpret_cast<uint32_t*>(base + w.bar);
     a.status = reinterpret_cast<uint32_t*>(base + w.status);
     a.h_bytes = (int)((size_t)T * k * g.inter * sizeof(float));
+    a.rec_bytes = (int)record_span(g);
     const size_t lds = 0;
-#define FUSED_CASE(TG)                                                                          \
-    if (xdt == OOM_BF16 && odt == OOM_BF16) return launch_fused_t<TG, OOM_BF16, OOM_BF16>(a, lds, st); \
-    if (xdt == OOM_BF16 && odt == OOM_F32) return launch_fused_t<TG, OOM_BF16, OOM_F32>(a, lds, st);   \
-    if (xdt == OOM_F32 && odt == OOM_BF16) return launch_fused_t<TG, OOM_F32, OOM_BF16>(a, lds, st);   \
-    return launch_fused_t<TG, OOM_F32, OOM_F32>(a, lds, st);
-    // one token: TG 1; more: groups of 4 tokens per pass over an item's weights
-    if (T == 1) {
-        FUSED_CASE(1)
+#define FUSED_CASE(TG, DCH)                                                                               \
+    if (xdt == OOM_BF16 && odt == OOM_BF16) return launch_fused_t<TG, DCH, OOM_BF16, OOM_BF16>(a, lds, st); \
+    if (xdt == OOM_BF16 && odt == OOM_F32) return launch_fused_t<TG, DCH, OOM_BF16, OOM_F32>(a, lds, st);   \
+    if (xdt == OOM_F32 && odt == OOM_BF16) return launch_fused_t<TG, DCH, OOM_F32, OOM_BF16>(a, lds, st);   \
+    return launch_fused_t<TG, DCH, OOM_F32, OOM_F32>(a, lds, st);
+    // one token routed to at most 2 FW experts: TG 1 with 512-column down chunks for the
+    // inter width; otherwise groups of 4 tokens per pass over an item's weights
+    if (T == 1 && k <= 2 * FW) {
+        if (g.inter <= 1024) {
+            FUSED_CASE(1, 2)
+        } else if (g.inter <= 1536) {
+            FUSED_CASE(1, 3)
+        } else {
+            FUSED_CASE(1, 4)
+        }
     } else {
-        FUSED_CASE(4)
+        FUSED_CASE(4, 0)
     }
 #undef FUSED_CASE
 }
