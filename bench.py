@@ -232,12 +232,94 @@ def bench_decode(args, T, zipf, config):
     return res
 
 
+def cpu_baseline_attn(q, k, v, table, kv_len, H, Hkv, D, scale, budget_s):
+    """The oracle's restatement of the reference attention (one thread) on this host
+    for about `budget_s` seconds. Returns (us_per_step, steps)."""
+    import oracle
+
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        oracle.attn_decode_paged(q, k, v, table, 16, kv_len, H, Hkv, D, scale)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and steps >= 2:
+            break
+    return el / steps * 1e6, steps
+
+
+def bench_attn(args):
+    """Paged GQA decode attention, batch 1: 64 query heads, 8 KV heads, head_dim 128,
+    32768 keys of bf16 K/V in 16-token pages in a seeded random page order, N(0, 1)
+    q/K/V, all keys visible, bf16 out."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    H, Hkv, D, L, P = 64, 8, 128, 32768, 16
+    n_pages = L // P
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    # two caches alternate between steps so K/V stream from HBM, not from the MALL
+    caches = []
+    for _ in range(2):
+        k = torch.randn((n_pages, P, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((n_pages, P, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        table = torch.randperm(n_pages, generator=g, device="cuda").to(torch.int32)
+        caches.append((k, v, table))
+    q = torch.randn((H, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((H, D), dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(hip.attn_decode_workspace_size(L, H, Hkv, D), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / D ** 0.5
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        k, v, table = caches[i % 2]
+        hip.attn_decode_paged(q, k, v, table, L, scale, out, ws, stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(args.steps):
+        step(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    bytes_step = 2 * L * Hkv * D * 2 + L // P * 4 + 2 * H * D * 2
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    res = {
+        "metric": "GQA paged decode attention us/step + achieved HBM GB/s (% of MI355X peak), 1 GPU",
+        "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 K/V/q, fp32 softmax and accumulate, bf16 out", "data": "synthetic",
+        "config": {"workload": "GQA decode attention, batch 1: 64 q heads, 8 KV heads, head_dim 128, 32768 keys, "
+                               "bf16 KV in 16-token pages in random page order; 2 caches alternate past the MALL",
+                   "heads": H, "kv_heads": Hkv, "head_dim": D, "kv_len": L, "page_size": P},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": measured_traffic("attn"), "kernel": "attn_decode_kernel (oom_attn_decode_paged)",
+                     "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
+    }
+    if not args.no_cpu:
+        kk, vv, tt = caches[0]
+        k16 = kk.view(torch.int16).cpu().numpy().view(np.uint16)
+        v16 = vv.view(torch.int16).cpu().numpy().view(np.uint16)
+        q16 = q.view(torch.int16).cpu().numpy().view(np.uint16)
+        us, n = cpu_baseline_attn(q16, k16, v16, tt.cpu().numpy(), L, H, Hkv, D, scale, args.cpu_seconds)
+        res["cpu_baseline"] = {"value": us, "unit": "us/step", "cores": 1, "kind": "port",
+                               "sample": f"{n} calls of the same attention step, oracle restatement of the reference's "
+                                         f"fp32 attention (one thread) on {cpu_model()}"}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "copy"])
+    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "attn", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -253,6 +335,8 @@ def main():
         gbs = copy_bandwidth(torch, 1 << 30, args.steps)
         res = {"metric": "device copy GB/s (read + write)", "value": gbs, "unit": "GB/s", "bytes_per_copy": 1 << 30,
                "copies": args.steps + 1}
+    elif args.config == "attn":
+        res = bench_attn(args)
     elif args.config == "decode1":
         res = bench_decode(args, 1, None, args.config)
     else:

@@ -46,6 +46,8 @@ SIGNATURES = {
     "oom_moe_plan": (I32, [P, I32, I32, I32, P, P, P, P]),
     "oom_moe_decode_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
     "oom_moe_decode_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
+    "oom_attn_decode_workspace_size": (SZ, [I32, I32, I32, I32]),
+    "oom_attn_decode_paged": (I32, [P, I32, P, P, P, I32, I32, I32, I32, I32, I32, F, P, I32, P, SZ, P]),
 }
 
 
@@ -175,3 +177,16 @@ def moe_decode_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, ou
     check(lib().oom_moe_decode_fp8(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k, ctypes.byref(geo),
                                    _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
                                    ws.numel() * ws.element_size(), _stream(stream)))
+
+
+def attn_decode_workspace_size(kv_len: int, heads: int, kv_heads: int, d: int) -> int:
+    return int(lib().oom_attn_decode_workspace_size(kv_len, heads, kv_heads, d))
+
+
+def attn_decode_paged(q, k_pages, v_pages, page_table, kv_len: int, scale: float, out, ws, stream=None) -> None:
+    """q [heads, d]; k_pages / v_pages bf16 [n_pages, page_size, kv_heads, d]; page_table i32."""
+    heads, d = q.shape
+    n_pages, page_size, kv_heads, _ = k_pages.shape
+    check(lib().oom_attn_decode_paged(_ptr(q), _dtype_code(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
+                                      n_pages, page_size, kv_len, heads, kv_heads, d, scale, _ptr(out),
+                                      _dtype_code(out), _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))

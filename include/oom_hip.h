@@ -132,6 +132,23 @@ int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const ui
                        int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
                        void* ws, size_t ws_bytes, void* stream);
 
+/* Paged GQA decode attention for one query token: out[h, :] = sum_j softmax_j(q_h . k_j
+ * * scale) v_j over the kv_len keys, query head h reading KV head h / (heads / kv_heads).
+ * q [heads, d] in q_dtype; k_pages and v_pages bf16 [n_pages, page_size, kv_heads, d]
+ * (16-byte aligned); key j lives in physical page page_table[j / page_size] (i32, one
+ * entry per page of the sequence; an entry outside [0, n_pages) reads zeros) at slot
+ * j % page_size. d = 128, heads / kv_heads <= 8, page_size a multiple of 16. fp32 dot
+ * products, exp and accumulation (fp32 q enters the bf16 matrix cores as an exact
+ * three-term split); out [heads, d] in out_dtype. Every key up to kv_len is visible
+ * (the decode position is the last one).
+ * Replaces Attention::attention at decode (crates/oominf-core/src/backend.rs:545-568;
+ * crates/oominf-cuda/src/attention.rs:265-346, which routes D=128, G=8 to attn_prefill,
+ * crates/oominf-cuda/kernels/attention.cu:419-553), over a paged bf16 cache. */
+size_t oom_attn_decode_workspace_size(int kv_len, int heads, int kv_heads, int d);
+int oom_attn_decode_paged(const void* q, int q_dtype, const uint16_t* k_pages, const uint16_t* v_pages,
+                          const int32_t* page_table, int n_pages, int page_size, int kv_len, int heads, int kv_heads,
+                          int d, float scale, void* out, int out_dtype, void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,14 @@ def test_argument_errors_without_a_device():
     assert rc == -1 and b"multiples of 16" in lib.oom_last_error()
     rc = lib.oom_moe_decode_fp8(null, null, 0, null, 1, 128, 8, ctypes.byref(geo), null, null, null, 0, null, 0, null)
     assert rc == -1 and b"null buffer" in lib.oom_last_error()
+    rc = lib.oom_attn_decode_paged(null, 1, null, null, null, 1, 16, 10, 64, 8, 64, 0.1, null, 1, null, 0, null)
+    assert rc == -1 and b"head_dim" in lib.oom_last_error()
+    rc = lib.oom_attn_decode_paged(null, 1, null, null, null, 1, 16, 10, 64, 4, 128, 0.1, null, 1, null, 0, null)
+    assert rc == -1 and b"at most 8" in lib.oom_last_error()
+    rc = lib.oom_attn_decode_paged(null, 1, null, null, null, 1, 8, 10, 64, 8, 128, 0.1, null, 1, null, 0, null)
+    assert rc == -1 and b"multiple of 16" in lib.oom_last_error()
+    rc = lib.oom_attn_decode_paged(null, 1, null, null, null, 1, 16, 10, 64, 8, 128, 0.1, null, 1, null, 0, null)
+    assert rc == -1 and b"null buffer" in lib.oom_last_error()
 
 
 def test_workspace_sizes():
