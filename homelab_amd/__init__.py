@@ -46,6 +46,10 @@ SIGNATURES = {
     "oom_moe_plan": (I32, [P, I32, I32, I32, P, P, P, P]),
     "oom_moe_decode_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
     "oom_moe_decode_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
+    "oom_quantize_rows_fp8": (I32, [P, I32, I64, I64, P, P, P]),
+    "oom_moe_grouped_gemm_fp8": (I32, [P, P, P, I32, I32, P, P, I32, P, I64, I64, I64, I64, P]),
+    "oom_moe_prefill_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
+    "oom_moe_prefill_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
     "oom_attn_decode_workspace_size": (SZ, [I32, I32, I32, I32]),
     "oom_attn_decode_paged": (I32, [P, I32, P, P, P, I32, I32, I32, I32, I32, I32, F, P, I32, P, SZ, P]),
 }
@@ -190,3 +194,25 @@ def attn_decode_paged(q, k_pages, v_pages, page_table, kv_len: int, scale: float
     check(lib().oom_attn_decode_paged(_ptr(q), _dtype_code(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
                                       n_pages, page_size, kv_len, heads, kv_heads, d, scale, _ptr(out),
                                       _dtype_code(out), _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
+
+
+def quantize_rows_fp8(x, q, scale, stream=None) -> None:
+    rows, cols = x.shape
+    check(lib().oom_quantize_rows_fp8(_ptr(x), _dtype_code(x), rows, cols, _ptr(q), _ptr(scale), _stream(stream)))
+
+
+def moe_grouped_gemm_fp8(recs, off, rows, n_experts: int, max_per_expert: int, xq, x_scale, x_group: int, y,
+                         N: int, K: int, w_off: int, s_off: int, stream=None) -> None:
+    check(lib().oom_moe_grouped_gemm_fp8(_ptr(recs), _ptr(off), _ptr(rows), n_experts, max_per_expert, _ptr(xq),
+                                         _ptr(x_scale), x_group, _ptr(y), N, K, w_off, s_off, _stream(stream)))
+
+
+def moe_prefill_fp8_workspace_size(T: int, E: int, k: int, geo: Fp8Record) -> int:
+    return int(lib().oom_moe_prefill_fp8_workspace_size(T, E, k, ctypes.byref(geo)))
+
+
+def moe_prefill_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, out, ws, stream=None) -> None:
+    T, E = logits.shape
+    check(lib().oom_moe_prefill_fp8(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k, ctypes.byref(geo),
+                                    _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
+                                    ws.numel() * ws.element_size(), _stream(stream)))

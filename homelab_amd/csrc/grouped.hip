@@ -1,0 +1,515 @@
+// Prefill MoE on gfx950: per-token e4m3 activation quantiser, FP8 x FP8 grouped GEMM on
+// the matrix cores (v_mfma_scale_f32_16x16x128_f8f6f4, unit block scales), the gate/up
+// pass with SwiGLU and the per-128-column e4m3 quantisation of h in its epilogue, and
+// the whole prefill step (router, plan, quantise, gate/up, down, combine) without a
+// host round trip.
+//
+// Grouped GEMM: y[a, r] = xs(a) * sum_kb ws(r, kb) * sum_{c in kb} e4m3(xq[row(a), c]) *
+// e4m3(W[r, c]) for the assignments a of each expert (the semantics of
+// crates/oominf-cuda/kernels/moe.cu:166-335, moe_tiled, with e4m3 activations): each MFMA
+// covers exactly one 128-column scale block, so its fp32 block sum is scaled by the
+// weight's 128 x 128 block scale (and, for per-group activations, the row's group
+// scale) before it joins the accumulator.
+//
+//  * A block takes a 128-assignment x 128-output tile of one expert (8 waves, each
+//    32 x 64); per K step of 128 the block stages the activation rows (gathered by
+//    assignment) and the weight rows in LDS (rows padded to 144 bytes), and the next
+//    step's global loads are in flight while the current step runs on the matrix cores.
+//  * Gate/up: both weight tiles share the activation tile; the epilogue forms
+//    h = silu(g) * u, finds each row's absmax over the tile's 128 columns (the
+//    quantisation group), and writes e4m3 h and its scale.
+#include <algorithm>
+
+#include "router.hpp"
+
+namespace oom {
+
+constexpr int GBM = 128;         // assignments per block tile
+constexpr int GBN = 128;         // outputs per block tile (one 128-row weight scale block)
+constexpr int GBK = 128;         // K step (one scale block)
+constexpr int GPITCH = 144;      // LDS row pitch in bytes
+constexpr int GTHREADS = 512;    // 8 waves: 4 x 2 of 32 x 64
+constexpr int G_BUF_FLAGS = 0x00020000;
+
+typedef int gi32x8 __attribute__((ext_vector_type(8)));
+typedef float gf32x4 __attribute__((ext_vector_type(4)));
+
+struct GArgs {
+    const uint64_t* recs;   // record of expert i (plan order)
+    const int32_t* off;     // assignments of expert i: [off[i], off[i + 1])
+    const int32_t* rows;    // activation row of assignment a (null: a itself)
+    const int32_t* tiles;   // device tile table: [2 mt] = expert, [2 mt + 1] = first assignment offset (or null)
+    const int32_t* ntiles;  // number of tiles in the table
+    const uint8_t* xq;      // e4m3 activations [rows, K]
+    const float* xs;        // per row (x_group 0) or per row and 128-column group (x_group 128)
+    int x_group;
+    int64_t N, K;
+    int64_t w_off, s_off;   // first (or only) weight part and its scales
+    int64_t w2_off, s2_off; // up part (gate/up pass)
+    float* y;               // [A, N] fp32 (plain pass)
+    uint8_t* hq;            // [A, N] e4m3 h (gate/up pass)
+    float* hs;              // [A, N / 128] h scales (gate/up pass)
+};
+
+// e4m3fn code of v, round to nearest even, saturating at +-448 (the quantiser's rule,
+// crates/oominf-core/src/fp8.rs:5-27), with the gfx950 OCP-FP8 conversion.
+__device__ __forceinline__ uint32_t e4m3_pair(float v0, float v1) {
+    v0 = fminf(fmaxf(v0, -448.0f), 448.0f);
+    v1 = fminf(fmaxf(v1, -448.0f), 448.0f);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false) & 0xffffu;
+}
+
+// ---- per-row activation quantiser: scale = absmax / 448 (1 for a zero row), q = e4m3(x / scale)
+// (crates/oominf-core/src/fp8.rs:52-88 applied per token). One block of 256 per row.
+template <int XDT>
+__global__ void __launch_bounds__(256) quant_rows_kernel(const void* __restrict__ x, int64_t cols,
+                                                         uint8_t* __restrict__ q, float* __restrict__ scale) {
+    __shared__ float wmax[4];
+    const int64_t r = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float m = 0.0f;
+    for (int64_t c = tid; c < cols; c += 256) m = fmaxf(m, fabsf(load_act<XDT>(x, r * cols + c)));
+    m = wave_max(m);
+    if (lane == 0) wmax[wave] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+    if (tid == 0) scale[r] = s;
+    for (int64_t c = 2 * tid; c < cols; c += 512) {
+        const float v0 = load_act<XDT>(x, r * cols + c) / s;
+        const float v1 = c + 1 < cols ? load_act<XDT>(x, r * cols + c + 1) / s : 0.0f;
+        const uint32_t p = e4m3_pair(v0, v1);
+        q[r * cols + c] = (uint8_t)(p & 0xff);
+        if (c + 1 < cols) q[r * cols + c + 1] = (uint8_t)(p >> 8);
+    }
+}
+
+// ---- the tile table of a device plan: tile mt = (expert i, assignments from off[i] + m0).
+// One block of 1024 threads; experts in chunks of 1024 with a running carry.
+__global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __restrict__ n_e_p,
+                                                             const int32_t* __restrict__ off,
+                                                             int32_t* __restrict__ tiles, int32_t* __restrict__ ntiles) {
+    __shared__ int wsum[16];
+    __shared__ int carry_s;
+    const int n_e = *n_e_p, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) carry_s = 0;
+    __syncthreads();
+    for (int c0 = 0; c0 < n_e; c0 += (int)blockDim.x) {
+        const int i = c0 + tid;
+        const int cnt = i < n_e ? (off[i + 1] - off[i] + GBM - 1) / GBM : 0;
+        // inclusive scan within the wave, then over the waves
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int before = carry_s;
+        for (int w = 0; w < wave; w++) before += wsum[w];
+        const int start = before + incl - cnt;
+        for (int t = 0; t < cnt; t++) {
+            tiles[2 * (start + t)] = i;
+            tiles[2 * (start + t) + 1] = t * GBM;
+        }
+        __syncthreads();
+        if (tid == (int)blockDim.x - 1) carry_s = start + cnt;
+        __syncthreads();
+    }
+    if (tid == 0) *ntiles = carry_s;
+}
+
+// One K step of a block tile: global -> registers (issued early), registers -> LDS.
+template <int NB>
+struct GStage {
+    uint4 a[2];
+    uint4 b[NB][2];
+};
+
+constexpr int G_OOB = 0x7ffffff0;  // past a weight resource (whose extent stays below 0x7fff0000): loads read 0
+
+__device__ __forceinline__ uint4 g_ld16(__amdgpu_buffer_rsrc_t r, int off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Step kb's activation and weight chunks of this thread. kb < 0 (past the last step):
+// the weight loads take an offset outside their resource (which spans exactly the
+// record's weight parts), so they read zeros without a memory access; the activation
+// resource has no tight bound (the row count is the caller's), so those loads re-read
+// the thread's step-0 chunk, an in-range address, and the data is dropped.
+template <int NB>
+__device__ __forceinline__ void gstage_load(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr, const int (&xo)[2],
+                                            const int (&wo)[NB][2], int kb, GStage<NB>& st) {
+    const int k0 = kb * GBK;
+#pragma unroll
+    for (int j = 0; j < 2; j++) st.a[j] = g_ld16(xr, kb >= 0 ? xo[j] + k0 : xo[j]);
+#pragma unroll
+    for (int m = 0; m < NB; m++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) st.b[m][j] = g_ld16(wr, kb >= 0 ? wo[m][j] + k0 : G_OOB);
+}
+
+template <int NB>
+__device__ __forceinline__ void gstage_store(const GStage<NB>& st, uint8_t* alds, uint8_t* blds, int tid) {
+    const int r = tid >> 3, c16 = (tid & 7) * 16;
+#pragma unroll
+    for (int j = 0; j < 2; j++) *reinterpret_cast<uint4*>(alds + (r + 64 * j) * GPITCH + c16) = st.a[j];
+#pragma unroll
+    for (int m = 0; m < NB; m++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            *reinterpret_cast<uint4*>(blds + (m * GBN + r + 64 * j) * GPITCH + c16) = st.b[m][j];
+}
+
+// 32 bytes of row `row` at K offset 32 (lane / 16): an MFMA operand (A: row = M index,
+// B: row = N index; both layouts take k = 32 (lane / 16) + byte).
+__device__ __forceinline__ gi32x8 gop(const uint8_t* base, int row, int lane) {
+    const uint8_t* p = base + row * GPITCH + 32 * (lane >> 4);
+    const uint4 lo = *reinterpret_cast<const uint4*>(p), hi = *reinterpret_cast<const uint4*>(p + 16);
+    gi32x8 v;
+    v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
+    v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
+    return v;
+}
+
+// MODE 0: y = scaled xq . W^T. MODE 1: gate and up (NB = 2), h = silu(g) * u quantised.
+template <int MODE>
+__global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
+    constexpr int NB = MODE == 1 ? 2 : 1;
+    __shared__ __align__(16) uint8_t alds[GBM * GPITCH];
+    __shared__ __align__(16) uint8_t blds[NB * GBN * GPITCH];
+    __shared__ float rowmax[GBM][2];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;  // rows 32 wm .. + 32, columns 64 wn .. + 64
+    // ---- which tile ----
+    int i, m0;
+    if (g.tiles) {
+        const int mt = blockIdx.y;
+        if (mt >= *g.ntiles) return;
+        i = g.tiles[2 * mt];
+        m0 = g.tiles[2 * mt + 1];
+    } else {
+        i = blockIdx.z;
+        m0 = blockIdx.y * GBM;
+    }
+    const int a0 = g.off[i], a1 = g.off[i + 1];
+    if (a0 + m0 >= a1) return;
+    const int n0 = blockIdx.x * GBN;
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
+    const int nkb = (int)(g.K / GBK);
+    // this thread's staging chunks: activation rows r and r + 64 of the tile (rows past
+    // the expert's range repeat its first), weight rows r and r + 64, 16 bytes at c16
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.xq), (short)0, 0x7fffffff, G_BUF_FLAGS);
+    const int wbytes = (int)(max(g.w_off, NB == 2 ? g.w2_off : g.w_off) + g.N * g.K);  // end of the weight parts
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, wbytes, G_BUF_FLAGS);
+    int xo[2], wo[NB][2];
+    {
+        const int r = tid >> 3, c16 = (tid & 7) * 16;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            int a = a0 + m0 + r + 64 * j;
+            if (a >= a1) a = a0;
+            xo[j] = (int)((g.rows ? g.rows[a] : a) * g.K) + c16;
+#pragma unroll
+            for (int m = 0; m < NB; m++)
+                wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r + 64 * j) * g.K) + c16;
+        }
+    }
+    const float* ws0 = reinterpret_cast<const float*>(rec + g.s_off) + (int64_t)(n0 / 128) * nkb;
+    const float* ws1 = reinterpret_cast<const float*>(rec + g.s2_off) + (int64_t)(n0 / 128) * nkb;
+    // this lane's output rows (per 16-row M subtile ms, element e): assignment index
+    int arow_out[2][4];
+#pragma unroll
+    for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) arow_out[ms][e] = a0 + m0 + 32 * wm + 16 * ms + 4 * (lane >> 4) + e;
+    float acc[NB][2][4][4];  // [matrix][M subtile][N subtile][element]
+#pragma unroll
+    for (int m = 0; m < NB; m++)
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+            for (int ns = 0; ns < 4; ns++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = 0.0f;
+    GStage<NB> st;
+    gstage_load<NB>(xr, wr, xo, wo, 0, st);
+    for (int kb = 0; kb < nkb; kb++) {
+        __syncthreads();  // the previous step's operand reads are done
+        gstage_store<NB>(st, alds, blds, tid);
+        __syncthreads();
+        gstage_load<NB>(xr, wr, xo, wo, kb + 1 < nkb ? kb + 1 : -1, st);
+        // per-row activation group scales of this step (x_group 128)
+        float xsk[2][4];
+        if (g.x_group) {
+#pragma unroll
+            for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int a = min(arow_out[ms][e], a1 - 1);
+                    const int64_t xr = g.rows ? g.rows[a] : a;
+                    xsk[ms][e] = g.xs[xr * nkb + kb];
+                }
+        }
+        float wsk[NB];
+        wsk[0] = ws0[kb];
+        if constexpr (NB == 2) wsk[1] = ws1[kb];
+        gi32x8 aop[2];
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++) aop[ms] = gop(alds, 32 * wm + 16 * ms + (lane & 15), lane);
+#pragma unroll
+        for (int m = 0; m < NB; m++)
+#pragma unroll
+            for (int ns = 0; ns < 4; ns++) {
+                const gi32x8 bop = gop(blds + m * GBN * GPITCH, 64 * wn + 16 * ns + (lane & 15), lane);
+#pragma unroll
+                for (int ms = 0; ms < 2; ms++) {
+                    const gf32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    const gf32x4 blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop[ms], bop, z, 0, 0, 0, 127,
+                                                                                       0, 127);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float s = g.x_group ? wsk[m] * xsk[ms][e] : wsk[m];
+                        acc[m][ms][ns][e] = fmaf(blk[e], s, acc[m][ms][ns][e]);
+                    }
+                }
+            }
+    }
+    // ---- epilogue ----
+    if constexpr (MODE == 0) {
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int a = arow_out[ms][e];
+                if (a >= a1) continue;
+                const float xsr = g.x_group ? 1.0f : g.xs[g.rows ? g.rows[a] : a];
+#pragma unroll
+                for (int ns = 0; ns < 4; ns++) {
+                    const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
+                    if (n < g.N) g.y[(int64_t)a * g.N + n] = g.x_group ? acc[0][ms][ns][e] : acc[0][ms][ns][e] * xsr;
+                }
+            }
+    } else {
+        // h = silu(xs g) * (xs u); row absmax over the tile's 128 columns
+        float h[2][4][4];
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int a = min(arow_out[ms][e], a1 - 1);
+                const float xsr = g.xs[g.rows ? g.rows[a] : a];
+                float mx = 0.0f;
+#pragma unroll
+                for (int ns = 0; ns < 4; ns++) {
+                    const float gv = acc[0][ms][ns][e] * xsr, uv = acc[1][ms][ns][e] * xsr;
+                    h[ms][ns][e] = siluf(gv) * uv;
+                    mx = fmaxf(mx, fabsf(h[ms][ns][e]));
+                }
+                // over the 16 lanes holding this row's columns (lane % 16)
+                mx = fmaxf(mx, dpp_f32<DPP_XOR1>(mx));
+                mx = fmaxf(mx, dpp_f32<DPP_XOR2>(mx));
+                mx = fmaxf(mx, lane_xor<4>(mx, lane));
+                mx = fmaxf(mx, lane_xor<8>(mx, lane));
+                if ((lane & 15) == 0) rowmax[32 * wm + 16 * ms + 4 * (lane >> 4) + e][wn] = mx;
+            }
+        __syncthreads();
+        const int ngrp = (int)(g.N / 128);
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int rr = 32 * wm + 16 * ms + 4 * (lane >> 4) + e;
+                const int a = arow_out[ms][e];
+                const float amax = fmaxf(rowmax[rr][0], rowmax[rr][1]);
+                const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+                if (a >= a1) continue;
+                if (wn == 0 && (lane & 15) == 0) g.hs[(int64_t)a * ngrp + n0 / 128] = s;
+#pragma unroll
+                for (int ns = 0; ns < 4; ns++) {
+                    const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
+                    g.hq[(int64_t)a * g.N + n] = (uint8_t)(e4m3_pair(h[ms][ns][e] / s, 0.0f) & 0xff);
+                }
+            }
+    }
+}
+
+// ---- host side -----------------------------------------------------------------------
+
+int launch_grouped(const GArgs& a, int mode, dim3 grid, hipStream_t st) {
+    if (mode == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
+    else hipLaunchKernelGGL(grouped_gemm_kernel<0>, grid, dim3(GTHREADS), 0, st, a);
+    return launched("grouped_gemm_fp8");
+}
+
+int launch_quant_rows(const void* x, int xdt, int64_t rows, int64_t cols, uint8_t* q, float* s, hipStream_t st) {
+    if (rows == 0) return OOM_OK;
+    if (xdt == OOM_BF16)
+        hipLaunchKernelGGL(quant_rows_kernel<OOM_BF16>, dim3((unsigned)rows), dim3(256), 0, st, x, cols, q, s);
+    else
+        hipLaunchKernelGGL(quant_rows_kernel<OOM_F32>, dim3((unsigned)rows), dim3(256), 0, st, x, cols, q, s);
+    return launched("quantize_rows_fp8");
+}
+
+int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, int32_t* tiles, int32_t* ntiles, hipStream_t st) {
+    hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(1024), 0, st, n_e, off, tiles, ntiles);
+    return launched("grouped_tiles");
+}
+
+}  // namespace oom
+
+// ---- C ABI -----------------------------------------------------------------------------
+
+namespace oom {
+int launch_combine(const float* y, const int32_t* slot, const float* w, void* out, int odt, int T, int H, int k,
+                   hipStream_t st);
+int check_geo(const OomFp8Record* g, const char* who);
+
+// Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | hq | hs | y.
+struct PrefillWs {
+    size_t plan, recs, xq, xs, tiles, hq, hs, y, total;
+    int max_tiles;
+};
+
+static size_t p_al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static PrefillWs prefill_ws(int T, int E, int k, const OomFp8Record& g) {
+    PrefillWs w;
+    const size_t A = (size_t)T * k, H = (size_t)g.hidden, I = (size_t)g.inter;
+    w.max_tiles = (int)(cdiv((int64_t)A, GBM) + std::min<int64_t>(E, (int64_t)A));
+    w.plan = 0;
+    w.recs = p_al256(PlanView::size(E, (int)A) * sizeof(int32_t));
+    w.xq = w.recs + p_al256((size_t)std::min<size_t>(E, A) * sizeof(uint64_t));
+    w.xs = w.xq + p_al256((size_t)T * H);
+    w.tiles = w.xs + p_al256((size_t)T * sizeof(float));
+    w.hq = w.tiles + p_al256((2 * (size_t)w.max_tiles + 1) * sizeof(int32_t));
+    w.hs = w.hq + p_al256(A * I);
+    w.y = w.hs + p_al256(A * (I / 128) * sizeof(float));
+    w.total = w.y + p_al256(A * H * sizeof(float));
+    return w;
+}
+}  // namespace oom
+
+extern "C" int oom_quantize_rows_fp8(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q,
+                                     float* scale, void* stream) {
+    using namespace oom;
+    OOM_REQUIRE(rows >= 0 && rows < (1ll << 31) && cols >= 1, "oom_quantize_rows_fp8: shape");
+    OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_quantize_rows_fp8: x_dtype");
+    if (rows == 0) return OOM_OK;
+    OOM_REQUIRE(x && q && scale, "oom_quantize_rows_fp8: null buffer");
+    return launch_quant_rows(x, x_dtype, rows, cols, q, scale, as_stream(stream));
+}
+
+extern "C" int oom_moe_grouped_gemm_fp8(const uint64_t* recs, const int32_t* off, const int32_t* rows, int n_experts,
+                                        int max_per_expert, const uint8_t* xq, const float* x_scale, int x_group,
+                                        float* y, int64_t N, int64_t K, int64_t w_off, int64_t s_off, void* stream) {
+    using namespace oom;
+    OOM_REQUIRE(n_experts >= 0 && n_experts <= 65535 && max_per_expert >= 0, "oom_moe_grouped_gemm_fp8: experts");
+    OOM_REQUIRE(N >= 128 && N % 128 == 0 && K >= 128 && K % 128 == 0 && N < (1 << 24) && K < (1 << 24),
+                "oom_moe_grouped_gemm_fp8: N and K must be multiples of 128");
+    OOM_REQUIRE(x_group == 0 || x_group == 128, "oom_moe_grouped_gemm_fp8: x_group must be 0 or 128");
+    OOM_REQUIRE(w_off >= 0 && s_off >= 0 && w_off % 16 == 0 && s_off % 4 == 0, "oom_moe_grouped_gemm_fp8: part offsets");
+    OOM_REQUIRE(w_off + N * K < 0x7fff0000ll, "oom_moe_grouped_gemm_fp8: weight part beyond 2 GiB of its record");
+    if (n_experts == 0 || max_per_expert == 0) return OOM_OK;
+    OOM_REQUIRE(recs && off && xq && x_scale && y, "oom_moe_grouped_gemm_fp8: null buffer");
+    OOM_REQUIRE(aligned(xq, 16), "oom_moe_grouped_gemm_fp8: xq must be 16-byte aligned");
+    GArgs a{};
+    a.recs = recs;
+    a.off = off;
+    a.rows = rows;
+    a.xq = xq;
+    a.xs = x_scale;
+    a.x_group = x_group;
+    a.N = N;
+    a.K = K;
+    a.w_off = w_off;
+    a.s_off = s_off;
+    a.w2_off = w_off;
+    a.s2_off = s_off;
+    a.y = y;
+    dim3 grid((unsigned)(N / GBN), (unsigned)cdiv(max_per_expert, GBM), (unsigned)n_experts);
+    return launch_grouped(a, 0, grid, as_stream(stream));
+}
+
+extern "C" size_t oom_moe_prefill_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo) {
+    if (!geo || T < 1 || E < 1 || k < 1) return 0;
+    return oom::prefill_ws(T, E, k, *geo).total;
+}
+
+extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T,
+                                   int E, int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out,
+                                   int out_dtype, void* ws, size_t ws_bytes, void* stream) {
+    using namespace oom;
+    if (int rc = check_geo(geo, "oom_moe_prefill_fp8")) return rc;
+    OOM_REQUIRE(geo->hidden % 128 == 0 && geo->inter % 128 == 0,
+                "oom_moe_prefill_fp8: hidden and inter must be multiples of 128");
+    OOM_REQUIRE(std::max({geo->gate_weight, geo->up_weight, geo->down_weight}) + geo->hidden * geo->inter < 0x7fff0000ll,
+                "oom_moe_prefill_fp8: weight parts beyond 2 GiB of their record");
+    OOM_REQUIRE(T >= 1 && (int64_t)T * k <= (1 << 24), "oom_moe_prefill_fp8: T must be >= 1 and T * k <= 2^24");
+    OOM_REQUIRE(k >= 1 && k <= 32 && E >= k && E <= 8192, "oom_moe_prefill_fp8: router top-k > 32 or experts > 8192");
+    OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_moe_prefill_fp8: x_dtype");
+    OOM_REQUIRE(out_dtype == OOM_F32 || out_dtype == OOM_BF16, "oom_moe_prefill_fp8: out_dtype");
+    OOM_REQUIRE(logits && x && all_recs && ids && weights && out, "oom_moe_prefill_fp8: null buffer");
+    const PrefillWs w = prefill_ws(T, E, k, *geo);
+    if (!ws || ws_bytes < w.total)
+        return fail(OOM_ERR_WORKSPACE, "oom_moe_prefill_fp8: workspace smaller than oom_moe_prefill_fp8_workspace_size()");
+    OOM_REQUIRE(aligned(ws, 256), "oom_moe_prefill_fp8: workspace must be 256-byte aligned");
+    uint8_t* base = reinterpret_cast<uint8_t*>(ws);
+    int32_t* plan = reinterpret_cast<int32_t*>(base + w.plan);
+    uint64_t* recs = reinterpret_cast<uint64_t*>(base + w.recs);
+    uint8_t* xq = base + w.xq;
+    float* xs = reinterpret_cast<float*>(base + w.xs);
+    int32_t* tiles = reinterpret_cast<int32_t*>(base + w.tiles);
+    int32_t* ntiles = tiles + 2 * w.max_tiles;
+    uint8_t* hq = base + w.hq;
+    float* hs = reinterpret_cast<float*>(base + w.hs);
+    float* y = reinterpret_cast<float*>(base + w.y);
+    hipStream_t st = as_stream(stream);
+    const int A = T * k;
+    PlanView pv{plan, E, A};
+    if (int rc = oom_router_topk(logits, ids, weights, T, E, k, stream)) return rc;
+    if (int rc = oom_moe_plan(ids, T, E, k, all_recs, plan, recs, stream)) return rc;
+    if (int rc = launch_quant_rows(x, x_dtype, T, geo->hidden, xq, xs, st)) return rc;
+    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), tiles, ntiles, st)) return rc;
+    GArgs a{};
+    a.recs = recs;
+    a.off = pv.off();
+    a.rows = pv.assign_tok();
+    a.tiles = tiles;
+    a.ntiles = ntiles;
+    a.xq = xq;
+    a.xs = xs;
+    a.x_group = 0;
+    a.N = geo->inter;
+    a.K = geo->hidden;
+    a.w_off = geo->gate_weight;
+    a.s_off = geo->gate_scale;
+    a.w2_off = geo->up_weight;
+    a.s2_off = geo->up_scale;
+    a.hq = hq;
+    a.hs = hs;
+    if (int rc = launch_grouped(a, 1, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles, 1), st)) return rc;
+    GArgs d{};
+    d.recs = recs;
+    d.off = pv.off();
+    d.rows = nullptr;
+    d.tiles = tiles;
+    d.ntiles = ntiles;
+    d.xq = hq;
+    d.xs = hs;
+    d.x_group = 128;
+    d.N = geo->hidden;
+    d.K = geo->inter;
+    d.w_off = geo->down_weight;
+    d.s_off = geo->down_scale;
+    d.w2_off = geo->down_weight;
+    d.s2_off = geo->down_scale;
+    d.y = y;
+    if (int rc = launch_grouped(d, 0, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles, 1), st)) return rc;
+    return launch_combine(y, pv.slot_assign(), weights, out, out_dtype, T, (int)geo->hidden, k, st);
+}

@@ -242,7 +242,7 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
     store_out<ODT>(out, i, acc);
 }
 
-static int check_geo(const OomFp8Record* geo, const char* who) {
+int check_geo(const OomFp8Record* geo, const char* who) {
     if (!geo) return fail(OOM_ERR_ARG, std::string(who) + ": null geometry");
     const OomFp8Record& g = *geo;
     bool ok = g.hidden >= 16 && g.inter >= 16 && g.hidden % 16 == 0 && g.inter % 16 == 0 && g.hidden <= (1 << 20) &&

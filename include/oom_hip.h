@@ -132,6 +132,40 @@ int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const ui
                        int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
                        void* ws, size_t ws_bytes, void* stream);
 
+/* Per-row e4m3 quantisation of activations: scale[r] = max_c |x[r, c]| / 448 (1 for an
+ * all-zero row), q[r, c] = e4m3(x[r, c] / scale[r]) rounded to nearest even and
+ * saturating at +-448 (crates/oominf-core/src/fp8.rs:5-88, block = one row). x [rows,
+ * cols] in x_dtype; q u8 [rows, cols]; scale f32 [rows]. The prefill's per-token
+ * activation quantiser. */
+int oom_quantize_rows_fp8(const void* x, int x_dtype, int64_t rows, int64_t cols, uint8_t* q, float* scale,
+                          void* stream);
+
+/* FP8 x FP8 grouped GEMM of one projection of each expert, on the matrix cores:
+ *   y[a, r] = xs(a) * sum_kb ws_e(r, kb) * sum_{c in kb} e4m3(xq[row(a), c]) * e4m3(W_e[r, c])
+ * for the assignments a in [off[i], off[i+1]) of expert i < n_experts (record at
+ * recs[i]; W_e [N, K] e4m3 at byte w_off, its 128 x 128 fp32 scales at s_off),
+ * row(a) = rows ? rows[a] : a. x_group 0: xs(a) = x_scale[row(a)] multiplies the result;
+ * x_group 128: x_scale[row(a) * K / 128 + kb] joins ws inside the kb sum. y f32 [A, N].
+ * N, K multiples of 128; max_per_expert bounds off[i+1] - off[i] (the host plan's).
+ * Replaces Experts::moe_tiled (crates/oominf-core/src/backend.rs:869-883;
+ * crates/oominf-cuda/src/experts.rs:214-260; crates/oominf-cuda/kernels/moe.cu:166-335)
+ * for e4m3 records and e4m3 activations. */
+int oom_moe_grouped_gemm_fp8(const uint64_t* recs, const int32_t* off, const int32_t* rows, int n_experts,
+                             int max_per_expert, const uint8_t* xq, const float* x_scale, int x_group, float* y,
+                             int64_t N, int64_t K, int64_t w_off, int64_t s_off, void* stream);
+
+/* One prefill MoE FFN step on the device, with no host synchronisation: router top-k,
+ * routing plan, x quantised per token to e4m3, gate and up grouped GEMMs with
+ * h = silu(g) * u quantised per (assignment, 128 columns) in the same pass, down grouped
+ * GEMM, slot-order weighted combine. logits f32 [T, E]; x [T, hidden] in x_dtype; out
+ * [T, hidden] in out_dtype; ids / weights as oom_router_topk. hidden and inter multiples
+ * of 128. The tiled prefill of Moe::forward (crates/oominf-models-qwen/src/moe.rs:700,
+ * 746-758: run_group over moe_tiled and moe_swiglu_range) with FP8 activations. */
+size_t oom_moe_prefill_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo);
+int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T, int E,
+                        int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
+                        void* ws, size_t ws_bytes, void* stream);
+
 /* Paged GQA decode attention for one query token: out[h, :] = sum_j softmax_j(q_h . k_j
  * * scale) v_j over the kv_len keys, query head h reading KV head h / (heads / kv_heads).
  * q [heads, d] in q_dtype; k_pages and v_pages bf16 [n_pages, page_size, kv_heads, d]
