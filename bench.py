@@ -314,12 +314,106 @@ def bench_attn(args):
     return res
 
 
+PEAK_FP8_TFLOPS = 5000.0
+
+
+def bench_prefill(args):
+    """MoE prefill step: 2048 tokens, hidden 4096, 128 experts top-8 with Zipf(1.1)-biased
+    N(0, 1) router logits, e4m3 128x128-block-scaled expert weights (gate/up 1536 x 4096,
+    down 4096 x 1536) from N(0, 0.02), bf16 x from N(0, 1); per-token e4m3 activations,
+    grouped GEMMs on FP8 MFMA, SiLU*mul, weighted combine (oom_moe_prefill_fp8)."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    T, E, k, H, I = 2048, 128, 8, 4096, 1536
+    geo = hip.record_geometry(H, I)
+    stride = hip.record_stride(geo)
+    log(f"bench: prefill T={T} E={E} k={k} H={H} I={I}; building an expert set of {E * stride / 1e9:.2f} GB")
+    rec = make_expert_set(E, geo, stride, 4321, torch)
+    addrs = torch.tensor([rec.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17)
+    n = args.warmup + args.steps
+    bias = torch.from_numpy(zipf_bias(E, 1.1, 7)).cuda()
+    logits = (torch.randn((n, T, E), generator=g, device="cuda") + bias).contiguous()
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ids = torch.empty((n, T, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n, T, k), dtype=torch.float32, device="cuda")
+    ws = torch.zeros(hip.moe_prefill_fp8_workspace_size(T, E, k, geo), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        hip.moe_prefill_fp8(logits[i], x, addrs, k, geo, ids[i], wts[i], out, ws, stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(args.warmup, n):
+        step(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    idn = ids[args.warmup:].cpu().numpy()
+    distinct = float(np.mean([len(np.unique(s_)) for s_ in idn]))
+    per_expert = 3 * H * I + 3 * (H // 128) * (I // 128) * 4
+    bytes_step = distinct * per_expert + T * H * 2 * 2
+    flops = 2.0 * T * k * 3 * H * I
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = {
+        "metric": "MoE FP8 prefill step us/step + achieved HBM GB/s and FP8 MFMA TFLOP/s (% of MI355X peak), 1 GPU",
+        "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3 weights and activations, fp32 accumulate, bf16 out", "data": "synthetic",
+        "config": {"workload": "MoE prefill grouped GEMM: 2048 tokens x hidden 4096, 128 experts top-8 with Zipf(1.1) "
+                               "biased logits, inter 1536, e4m3 128x128-block-scaled weights, per-token e4m3 "
+                               "activations", "tokens": T, "experts": E, "top_k": k, "hidden": H, "inter": I,
+                   "distinct_experts_per_step": distinct, "tokens_per_s": T / (ms * 1e-3)},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": measured_traffic("prefill"), "kernel": "oom_moe_prefill_fp8 step (all its kernels)",
+                     "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
+        "mfma": {"achieved": tflops, "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s", "frac": tflops / PEAK_FP8_TFLOPS,
+                 "flops_per_step": flops},
+    }
+    if not args.no_cpu:
+        import oracle
+
+        host = rec.cpu().numpy()
+        ogeo = oracle.record_geometry(H, I)
+        sample = 64
+        lg = logits[0, :sample].cpu().numpy()
+        xs = x[:sample].float().cpu().numpy()
+        cores = usable_cores()
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            ids_h, w_h = oracle.router_topk(lg, k)
+            experts, off, tok, slot = oracle.moe_plan(ids_h, E)
+            jobs = [tok[off[i]:off[i + 1]] for i in range(len(experts))]
+            y = oracle.host_experts(ogeo, [host[e] for e in experts], jobs, xs, cores)
+            oracle.moe_combine_slots(y, slot, w_h)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds and reps >= 1:
+                break
+        res["cpu_baseline"] = {"value": el / reps / sample * T * 1e6, "unit": "us/step", "cores": cores, "kind": "port",
+                               "sample": f"{reps} runs of the first {sample} tokens of a step (router, plan, "
+                                         f"HostExperts, combine: the reference CPU path, oracle restatement), scaled "
+                                         f"to {T} tokens, on {cpu_model()}"}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "attn", "copy"])
+    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "attn", "prefill", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -337,6 +431,8 @@ def main():
                "copies": args.steps + 1}
     elif args.config == "attn":
         res = bench_attn(args)
+    elif args.config == "prefill":
+        res = bench_prefill(args)
     elif args.config == "decode1":
         res = bench_decode(args, 1, None, args.config)
     else:

@@ -230,16 +230,30 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint64_t* __restric
 
 // out[t, c] = sum_s w[t, s] * y[slot_assign[t, s], c] in slot order
 // (crates/oominf-cuda/kernels/moe.cu:153-164).
+// out[t, c] = sum_s w[t, s] * y[slot[t, s], c] in slot order. Block (token t, column
+// chunk of 1024): each thread 4 consecutive columns with 16-byte loads of y.
 template <int ODT>
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ slot,
                                                           const float* __restrict__ w, void* __restrict__ out, int T,
                                                           int H, int k) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)T * H) return;
-    int t = (int)(i / H), c = (int)(i % H);
-    float acc = 0.0f;
-    for (int s = 0; s < k; s++) acc = fmaf(w[t * k + s], y[(size_t)slot[t * k + s] * H + c], acc);
-    store_out<ODT>(out, i, acc);
+    const int t = blockIdx.x, c0 = blockIdx.y * 1024 + 4 * threadIdx.x;
+    if (c0 >= H) return;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool vec = c0 + 4 <= H && (H & 3) == 0;
+    for (int s = 0; s < k; s++) {
+        const float ws = w[t * k + s];
+        const float* row = y + (size_t)slot[t * k + s] * H;
+        if (vec) {
+            const float4 v = *reinterpret_cast<const float4*>(row + c0);
+            acc[0] = fmaf(ws, v.x, acc[0]);
+            acc[1] = fmaf(ws, v.y, acc[1]);
+            acc[2] = fmaf(ws, v.z, acc[2]);
+            acc[3] = fmaf(ws, v.w, acc[3]);
+        } else {
+            for (int j = 0; j < 4 && c0 + j < H; j++) acc[j] = fmaf(ws, row[c0 + j], acc[j]);
+        }
+    }
+    for (int j = 0; j < 4 && c0 + j < H; j++) store_out<ODT>(out, (size_t)t * H + c0 + j, acc[j]);
 }
 
 int check_geo(const OomFp8Record* geo, const char* who) {
@@ -283,8 +297,7 @@ int launch_down(const uint64_t* recs, const int32_t* off, int grid_e, const floa
 
 int launch_combine(const float* y, const int32_t* slot, const float* w, void* out, int odt, int T, int H, int k,
                    hipStream_t st) {
-    size_t n = (size_t)T * H;
-    dim3 grid((unsigned)((n + 255) / 256));
+    dim3 grid((unsigned)T, (unsigned)cdiv(H, 1024));
     if (odt == OOM_BF16)
         hipLaunchKernelGGL((moe_combine_kernel<OOM_BF16>), grid, dim3(256), 0, st, y, slot, w, out, T, H, k);
     else

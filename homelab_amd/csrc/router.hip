@@ -3,6 +3,9 @@
 
 namespace oom {
 
+// Experts up to which the plan ranks slots with ballots and per-wave LDS counts.
+constexpr int PLAN_FAST_E = 512;
+
 // One wave per token (grid T, block 64, dynamic LDS E floats).
 __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict__ logits, int32_t* __restrict__ ids,
                                                          float* __restrict__ weights, int E, int k) {
@@ -93,6 +96,42 @@ __global__ void __launch_bounds__(1024) moe_plan_kernel(const int32_t* __restric
     for (int i = n_e + tid; i <= E; i += blockDim.x) plan.off()[i] = A;
     if (tid == 0) *plan.n_e() = n_e;
     __syncthreads();
+    if (E <= PLAN_FAST_E) {
+        // Positions in rounds of 1024 slots. Within a wave, the lanes holding the same id
+        // find each other by ballots over the id's bits (rank = peers below this lane);
+        // per-wave counts per id in LDS give the waves before this one.
+        int* wcnt = lds + E;  // [16][E]
+        const int lane = tid & 63, wave = tid >> 6, nbits = 32 - __builtin_clz((unsigned)max(E - 1, 1));
+        for (int base = 0; base < A; base += blockDim.x) {
+            for (int i = tid; i < 16 * E; i += blockDim.x) wcnt[i] = 0;
+            __syncthreads();
+            const int s = base + tid;
+            const int e = s < A ? ids[s] : -1;
+            uint64_t peers = __ballot(e >= 0);
+            for (int b = 0; b < nbits; b++) {
+                const uint64_t bal = __ballot(e >= 0 && ((e >> b) & 1));
+                peers &= ((e >> b) & 1) ? bal : ~bal;
+            }
+            const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+            const int rank = (int)__builtin_popcountll(peers & below);
+            if (e >= 0 && rank == 0) wcnt[wave * E + e] = (int)__builtin_popcountll(peers);
+            __syncthreads();
+            if (e >= 0) {
+                int pos = start[e] + rank;
+                for (int w = 0; w < wave; w++) pos += wcnt[w * E + e];
+                plan.assign_tok()[pos] = s / k;
+                plan.slot_assign()[s] = pos;
+            }
+            __syncthreads();
+            for (int i = tid; i < E; i += blockDim.x) {
+                int c = 0;
+                for (int w = 0; w < 16; w++) c += wcnt[w * E + i];
+                start[i] += c;
+            }
+            __syncthreads();
+        }
+        return;
+    }
     // Positions in rounds of blockDim slots: a slot's rank among the equal ids before it.
     for (int base = 0; base < A; base += blockDim.x) {
         int s = base + tid;
@@ -132,7 +171,9 @@ extern "C" int oom_moe_plan(const int32_t* ids, int T, int E, int k, const uint6
     OOM_REQUIRE(T >= 1 && k >= 1 && E >= 1 && E <= 8192, "oom_moe_plan: shape unsupported");
     OOM_REQUIRE((int64_t)T * k <= (1 << 24), "oom_moe_plan: too many assignments");
     OOM_REQUIRE(ids && all_recs && plan && recs, "oom_moe_plan: null buffer");
-    size_t lds = ((size_t)E + 1024) * sizeof(int);
+    // count / start [E], then the rank rounds' table: per-wave counts [16][E] (E <= PLAN_FAST_E)
+    // or the ids of one round [1024]
+    size_t lds = ((size_t)E + (E <= oom::PLAN_FAST_E ? 16 * (size_t)E : 1024)) * sizeof(int);
     hipLaunchKernelGGL(oom::moe_plan_kernel, dim3(1), dim3(1024), lds, oom::as_stream(stream), ids, T * k, E, k,
                        all_recs, plan, recs);
     return oom::launched("oom_moe_plan");
