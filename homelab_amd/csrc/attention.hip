@@ -95,15 +95,6 @@ __device__ __forceinline__ void kv_load(const AttnArgs& a, int g, int key0, int 
     }
 }
 
-// Compiler-only ordering for the in-wave LDS exchange: a wave's LDS operations complete
-// in issue order, so another lane's ds_write is visible to a later ds_read of the same
-// wave; no wait on outstanding global loads (the next tile's) is needed.
-__device__ __forceinline__ void wave_lds_order() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_wave_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // One 16-key tile: scores, online softmax update of (m, l) for head lane % 16, and
 // acc += P . V. plds / clds are this wave's LDS rows.
 template <int D, int NQ>

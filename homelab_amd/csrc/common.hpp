@@ -90,6 +90,15 @@ __device__ __forceinline__ void store_out(void* p, size_t i, float v) {
 
 __device__ __forceinline__ float siluf(float v) { return v / (1.0f + expf(-v)); }
 
+// Compiler-only ordering for an exchange through LDS inside one wave: a wave's LDS
+// operations complete in issue order, so another lane's ds_write is visible to a later
+// ds_read of the same wave; no wait on outstanding global memory operations is needed.
+__device__ __forceinline__ void wave_lds_order() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // ---- wavefront reductions (wave64) -----------------------------------------------
 
 // v of another lane through DPP (no LDS): CTRL is a gfx9 dpp_ctrl code.

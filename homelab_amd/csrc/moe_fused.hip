@@ -585,6 +585,41 @@ __device__ __forceinline__ void grid_barrier(const FusedArgs& a) {
     __syncthreads();
 }
 
+// The plan of up to 64 slots on one wave, lane s = slot s: ranks by readlane
+// broadcast, no LDS round trips. Reads pl.ids, writes slot_assign, assign_tok, experts,
+// off and n_e.
+__device__ __forceinline__ void plan_wave(PlanLds& pl, int A, int k, int lane) {
+    const int e = lane < A ? pl.ids[lane] : 0x7fffffff;
+    int pos = 0, below = 0, first = 1;
+    for (int j = 0; j < A; j++) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        pos += (ej < e) || (ej == e && j < lane);
+        below += ej < e;
+        first &= !(ej == e && j < lane);
+    }
+    const uint64_t firsts = __ballot(lane < A && first);
+    if (lane < A) {
+        pl.slot_assign[lane] = pos;
+        pl.assign_tok[pos] = lane / k;
+        if (first) {
+            // experts in id order: the rank of this first slot among first slots by id
+            int eidx = 0;
+            for (int j = 0; j < A; j++) {
+                const int ej = __builtin_amdgcn_readlane(e, j);
+                const int fj = (int)((firsts >> j) & 1ull);
+                eidx += fj && ej < e;
+            }
+            pl.experts[eidx] = e;
+            pl.off[eidx] = below;
+        }
+    }
+    if (lane == 0) {
+        const int n = (int)__builtin_popcountll(firsts);
+        pl.n_e = n;
+        pl.off[n] = A;
+    }
+}
+
 template <int TG, int DCH, int XDT, int ODT>
 __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
     __shared__ PlanLds pl;
@@ -595,76 +630,59 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
     if (tid < E) pl.recs[tid] = a.all_recs[tid];
     XRow<XDT> xr;
     if constexpr (TG == 1) xrow_load<XDT>(a.x, (int)a.H, lane, xr);
-    // ---- routing (every block) ----
-    for (int t = wave; t < T; t += FW) {
-        int id = 0;
-        float w = 0.0f;
-        route_token_regs(a.logits + (size_t)t * E, E, k, lane, id, w);
-        if (lane < k) {
-            pl.ids[t * k + lane] = id;
-            pl.w[t * k + lane] = w;
-        }
-    }
-    __syncthreads();
-    // ---- plan: slots sorted by (expert, slot); experts in id order ----
-    if (A <= 64) {
-        // one wave, lane s = slot s: ranks by readlane broadcast, no LDS round trips
+    // ---- routing and plan: slots sorted by (expert, slot), experts in id order ----
+    if (T == 1) {
+        // one token: wave 0 routes it and plans in place, one block-wide sync
         if (wave == 0) {
-            const int e = lane < A ? pl.ids[lane] : 0x7fffffff;
-            int pos = 0, below = 0, first = 1;
-            for (int j = 0; j < A; j++) {
-                const int ej = __builtin_amdgcn_readlane(e, j);
-                pos += (ej < e) || (ej == e && j < lane);
-                below += ej < e;
-                first &= !(ej == e && j < lane);
+            int id = 0;
+            float w = 0.0f;
+            route_token_regs(a.logits, E, k, lane, id, w);
+            if (lane < k) {
+                pl.ids[lane] = id;
+                pl.w[lane] = w;
             }
-            const uint64_t firsts = __ballot(lane < A && first);
-            if (lane < A) {
-                pl.slot_assign[lane] = pos;
-                pl.assign_tok[pos] = lane / k;
-                if (first) {
-                    // experts in id order: the rank of this first slot among first slots by id
-                    int eidx = 0;
-                    for (int j = 0; j < A; j++) {
-                        const int ej = __builtin_amdgcn_readlane(e, j);
-                        const int fj = (int)((firsts >> j) & 1ull);
-                        eidx += fj && ej < e;
-                    }
-                    pl.experts[eidx] = e;
-                    pl.off[eidx] = below;
-                }
-            }
-            if (lane == 0) {
-                const int n = (int)__builtin_popcountll(firsts);
-                pl.n_e = n;
-                pl.off[n] = A;
-            }
+            wave_lds_order();
+            plan_wave(pl, A, k, lane);
         }
     } else {
-        for (int s = tid; s < A; s += blockDim.x) {
-            const int e = pl.ids[s];
-            int pos = 0;
-            for (int s2 = 0; s2 < A; s2++) {
-                const int e2 = pl.ids[s2];
-                pos += (e2 < e) || (e2 == e && s2 < s);
+        for (int t = wave; t < T; t += FW) {
+            int id = 0;
+            float w = 0.0f;
+            route_token_regs(a.logits + (size_t)t * E, E, k, lane, id, w);
+            if (lane < k) {
+                pl.ids[t * k + lane] = id;
+                pl.w[t * k + lane] = w;
             }
-            pl.sorted[pos] = e;
-            pl.slot_assign[s] = pos;
-            pl.assign_tok[pos] = s / k;
         }
         __syncthreads();
-        for (int p = tid; p < A; p += blockDim.x) {
-            if (p == 0 || pl.sorted[p - 1] != pl.sorted[p]) {
-                int idx = 0;
-                for (int q = 1; q <= p; q++) idx += pl.sorted[q - 1] != pl.sorted[q];
-                pl.experts[idx] = pl.sorted[p];
-                pl.off[idx] = p;
+        if (A <= 64) {
+            if (wave == 0) plan_wave(pl, A, k, lane);
+        } else {
+            for (int s = tid; s < A; s += blockDim.x) {
+                const int e = pl.ids[s];
+                int pos = 0;
+                for (int s2 = 0; s2 < A; s2++) {
+                    const int e2 = pl.ids[s2];
+                    pos += (e2 < e) || (e2 == e && s2 < s);
+                }
+                pl.sorted[pos] = e;
+                pl.slot_assign[s] = pos;
+                pl.assign_tok[pos] = s / k;
             }
-            if (p == A - 1) {
-                int n = 1;
-                for (int q = 1; q < A; q++) n += pl.sorted[q - 1] != pl.sorted[q];
-                pl.n_e = n;
-                pl.off[n] = A;
+            __syncthreads();
+            for (int p = tid; p < A; p += blockDim.x) {
+                if (p == 0 || pl.sorted[p - 1] != pl.sorted[p]) {
+                    int idx = 0;
+                    for (int q = 1; q <= p; q++) idx += pl.sorted[q - 1] != pl.sorted[q];
+                    pl.experts[idx] = pl.sorted[p];
+                    pl.off[idx] = p;
+                }
+                if (p == A - 1) {
+                    int n = 1;
+                    for (int q = 1; q < A; q++) n += pl.sorted[q - 1] != pl.sorted[q];
+                    pl.n_e = n;
+                    pl.off[n] = A;
+                }
             }
         }
     }

@@ -77,13 +77,37 @@ __device__ __forceinline__ void route_token_wave(const float* __restrict__ l, in
     if (lane < k) w_out = w_out / picked;
 }
 
+// Maximum over the wave of a 64-bit unsigned key (every lane ends with it).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v, int lane) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+#define OOM_MAX_U64_STEP(O)                                                                    \
+    {                                                                                          \
+        const uint32_t plo = __float_as_uint(lane_xor<O>(__uint_as_float(lo), lane));          \
+        const uint32_t phi = __float_as_uint(lane_xor<O>(__uint_as_float(hi), lane));          \
+        const bool take = ((uint64_t)phi << 32 | plo) > ((uint64_t)hi << 32 | lo);             \
+        lo = take ? plo : lo;                                                                  \
+        hi = take ? phi : hi;                                                                  \
+    }
+    OOM_MAX_U64_STEP(1)
+    OOM_MAX_U64_STEP(2)
+    OOM_MAX_U64_STEP(4)
+    OOM_MAX_U64_STEP(8)
+    OOM_MAX_U64_STEP(16)
+    OOM_MAX_U64_STEP(32)
+#undef OOM_MAX_U64_STEP
+    return (uint64_t)hi << 32 | lo;
+}
+
 // route_token_wave for E <= 256, without LDS round trips: lane l holds experts
-// l + 64 q (q < 4) in registers; sums keep the reference's order (sum32_xor_order);
-// each of the k rounds takes the wave maximum of p, then the lowest id holding it
-// (ballots), which is the reference's argmax with ties to the lower id.
+// l + 64 q (q < 4) in registers; sums keep the reference's order (sum32_xor_order).
+// The k picks rank experts by one 64-bit key, the probability's bits above the
+// complemented id: p >= 0, so a larger key is a larger p, and among equal p the lower
+// id, which is the reference's argmax with ties to the lower id. Each round is one wave
+// maximum of the lanes' best keys; the winner's lane drops that key (0 is below every
+// expert's key) and takes its next best.
 __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int k, int lane, int& id_out,
                                                  float& w_out) {
-    float lv[4], p[4];
+    float lv[4];
     float m = -INFINITY;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -101,25 +125,30 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, in
         w8[2 * q + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
     }
     const float sum = ((w8[0] + w8[4]) + (w8[2] + w8[6])) + ((w8[1] + w8[5]) + (w8[3] + w8[7]));
+    uint64_t key[4], best_mine = 0;
 #pragma unroll
-    for (int q = 0; q < 4; q++) p[q] = lane + 64 * q < E ? ex[q] / sum : -3.0f;
+    for (int q = 0; q < 4; q++) {
+        const int e = lane + 64 * q;
+        key[q] = e < E ? ((uint64_t)__float_as_uint(ex[q] / sum) << 32) | (uint32_t)~(uint32_t)e : 0ull;
+        best_mine = key[q] > best_mine ? key[q] : best_mine;
+    }
     float picked = 0.0f;
     for (int r = 0; r < k; r++) {
-        const float best = wave_max(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])));
-        int e = -1;
+        const uint64_t best = wave_max_u64(best_mine, lane);
+        const int e = (int)~(uint32_t)best;
+        const float p = __uint_as_float((uint32_t)(best >> 32));
+        if ((e & 63) == lane) {
+            best_mine = 0;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint64_t b = __ballot(p[q] == best);
-            if (e < 0 && b) e = 64 * q + (int)__builtin_ctzll(b);
+            for (int q = 0; q < 4; q++) {
+                if (key[q] == best) key[q] = 0;
+                best_mine = key[q] > best_mine ? key[q] : best_mine;
+            }
         }
-        // the winner's lane marks it used (below every probability)
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-            if (64 * q + lane == e) p[q] = -2.0f;
-        picked += best;
+        picked += p;
         if (lane == r) {
             id_out = e;
-            w_out = best;
+            w_out = p;
         }
     }
     if (lane < k) w_out = w_out / picked;
