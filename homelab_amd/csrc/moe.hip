@@ -11,6 +11,7 @@
 // the weight decode is e4m3 * 128x128 block scale, applied to each lane's 16-term
 // partial (16 columns never straddle a 128-column block).
 #include "router.hpp"
+#include "stream.hpp"
 
 namespace oom {
 
@@ -324,8 +325,8 @@ static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 static DecodeWs decode_ws(int T, int E, int k, const OomFp8Record& g) {
     DecodeWs w;
     size_t A = (size_t)T * k;
-    w.plan = 0;
-    w.recs = al256(PlanView::size(E, (int)A) * sizeof(int32_t));
+    w.plan = WS_HEADER;  // the header holds the one-launch kernels' state between calls
+    w.recs = w.plan + al256(PlanView::size(E, (int)A) * sizeof(int32_t));
     w.h = w.recs + al256((size_t)std::min<size_t>(E, A) * sizeof(uint64_t));
     w.y = w.h + al256(A * (size_t)g.inter * sizeof(float));
     w.total = w.y + al256(A * (size_t)g.hidden * sizeof(float));

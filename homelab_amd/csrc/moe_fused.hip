@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include "router.hpp"
+#include "stream.hpp"
 
 namespace oom {
 
@@ -40,11 +41,6 @@ constexpr int F_EMAX = 256;  // experts (register router; larger E takes the mul
 constexpr int F_HMAX = 4096; // hidden: 4 chunks of 1024 per lane row
 constexpr int F_IMAX = 2048; // inter: 2 chunks
 constexpr uint32_t F_SPIN_LIMIT = 1u << 22;
-constexpr int BAR_GROUPS = 8;   // barrier groups (one per XCD)
-constexpr int BAR_STRIDE = 64;  // u32 words between counters: one 256-byte line each
-constexpr int TICKET_STRIDE = 64;
-constexpr int BUF_FLAGS = 0x00020000;  // buffer resource word 3: 32-bit data format
-constexpr int OOB = 0x7ffffff0;        // an offset past every resource: loads read 0
 
 struct FusedArgs {
     const float* logits;
@@ -89,29 +85,10 @@ __device__ __forceinline__ void load16(const void* base, size_t off, float* v) {
     }
 }
 
-// Values handed between waves of different XCDs inside the kernel (h, y) move with
-// device-coherent (sc1) dword stores and loads, which skip the per-XCD L2 instead of
-// writing it back or invalidating it: an agent-scope fence lowers to buffer_wbl2 /
-// buffer_inv of the whole L2, far too costly per work item. A producer waits for its
-// stores (s_waitcnt) before it bumps the counter a consumer polls.
-__device__ __forceinline__ void st_dev(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Cache-policy bit of buffer loads for a device-coherent (sc1) access on gfx950.
-constexpr int BUF_SC1 = 16;
-
-// All of this wave's memory operations complete (stores acknowledged) before the next.
-__device__ __forceinline__ void wait_mem() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 struct PlanLds {
     uint64_t recs[F_EMAX];  // all_recs, read once per block
+    uint64_t keys[2 * FW];  // one-token routing scratch (route_select)
+    float p[2 * FW];
     int n_e;
     int experts[F_AMAX];
     int off[F_AMAX + 1];
@@ -351,52 +328,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rec_rsrc(const PlanLds& pl, in
                                              BUF_FLAGS);
 }
 
-__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, int off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-}
-__device__ __forceinline__ float ldf(__amdgpu_buffer_rsrc_t r, int off) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
-
-// The token's activations: lane l holds columns 1024 c + 16 l .. + 16 (c < 4), zeros
-// past hidden.
-template <int XDT>
-struct XRow;
-template <>
-struct XRow<OOM_BF16> {
-    uint32_t w[4][8];
-};
-template <>
-struct XRow<OOM_F32> {
-    float v[4][16];
-};
-
-template <int XDT>
-__device__ __forceinline__ void xrow_load(const void* x, int H, int lane, XRow<XDT>& xr) {
-    constexpr int ES = XDT == OOM_BF16 ? 2 : 4;
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, H * ES, BUF_FLAGS);
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const int col = c * 1024 + lane * 16;
-        const int off = col < H ? col * ES : OOB;
-        if constexpr (XDT == OOM_BF16) {
-            const uint4 a0 = ld16(r, off), a1 = ld16(r, off + 16);
-            xr.w[c][0] = a0.x; xr.w[c][1] = a0.y; xr.w[c][2] = a0.z; xr.w[c][3] = a0.w;
-            xr.w[c][4] = a1.x; xr.w[c][5] = a1.y; xr.w[c][6] = a1.z; xr.w[c][7] = a1.w;
-        } else {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint4 v = ld16(r, off + 16 * q);
-                xr.v[c][4 * q] = __uint_as_float(v.x);
-                xr.v[c][4 * q + 1] = __uint_as_float(v.y);
-                xr.v[c][4 * q + 2] = __uint_as_float(v.z);
-                xr.v[c][4 * q + 3] = __uint_as_float(v.w);
-            }
-        }
-    }
-}
-
 // Gate/up item `it` (expert it / I, row it % I): one gate row and one up row, 1024
 // columns per chunk, and their 128 x 128-block scales; an item past NG reads zeros.
 struct Gate1 {
@@ -620,7 +551,7 @@ __device__ __forceinline__ void plan_wave(PlanLds& pl, int A, int k, int lane) {
     }
 }
 
-template <int TG, int DCH, int XDT, int ODT>
+template <int TG, int DCH, int EQ, int XDT, int ODT>
 __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
     __shared__ PlanLds pl;
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
@@ -634,15 +565,17 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
     if (T == 1) {
         // one token: wave 0 routes it and plans in place, one block-wide sync
         if (wave == 0) {
-            int id = 0;
-            float w = 0.0f;
-            route_token_regs(a.logits, E, k, lane, id, w);
+            // picks and plan in one pass (ballot radix selection); with one token the
+            // plan's assignment i is expert slot i
+            route_select<EQ>(a.logits, E, k, lane, pl.keys, pl.p, pl.experts, pl.ids, pl.w, pl.slot_assign);
             if (lane < k) {
-                pl.ids[lane] = id;
-                pl.w[lane] = w;
+                pl.off[lane] = lane;
+                pl.assign_tok[lane] = 0;
             }
-            wave_lds_order();
-            plan_wave(pl, A, k, lane);
+            if (lane == 0) {
+                pl.n_e = k;
+                pl.off[k] = k;
+            }
         }
     } else {
         for (int t = wave; t < T; t += FW) {
@@ -769,55 +702,47 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
 
 static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// h and y follow the workspace header, which holds the barrier words, the tickets and
+// the status word (the state a call leaves for the next).
 struct FusedWs {
-    size_t h, y, tickets, bar, status, total;
+    size_t h, y, total;
 };
 
 static FusedWs fused_ws(int T, int E, int k, const OomFp8Record& g) {
     FusedWs w;
     size_t A = (size_t)T * k;
-    w.h = 0;
-    w.y = al256(A * (size_t)g.inter * sizeof(float));
-    w.tickets = w.y + al256(A * (size_t)g.hidden * sizeof(float));
-    w.bar = w.tickets + (size_t)cdiv(g.hidden, FD_R) * TICKET_STRIDE * sizeof(uint32_t);
-    w.status = w.bar + (2 * BAR_GROUPS + 1) * BAR_STRIDE * sizeof(uint32_t);
-    w.total = w.status + 256;
+    w.h = WS_HEADER;
+    w.y = w.h + al256(A * (size_t)g.inter * sizeof(float));
+    w.total = w.y + al256(A * (size_t)g.hidden * sizeof(float));
     return w;
-}
-
-// Bytes of a record up to the end of its last part (the span its buffer resource covers).
-static int64_t record_span(const OomFp8Record& g) {
-    const int64_t nbg = cdiv(g.inter, 128) * cdiv(g.hidden, 128) * 4;
-    return std::max({g.gate_weight + g.inter * g.hidden, g.gate_scale + nbg, g.up_weight + g.inter * g.hidden,
-                     g.up_scale + nbg, g.down_weight + g.hidden * g.inter, g.down_scale + nbg});
 }
 
 bool fused_supported(int T, int E, int k, const OomFp8Record& g) {
     return (int64_t)T * k <= F_AMAX && E <= F_EMAX && g.hidden <= F_HMAX && g.inter <= F_IMAX && T <= 64 &&
-           record_span(g) < OOB;
+           record_span(g) < OOB && cdiv(g.hidden, FD_R) <= MAX_TILES;
 }
 
 size_t fused_workspace_size(int T, int E, int k, const OomFp8Record& g) { return fused_ws(T, E, k, g).total; }
 
 // Blocks of the fused kernel that fit on the device at once (all must be resident).
-template <int TG, int DCH, int XDT, int ODT>
+template <int TG, int DCH, int EQ, int XDT, int ODT>
 static int resident_blocks(int dev, size_t lds) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, DCH, XDT, ODT>, 256, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>, 256, lds) !=
         hipSuccess)
         return 0;
     return cus * per;
 }
 
-template <int TG, int DCH, int XDT, int ODT>
+template <int TG, int DCH, int EQ, int XDT, int ODT>
 static int launch_fused_t(const FusedArgs& a, size_t lds, hipStream_t st) {
     static thread_local int cached_dev = -1, cached_blocks = 0;
     static thread_local size_t cached_lds = 0;
     int dev = 0;
     (void)hipGetDevice(&dev);
     if (dev != cached_dev || lds != cached_lds) {
-        cached_blocks = resident_blocks<TG, DCH, XDT, ODT>(dev, lds);
+        cached_blocks = resident_blocks<TG, DCH, EQ, XDT, ODT>(dev, lds);
         cached_dev = dev;
         cached_lds = lds;
     }
@@ -825,7 +750,7 @@ static int launch_fused_t(const FusedArgs& a, size_t lds, hipStream_t st) {
     // never more waves than items (at most min(E, A) experts' worth)
     const int64_t items = (int64_t)std::min(a.E, a.T * a.k) * (cdiv(a.I, TG == 1 ? 1 : FG_R) + cdiv(a.H, FD_R));
     const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, cdiv(items, FW)));
-    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, DCH, XDT, ODT>), dim3(blocks), dim3(256), lds, st, a);
+    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>), dim3(blocks), dim3(256), lds, st, a);
     return launched("oom_moe_decode_fp8");
 }
 
@@ -853,29 +778,39 @@ int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* al
     a.out = out;
     a.h = reinterpret_cast<float*>(base + w.h);
     a.y = reinterpret_cast<float*>(base + w.y);
-    a.tickets = reinterpret_cast<uint32_t*>(base + w.tickets);
-    a.bar = reinterpret_cast<uint32_t*>(base + w.bar);
-    a.status = reinterpret_cast<uint32_t*>(base + w.status);
+    a.tickets = reinterpret_cast<uint32_t*>(base + WS_TICKETS);
+    a.bar = reinterpret_cast<uint32_t*>(base + WS_BAR);
+    a.status = reinterpret_cast<uint32_t*>(base + WS_STATUS);
     a.h_bytes = (int)((size_t)T * k * g.inter * sizeof(float));
     a.rec_bytes = (int)record_span(g);
     const size_t lds = 0;
-#define FUSED_CASE(TG, DCH)                                                                               \
-    if (xdt == OOM_BF16 && odt == OOM_BF16) return launch_fused_t<TG, DCH, OOM_BF16, OOM_BF16>(a, lds, st); \
-    if (xdt == OOM_BF16 && odt == OOM_F32) return launch_fused_t<TG, DCH, OOM_BF16, OOM_F32>(a, lds, st);   \
-    if (xdt == OOM_F32 && odt == OOM_BF16) return launch_fused_t<TG, DCH, OOM_F32, OOM_BF16>(a, lds, st);   \
-    return launch_fused_t<TG, DCH, OOM_F32, OOM_F32>(a, lds, st);
+#define FUSED_CASE(TG, DCH, EQ)                                                                               \
+    if (xdt == OOM_BF16 && odt == OOM_BF16) return launch_fused_t<TG, DCH, EQ, OOM_BF16, OOM_BF16>(a, lds, st); \
+    if (xdt == OOM_BF16 && odt == OOM_F32) return launch_fused_t<TG, DCH, EQ, OOM_BF16, OOM_F32>(a, lds, st);   \
+    if (xdt == OOM_F32 && odt == OOM_BF16) return launch_fused_t<TG, DCH, EQ, OOM_F32, OOM_BF16>(a, lds, st);   \
+    return launch_fused_t<TG, DCH, EQ, OOM_F32, OOM_F32>(a, lds, st);
     // one token routed to at most 2 FW experts: TG 1 with 512-column down chunks for the
     // inter width; otherwise groups of 4 tokens per pass over an item's weights
     if (T == 1 && k <= 2 * FW) {
-        if (g.inter <= 1024) {
-            FUSED_CASE(1, 2)
-        } else if (g.inter <= 1536) {
-            FUSED_CASE(1, 3)
+        if (E <= 128) {
+            if (g.inter <= 1024) {
+                FUSED_CASE(1, 2, 2)
+            } else if (g.inter <= 1536) {
+                FUSED_CASE(1, 3, 2)
+            } else {
+                FUSED_CASE(1, 4, 2)
+            }
         } else {
-            FUSED_CASE(1, 4)
+            if (g.inter <= 1024) {
+                FUSED_CASE(1, 2, 4)
+            } else if (g.inter <= 1536) {
+                FUSED_CASE(1, 3, 4)
+            } else {
+                FUSED_CASE(1, 4, 4)
+            }
         }
     } else {
-        FUSED_CASE(4, 0)
+        FUSED_CASE(4, 0, 4)
     }
 #undef FUSED_CASE
 }

@@ -154,6 +154,90 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, in
     if (lane < k) w_out = w_out / picked;
 }
 
+// route_token_regs's routing of one token (E <= 64 EQ <= 256, k <= 8) without k serial
+// rounds, with the one-token plan in the same pass. Every expert gets a key that orders
+// as the reference's argmax does (larger p first, ties to the lower id): bit 39 set for
+// a real expert, p's bits in 38..8, 255 - id in 7..0. The k-th largest key K comes from
+// a radix descent on ballots: each step keeps a candidate bit if at least k keys reach
+// the candidate, and the descent stops when exactly k do. The picks are the keys >= K:
+// their ballot bits in lane order are the experts in id order (the plan's order), and a
+// pick's rank among the k picks is its pick order. Weights are p / (sum of the picks' p
+// in pick order), as the reference renormalises (crates/oominf-cuda/kernels/ops.cu:230-294).
+// Written to LDS: experts[i] (ids ascending), ids[r] and w[r] (pick order) and
+// slot_assign[r] (the id-order position of pick r). keys and p are k-entry LDS scratch.
+template <int EQ>
+__device__ __forceinline__ void route_select(const float* __restrict__ l, int E, int k, int lane, uint64_t* keys,
+                                             float* p, int* experts, int* ids, float* w, int* slot_assign) {
+    float lv[EQ];
+    float m = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        lv[q] = lane + 64 * q < E ? l[lane + 64 * q] : -INFINITY;
+        m = fmaxf(m, lv[q]);
+    }
+    m = wave_max(m);
+    // the reference's 256-thread block sum: virtual thread lane + 64 q holds expert
+    // lane + 64 q; groups of 32 threads absent here (q >= EQ) add zeros, which leaves
+    // the sum's bits as route_token_regs computes them
+    float ex[EQ], w8[8];
+#pragma unroll
+    for (int g = 0; g < 8; g++) w8[g] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        ex[q] = lane + 64 * q < E ? expf(lv[q] - m) : 0.0f;
+        const float s = sum32_xor_order(0.0f + ex[q]);
+        w8[2 * q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+        w8[2 * q + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+    }
+    const float sum = ((w8[0] + w8[4]) + (w8[2] + w8[6])) + ((w8[1] + w8[5]) + (w8[3] + w8[7]));
+    uint64_t key[EQ];
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        const int e = lane + 64 * q;
+        key[q] = e < E ? (1ull << 39) | ((uint64_t)__float_as_uint(ex[q] / sum) << 8) | (uint64_t)(255 - e) : 0ull;
+    }
+    // radix descent: every real key reaches 1 << 39, so at least E >= k keys do
+    uint64_t kth = 1ull << 39;
+    for (int b = 38; b >= 0; b--) {
+        const uint64_t cand = kth | (1ull << b);
+        int cnt = 0;
+#pragma unroll
+        for (int q = 0; q < EQ; q++) cnt += (int)__builtin_popcountll(__ballot(key[q] >= cand));
+        if (cnt >= k) {
+            kth = cand;
+            if (cnt == k) break;
+        }
+    }
+    // the picks in id order: lane order within q, q ascending (expert lane + 64 q)
+    int base = 0;
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        const uint64_t sel = __ballot(key[q] >= kth);
+        if (key[q] >= kth) {
+            const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
+            keys[pos] = key[q];
+        }
+        base += (int)__builtin_popcountll(sel);
+    }
+    wave_lds_order();
+    const uint64_t mine = lane < k ? keys[lane] : 0ull;
+    int rank = 0;
+    for (int j = 0; j < k; j++) rank += keys[j] > mine;
+    const float pm = __uint_as_float((uint32_t)(mine >> 8) & 0x7fffffffu);
+    if (lane < k) {
+        const int e = 255 - (int)(mine & 255u);
+        experts[lane] = e;
+        ids[rank] = e;
+        slot_assign[rank] = lane;
+        p[rank] = pm;
+    }
+    wave_lds_order();
+    float picked = 0.0f;
+    for (int r = 0; r < k; r++) picked += p[r];
+    if (lane < k) w[rank] = pm / picked;
+}
+
 // Routing-plan buffer (i32) of a step with T tokens, E experts and top k:
 //   [0]                     n_e, the number of distinct experts
 //   [1, 1 + E)              experts: distinct ids ascending, then -1
