@@ -33,7 +33,9 @@
 
 namespace oom {
 
-constexpr int FW = 4;        // waves per block
+constexpr int FW = 4;        // waves per block (more than one token)
+constexpr int FW1 = 8;       // waves per block with one token: one expert slot each
+constexpr int FD1_NP = 8;    // row pairs of a one-token down tile (16 rows)
 constexpr int FG_R = 2;      // gate (and up) rows per gate/up item
 constexpr int FD_R = 8;      // output rows per down item
 constexpr int F_AMAX = 512;  // assignments (T * k) per step
@@ -87,9 +89,10 @@ __device__ __forceinline__ void load16(const void* base, size_t off, float* v) {
 
 struct PlanLds {
     uint64_t recs[F_EMAX];  // all_recs, read once per block
-    uint64_t keys[2 * FW];  // one-token routing scratch (route_select)
-    float p[2 * FW];
+    uint64_t keys[FW1];     // one-token routing scratch (route_select)
+    float p[FW1];
     int n_e;
+    uint32_t claims;        // one token: items of this block claimed so far
     int experts[F_AMAX];
     int off[F_AMAX + 1];
     int assign_tok[F_AMAX];
@@ -390,7 +393,7 @@ __device__ __forceinline__ void gate1_compute(const FusedArgs& a, const PlanLds&
 // 512-column chunk c < DCH; one scale per chunk (the 8 rows share a 128-row block).
 template <int DCH>
 struct Down1 {
-    uint4 w[4][DCH];
+    uint4 w[FD1_NP][DCH];
     float s[DCH];
 };
 
@@ -398,14 +401,14 @@ template <int DCH>
 __device__ __forceinline__ void down1_load(const FusedArgs& a, const PlanLds& pl, int i, int tile, bool valid, int lane,
                                            Down1<DCH>& d) {
     const int H = (int)a.H, I = (int)a.I, nkb = (I + 127) >> 7;
-    const int r0 = valid ? tile * FD_R : 0;
+    const int r0 = valid ? tile * 2 * FD1_NP : 0;
     const __amdgpu_buffer_rsrc_t r = rec_rsrc(pl, valid ? i : 0, valid ? a.rec_bytes : 0);
     const int half = lane >> 5, l = lane & 31;
 #pragma unroll
     for (int c = 0; c < DCH; c++) {
         const int col = c * 512 + l * 16;
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
+        for (int p = 0; p < FD1_NP; p++) {
             const int row = r0 + 2 * p + half;
             d.w[p][c] = ld16(r, row < H && col < I ? (int)a.dw + row * I + col : OOB);
         }
@@ -445,13 +448,13 @@ __device__ __forceinline__ void down1_h(const FusedArgs& a, int as, bool valid, 
     }
 }
 
-// The item's 8 row totals: row pair p's total ends in lanes 8 p .. 8 p + 7 of each half
+// The tile's 16 row totals: row pair p's total ends in lanes 4 p .. 4 p + 3 of each half
 // (lanes 0..31: row 2 p, lanes 32..63: row 2 p + 1 of the tile).
 template <int DCH>
 __device__ __forceinline__ float down1_rows(const Down1<DCH>& d, const float (&hv)[DCH][16], int lane) {
-    float acc[4];
+    float acc[FD1_NP];
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
+    for (int p = 0; p < FD1_NP; p++) {
         float s = 0.0f;
 #pragma unroll
         for (int c = 0; c < DCH; c++) {
@@ -464,7 +467,7 @@ __device__ __forceinline__ float down1_rows(const Down1<DCH>& d, const float (&h
         }
         acc[p] = s;
     }
-    return wave_sum_multi<4, 16>(acc, lane);
+    return wave_sum_multi<FD1_NP, 16>(acc, lane);
 }
 
 // Grid-wide barrier, one arrival per block, in two levels so no counter sees more
@@ -552,7 +555,8 @@ __device__ __forceinline__ void plan_wave(PlanLds& pl, int A, int k, int lane) {
 }
 
 template <int TG, int DCH, int EQ, int XDT, int ODT>
-__global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
+__global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused_kernel(FusedArgs a) {
+    constexpr int WB = TG == 1 ? FW1 : FW;  // waves per block
     __shared__ PlanLds pl;
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -575,6 +579,7 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
             if (lane == 0) {
                 pl.n_e = k;
                 pl.off[k] = k;
+                pl.claims = 0u;
             }
         }
     } else {
@@ -626,52 +631,56 @@ __global__ void __launch_bounds__(256) moe_decode_fused_kernel(FusedArgs a) {
             a.weights[s] = pl.w[s];
         }
     const int n_e = pl.n_e;
-    const int NW = gridDim.x * FW, gwave = blockIdx.x * FW + wave;
+    const int NW = gridDim.x * WB, gwave = blockIdx.x * WB + wave;
     const int tiles_d = (int)((a.H + FD_R - 1) / FD_R), ND = n_e * tiles_d;
     if constexpr (TG == 1) {
         // ---- phase 1, one token: item it = (expert it / I, row it % I); the next item's
         // loads are in flight while the current one is reduced ----
         const int NG = n_e * (int)a.I;
+        // Block b owns items b WB + c % WB + (c / WB) NW (c = 0, 1, ...); its waves claim
+        // them in that order from a counter in LDS, so a wave that gets fewer issue slots
+        // (the second wave of a SIMD) takes fewer items than its partner.
+        auto claim = [&]() -> int {
+            uint32_t c = 0;
+            if (lane == 0) c = __hip_atomic_fetch_add(&pl.claims, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            c = __builtin_amdgcn_readfirstlane(c);
+            return (int)(blockIdx.x * WB + c % WB + (c / WB) * NW);
+        };
         Gate1 w0, w1;
-        gate1_load(a, pl, gwave, NG, lane, w0);
-        // this block's first output tile for two expert slots streams behind the wave's
-        // first gate/up item: block b takes tiles b, b + G, ... for all (<= 8) experts,
-        // wave w the experts w and w + FW
-        const int s0 = wave, s1 = wave + FW, tb0 = blockIdx.x;
-        Down1<DCH> d0, d1;
-        down1_load<DCH>(a, pl, s0, tb0, s0 < n_e && tb0 < tiles_d, lane, d0);
-        down1_load<DCH>(a, pl, s1, tb0, s1 < n_e && tb0 < tiles_d, lane, d1);
-        for (int it = gwave; it < NG; it += 2 * NW) {
-            gate1_load(a, pl, it + NW, NG, lane, w1);
-            gate1_compute<XDT>(a, pl, it, NG, w0, xr, lane);
-            if (it + NW >= NG) break;
-            gate1_load(a, pl, it + 2 * NW, NG, lane, w0);
-            gate1_compute<XDT>(a, pl, it + NW, NG, w1, xr, lane);
+        int it0 = claim();
+        gate1_load(a, pl, it0, NG, lane, w0);
+        // this block's first 16-row output tile of the wave's expert slot (one slot per
+        // wave) streams behind the wave's first gate/up item: block b takes tiles b,
+        // b + G, ... for all (<= 8) experts
+        const int s0 = wave, tb0 = blockIdx.x, tiles1 = (int)((a.H + 2 * FD1_NP - 1) / (2 * FD1_NP));
+        Down1<DCH> d0;
+        down1_load<DCH>(a, pl, s0, tb0, s0 < n_e && tb0 < tiles1, lane, d0);
+        while (it0 < NG) {
+            const int it1 = claim();
+            gate1_load(a, pl, it1, NG, lane, w1);
+            gate1_compute<XDT>(a, pl, it0, NG, w0, xr, lane);
+            if (it1 >= NG) break;
+            it0 = claim();
+            gate1_load(a, pl, it0, NG, lane, w0);
+            gate1_compute<XDT>(a, pl, it1, NG, w1, xr, lane);
         }
         wait_mem();  // this wave's h stores (and loads) are complete before its block arrives
         grid_barrier(a);
-        // ---- phase 2, one token: the slots' h once, then per tile the 8 rows of each
+        // ---- phase 2, one token: the slot's h once, then per tile the 16 rows of each
         // expert into LDS and the slot-order combine by wave 0 ----
-        __shared__ float ylds[2 * FW][FD_R];
-        float h0[DCH][16], h1[DCH][16];
+        __shared__ float ylds[FW1][2 * FD1_NP];
+        float h0[DCH][16];
         down1_h<DCH>(a, pl.off[s0 < n_e ? s0 : 0], s0 < n_e, lane, h0);
-        down1_h<DCH>(a, pl.off[s1 < n_e ? s1 : 0], s1 < n_e, lane, h1);
-        const int prow = 2 * ((lane & 31) >> 3) + (lane >> 5);  // this lane group's row in the tile
-        for (int tb = tb0; tb < tiles_d; tb += gridDim.x) {
-            if (tb != tb0) {
-                down1_load<DCH>(a, pl, s0, tb, s0 < n_e, lane, d0);
-                down1_load<DCH>(a, pl, s1, tb, s1 < n_e, lane, d1);
-            }
-            const float y0 = down1_rows<DCH>(d0, h0, lane), y1 = down1_rows<DCH>(d1, h1, lane);
-            if ((lane & 7) == 0) {
-                ylds[s0][prow] = y0;
-                ylds[s1][prow] = y1;
-            }
+        const int prow = 2 * ((lane & 31) >> 2) + (lane >> 5);  // this lane group's row in the tile
+        for (int tb = tb0; tb < tiles1; tb += gridDim.x) {
+            if (tb != tb0) down1_load<DCH>(a, pl, s0, tb, s0 < n_e, lane, d0);
+            const float y0 = down1_rows<DCH>(d0, h0, lane);
+            if ((lane & 3) == 0) ylds[s0][prow] = y0;
             __syncthreads();
             // out[r] = sum over slots in order of w[s] * y[slot_assign[s]][r]; with one
             // token, assignment i is expert slot i
-            const int r = tb * FD_R + lane;
-            if (wave == 0 && lane < FD_R && r < (int)a.H) {
+            const int r = tb * 2 * FD1_NP + lane;
+            if (wave == 0 && lane < 2 * FD1_NP && r < (int)a.H) {
                 float acc = 0.0f;
                 for (int s = 0; s < k; s++) acc = fmaf(pl.w[s], ylds[pl.slot_assign[s]][lane], acc);
                 store_out<ODT>(a.out, r, acc);
@@ -729,7 +738,8 @@ template <int TG, int DCH, int EQ, int XDT, int ODT>
 static int resident_blocks(int dev, size_t lds) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>, 256, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>,
+                                                     TG == 1 ? 64 * FW1 : 64 * FW, lds) !=
         hipSuccess)
         return 0;
     return cus * per;
@@ -748,9 +758,10 @@ static int launch_fused_t(const FusedArgs& a, size_t lds, hipStream_t st) {
     }
     if (cached_blocks <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
     // never more waves than items (at most min(E, A) experts' worth)
+    const int wb = TG == 1 ? FW1 : FW;
     const int64_t items = (int64_t)std::min(a.E, a.T * a.k) * (cdiv(a.I, TG == 1 ? 1 : FG_R) + cdiv(a.H, FD_R));
-    const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, cdiv(items, FW)));
-    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>), dim3(blocks), dim3(256), lds, st, a);
+    const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, cdiv(items, wb)));
+    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>), dim3(blocks), dim3(64 * wb), lds, st, a);
     return launched("oom_moe_decode_fp8");
 }
 
@@ -789,9 +800,9 @@ int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* al
     if (xdt == OOM_BF16 && odt == OOM_F32) return launch_fused_t<TG, DCH, EQ, OOM_BF16, OOM_F32>(a, lds, st);   \
     if (xdt == OOM_F32 && odt == OOM_BF16) return launch_fused_t<TG, DCH, EQ, OOM_F32, OOM_BF16>(a, lds, st);   \
     return launch_fused_t<TG, DCH, EQ, OOM_F32, OOM_F32>(a, lds, st);
-    // one token routed to at most 2 FW experts: TG 1 with 512-column down chunks for the
+    // one token routed to at most FW1 experts: TG 1 with 512-column down chunks for the
     // inter width; otherwise groups of 4 tokens per pass over an item's weights
-    if (T == 1 && k <= 2 * FW) {
+    if (T == 1 && k <= FW1) {
         if (E <= 128) {
             if (g.inter <= 1024) {
                 FUSED_CASE(1, 2, 2)
