@@ -470,54 +470,8 @@ __device__ __forceinline__ float down1_rows(const Down1<DCH>& d, const float (&h
     return wave_sum_multi<FD1_NP, 16>(acc, lane);
 }
 
-// Grid-wide barrier, one arrival per block, in two levels so no counter sees more
-// than 64 arrivals: block b arrives at group b % G (G = 8, one group per XCD under
-// round-robin dispatch); the last of a group arrives at the top counter; the last of
-// those publishes the next generation in every group's generation word, which that
-// group's blocks poll. Counters are reset by their last arrival and generations only
-// grow, so nothing needs clearing between calls. Used once per kernel.
-__device__ __forceinline__ void grid_barrier(const FusedArgs& a) {
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t G = min(gridDim.x, (uint32_t)BAR_GROUPS), g = blockIdx.x % G;
-        const uint32_t n_g = (gridDim.x - g + G - 1) / G;
-        uint32_t* cnt = a.bar + g * BAR_STRIDE;
-        uint32_t* genw = a.bar + (BAR_GROUPS + 1 + g) * BAR_STRIDE;
-        uint32_t* top = a.bar + BAR_GROUPS * BAR_STRIDE;
-        // the generation is read before this block arrives, and waited for: memory
-        // operations to different addresses may be performed out of order, and a read
-        // after the last arrival would see the next generation and wait for one more
-        const uint32_t gen = __hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_mem();
-        const uint32_t target = gen + 1u;
-        bool released = false;
-        if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_g - 1) {
-            __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            wait_mem();
-            if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1) {
-                __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                wait_mem();
-                for (uint32_t q = 0; q < G; q++)
-                    __hip_atomic_store(a.bar + (BAR_GROUPS + 1 + q) * BAR_STRIDE, target, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                wait_mem();
-                released = true;
-            }
-        }
-        if (!released) {
-            uint32_t spins = 0;
-            while ((int32_t)(__hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-                __builtin_amdgcn_s_sleep(4);
-                if (++spins > F_SPIN_LIMIT) {
-                    __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-            }
-        }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    }
-    __syncthreads();
-}
+// Grid-wide barrier over the workspace header's barrier words (stream.hpp). Used once per kernel.
+__device__ __forceinline__ void grid_barrier(const FusedArgs& a) { grid_barrier_words(a.bar, a.status, F_SPIN_LIMIT); }
 
 // The plan of up to 64 slots on one wave, lane s = slot s: ranks by readlane
 // broadcast, no LDS round trips. Reads pl.ids, writes slot_assign, assign_tok, experts,

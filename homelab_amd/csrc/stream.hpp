@@ -113,6 +113,57 @@ __device__ __forceinline__ void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// ---- grid barrier -------------------------------------------------------------------------
+// One arrival per block, in two levels so no counter sees more than 64 arrivals: block b
+// arrives at group b % G (G = 8, one group per XCD under round-robin dispatch); the last
+// of a group arrives at the top counter; the last of those publishes the next generation
+// in every group's generation word, which that group's blocks poll. Counters are reset by
+// their last arrival and generations only grow, so nothing needs clearing between calls.
+// `bar` is the workspace header's barrier area; a wait that gives up sets *status = 1.
+// Every block of the grid must be resident.
+__device__ __forceinline__ void grid_barrier_words(uint32_t* bar, uint32_t* status, uint32_t spin_limit) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t G = min(gridDim.x, (uint32_t)BAR_GROUPS), g = blockIdx.x % G;
+        const uint32_t n_g = (gridDim.x - g + G - 1) / G;
+        uint32_t* cnt = bar + g * BAR_STRIDE;
+        uint32_t* genw = bar + (BAR_GROUPS + 1 + g) * BAR_STRIDE;
+        uint32_t* top = bar + BAR_GROUPS * BAR_STRIDE;
+        // the generation is read before this block arrives, and waited for: memory
+        // operations to different addresses may be performed out of order, and a read
+        // after the last arrival would see the next generation and wait for one more
+        const uint32_t gen = __hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_mem();
+        const uint32_t target = gen + 1u;
+        bool released = false;
+        if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_g - 1) {
+            __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wait_mem();
+            if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1) {
+                __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wait_mem();
+                for (uint32_t q = 0; q < G; q++)
+                    __hip_atomic_store(bar + (BAR_GROUPS + 1 + q) * BAR_STRIDE, target, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                wait_mem();
+                released = true;
+            }
+        }
+        if (!released) {
+            uint32_t spins = 0;
+            while ((int32_t)(__hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+                __builtin_amdgcn_s_sleep(4);
+                if (++spins > spin_limit) {
+                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+    __syncthreads();
+}
+
 // ---- host -------------------------------------------------------------------------------
 
 // Bytes of a record up to the end of its last part (the span a buffer resource covers).
