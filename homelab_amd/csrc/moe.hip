@@ -315,6 +315,12 @@ size_t fused_workspace_size(int T, int E, int k, const OomFp8Record& g);
 int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* all_recs, int T, int E, int k,
                  const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st);
 
+// The one-launch bf16-MFMA path for 2..16 tokens (moe_batch.hip) and its workspace.
+bool batch_supported(int T, int E, int k, const OomFp8Record& g, int xdt, const void* x);
+size_t batch_workspace_size(int T, int k, const OomFp8Record& g);
+int launch_batch(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
+                 const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st);
+
 // Workspace of the multi-launch path of oom_moe_decode_fp8: plan | recs | h | y.
 struct DecodeWs {
     size_t plan, recs, h, y, total;
@@ -371,7 +377,8 @@ extern "C" int oom_moe_combine_slots(const float* y, const int32_t* slot_assign,
 
 extern "C" size_t oom_moe_decode_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo) {
     if (!geo || T < 1 || E < 1 || k < 1) return 0;
-    return std::max(oom::decode_ws(T, E, k, *geo).total, oom::fused_workspace_size(T, E, k, *geo));
+    return std::max({oom::decode_ws(T, E, k, *geo).total, oom::fused_workspace_size(T, E, k, *geo),
+                     oom::batch_workspace_size(T, k, *geo)});
 }
 
 extern "C" int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T,
@@ -389,6 +396,8 @@ extern "C" int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtyp
     if (!ws || ws_bytes < oom_moe_decode_fp8_workspace_size(T, E, k, geo))
         return fail(OOM_ERR_WORKSPACE, "oom_moe_decode_fp8: workspace smaller than oom_moe_decode_fp8_workspace_size()");
     OOM_REQUIRE(aligned(ws, 256), "oom_moe_decode_fp8: workspace must be 256-byte aligned");
+    if (batch_supported(T, E, k, *geo, x_dtype, x))
+        return launch_batch(logits, x, all_recs, T, E, k, *geo, ids, weights, out, out_dtype, ws, as_stream(stream));
     if (fused_supported(T, E, k, *geo))
         return launch_fused(logits, x, x_dtype, all_recs, T, E, k, *geo, ids, weights, out, out_dtype, ws,
                             as_stream(stream));

@@ -1,0 +1,462 @@
+// Decode MoE FFN step for a small batch (2..16 tokens, bf16 activations) on bf16 MFMA in
+// one persistent kernel: router top-k, routing plan, gate/up + SwiGLU, one grid barrier,
+// down projection, a second grid barrier and the slot-order combine (the routed part of
+// crates/oominf-models-qwen/src/moe.rs:290-366; arithmetic of
+// crates/oominf-cuda/kernels/moe.cu:52-164).
+//
+// With 16 tokens the routed experts' multiply-adds (16 x 8 x 3 x 4096 x 1536) outgrow the
+// vector ALUs, so the products run on v_mfma_f32_16x16x32_bf16: e4m3 weights convert to
+// bf16 exactly, bf16 activations are exact, the products are exact in fp32 and sum in
+// fp32, as the reference's fp32 multiply-adds do (in another order).
+//
+//  * Every block routes all tokens (one wave per token) and plans into LDS, and stages
+//    the tokens' activations in LDS (bf16 rows, padded so the 16 rows start in different
+//    banks). The workspace header's barrier words are the only state kept between calls.
+//  * Phase 1: item = (expert, 8 intermediate rows). The MFMA A tile stacks the 8 gate rows
+//    over the 8 up rows (lane l: row l % 16, 32 bytes of each 128-column K step), B is the
+//    expert's tokens (column n = assignment n of the expert). A K step is 4 MFMAs whose sum
+//    is scaled by the rows' 128 x 128 block scale before it joins the accumulator; the
+//    wave's next K steps (B_DEPTH of them) are in flight meanwhile. At the item's end a
+//    lane swap meets gate and up: h = silu(g) * u, stored per token (16 bytes per lane).
+//  * A grid barrier (every block resident).
+//  * Phase 2: item = (expert, 16 output rows); block b takes a contiguous range of items,
+//    so it serves one or two experts: it stages that expert's h in LDS as h ~ hi + lo, two
+//    bf16 terms (lo = bf16(h - hi): 16 significant bits, relative error <= 2^-16), and its
+//    waves take the expert's row tiles. A K step is 8 MFMAs (hi and lo). y rows go out per
+//    assignment with no wait; the first K steps of the block's first tiles load before the
+//    barrier.
+//  * A second grid barrier, then the combine: out[t] = sum over t's slots, in slot order,
+//    of w y, one lane per 4 rows of a token.
+// h and y move between blocks with device-coherent (sc1) stores and loads.
+#include "router.hpp"
+#include "stream.hpp"
+
+namespace oom {
+
+constexpr int B_W = 8;             // waves per block
+constexpr int B_T = 16;            // tokens: one MFMA column tile
+constexpr int B_KMAX = 8;          // router top-k
+constexpr int B_AMAX = B_T * B_KMAX;
+constexpr int B_HMAX = 4096;
+constexpr int B_IMAX = 2048;
+constexpr int B_DEPTH = 8;         // K steps in flight per wave
+constexpr int B_XS = B_HMAX + 8;   // LDS row stride (bf16) of the activations
+constexpr int B_HS = B_IMAX + 8;   // LDS row stride (bf16) of h
+constexpr int B_TILE = 16;         // output rows of a phase-2 item
+constexpr uint32_t B_SPIN = 1u << 22;
+
+typedef __bf16 bbf16x8 __attribute__((ext_vector_type(8)));
+typedef float bf32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t bu32x4 __attribute__((ext_vector_type(4)));
+
+struct BArgs {
+    const float* logits;
+    const uint16_t* x;  // bf16 [T, H]
+    const uint64_t* all_recs;
+    int T, E, k, H, I;
+    int gw, gs, uw, us, dw, ds;  // record part offsets
+    int rec_bytes;               // bytes of a record up to the end of its last part
+    int32_t* ids;
+    float* weights;
+    void* out;
+    float* h;  // [A, I]
+    float* y;  // [A, H]
+    uint32_t* hdr;
+};
+
+struct BLds {
+    uint64_t recs[256];
+    int ids[B_AMAX];
+    float w[B_AMAX];
+    int sorted[B_AMAX];
+    int experts[B_AMAX];
+    int off[B_AMAX + 1];
+    int assign_tok[B_AMAX];
+    int slot_assign[B_AMAX];
+    int n_e;
+    union {
+        uint16_t x[B_T * B_XS];       // phase 1: the tokens' activations, bf16
+        uint16_t hh[2][B_T * B_HS];   // phase 2: the staged expert's h, hi and lo bf16 terms
+    } u;
+};
+
+// One K step of a wave: 32 bytes of this lane's A row and the row's block scale.
+struct KStep {
+    uint4 w[2];
+    float s;
+};
+
+// 8 e4m3 weights (two words) as a bf16 MFMA operand, exactly.
+__device__ __forceinline__ bbf16x8 e4m3x8_bf16(uint32_t w0, uint32_t w1) {
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+    const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+    const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+    return bbf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ bbf16x8 lds_bf16x8(const uint16_t* p) {
+    return __builtin_bit_cast(bbf16x8, *reinterpret_cast<const uint4*>(p));
+}
+
+// 16 bytes of four floats with a device-coherent store (zeros-cost resource check).
+__device__ __forceinline__ void st_dev16(__amdgpu_buffer_rsrc_t r, int off, const float (&v)[4]) {
+    const bu32x4 d = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(d, r, off, 0, BUF_SC1);
+}
+
+// ---- phase 1: gate/up ------------------------------------------------------------------
+
+// K step ks of item it (slot it / nrt, intermediate rows 8 (it % nrt) ..): lane l takes
+// row m = l % 16 (gate row j0 + m for m < 8, up row j0 + m - 8 otherwise) and bytes
+// 128 ks + 32 (l / 16) .. + 32, and the block scale of its output rows; zeros past the
+// item list, inter or hidden.
+__device__ __forceinline__ void gu_load(const BArgs& a, const BLds& L, int it, int ks, bool valid, int nrt, int lane,
+                                        KStep& t) {
+    const int i = valid ? it / nrt : 0, rt = valid ? it - i * nrt : 0;
+    const int m = lane & 15, kq = lane >> 4;
+    const int j = rt * 8 + (m & 7);
+    const bool up = m >= 8;
+    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(L.recs[L.experts[i]], valid ? a.rec_bytes : 0);
+    const int col = ks * 128 + 32 * kq;
+    const int base = (up ? a.uw : a.gw) + j * a.H + col;
+    const bool rowok = j < a.I;
+    t.w[0] = ld16(r, rowok && col < a.H ? base : OOB);
+    t.w[1] = ld16(r, rowok && col + 16 < a.H ? base + 16 : OOB);
+    // the scale multiplies this lane's outputs, rows 4 (l / 16) + e: gate rows in lanes
+    // 0..31, up rows in 32..63 (the item's 8 rows share one 128-row block)
+    const int nkb = (a.H + 127) >> 7, j0 = rt * 8;
+    t.s = ldf(r, j0 < a.I && ks * 128 < a.H ? (lane >= 32 ? a.us : a.gs) + ((j0 >> 7) * nkb + ks) * 4 : OOB);
+}
+
+// c += scale * (A . B) over the K step: 4 MFMAs, B = the tokens' activations at the same
+// 32 columns per lane group (column n: assignment a0 + n; past nb the first one's).
+__device__ __forceinline__ void gu_mfma(const BLds& L, const KStep& t, int ks, int a0, int nb, int lane, bf32x4& c) {
+    const int kq = lane >> 4, n = lane & 15;
+    const int tok = L.assign_tok[a0 + (n < nb ? n : 0)];
+    const uint16_t* xr = &L.u.x[tok * B_XS + ks * 128 + 32 * kq];
+    const uint32_t wd[8] = {t.w[0].x, t.w[0].y, t.w[0].z, t.w[0].w, t.w[1].x, t.w[1].y, t.w[1].z, t.w[1].w};
+    bf32x4 cs = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int mm = 0; mm < 4; mm++)
+        cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_bf16(wd[2 * mm], wd[2 * mm + 1]), lds_bf16x8(xr + 8 * mm),
+                                                     cs, 0, 0, 0);
+#pragma unroll
+    for (int e = 0; e < 4; e++) c[e] = fmaf(cs[e], t.s, c[e]);
+}
+
+// End of item (slot i, rows j0 ..): lane l holds rows 4 (l / 16) + e of column n = l % 16;
+// rows 0..7 (lanes 0..31) are gate, 8..15 (lanes 32..63) up. h = silu(g) * u in lanes
+// 0..31 (v_permlane32_swap brings the up value), 4 consecutive rows per lane.
+__device__ __forceinline__ void gu_store(const BArgs& a, __amdgpu_buffer_rsrc_t hr, int j0, int a0, int nb,
+                                         int lane, const bf32x4& c) {
+    float hv[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(c[e]), __float_as_uint(c[e]), false, false);
+        hv[e] = siluf(c[e]) * __uint_as_float(r[1]);
+    }
+    const int n = lane & 15, j = j0 + 4 * (lane >> 4);
+    if (lane < 32 && n < nb && j < a.I) st_dev16(hr, ((a0 + n) * a.I + j) * 4, hv);
+}
+
+// ---- phase 2: down ---------------------------------------------------------------------
+
+// K step ks of output tile r0 of slot i: lane l takes row r0 + l % 16, bytes
+// 128 ks + 32 (l / 16) .. + 32 of it; the tile's block scale.
+__device__ __forceinline__ void dn_load(const BArgs& a, const BLds& L, int i, int r0, int ks, bool valid, int lane,
+                                        KStep& t) {
+    const int kq = lane >> 4, row = r0 + (lane & 15);
+    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(L.recs[L.experts[valid ? i : 0]], valid ? a.rec_bytes : 0);
+    const int col = ks * 128 + 32 * kq;
+    const int base = a.dw + row * a.I + col;
+    const bool rowok = row < a.H;
+    t.w[0] = ld16(r, rowok && col < a.I ? base : OOB);
+    t.w[1] = ld16(r, rowok && col + 16 < a.I ? base + 16 : OOB);
+    const int nkb = (a.I + 127) >> 7;
+    t.s = ldf(r, r0 < a.H && ks * 128 < a.I ? a.ds + ((r0 >> 7) * nkb + ks) * 4 : OOB);
+}
+
+__device__ __forceinline__ void dn_mfma(const BLds& L, const KStep& t, int ks, int lane, bf32x4& c) {
+    const int kq = lane >> 4, n = lane & 15;
+    const uint16_t* hi = &L.u.hh[0][n * B_HS + ks * 128 + 32 * kq];
+    const uint16_t* lo = &L.u.hh[1][n * B_HS + ks * 128 + 32 * kq];
+    const uint32_t wd[8] = {t.w[0].x, t.w[0].y, t.w[0].z, t.w[0].w, t.w[1].x, t.w[1].y, t.w[1].z, t.w[1].w};
+    bf32x4 cs = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int mm = 0; mm < 4; mm++) {
+        const bbf16x8 av = e4m3x8_bf16(wd[2 * mm], wd[2 * mm + 1]);
+        cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, lds_bf16x8(hi + 8 * mm), cs, 0, 0, 0);
+        cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, lds_bf16x8(lo + 8 * mm), cs, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) c[e] = fmaf(cs[e], t.s, c[e]);
+}
+
+template <int ODT>
+__global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
+    __shared__ BLds L;
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int T = a.T, E = a.E, k = a.k, A = T * k, H = a.H, I = a.I;
+    uint32_t* const status = a.hdr + WS_STATUS / 4;
+    // ---- set-up: record table; activations (thread tid: columns 8 tid .. + 8 of every
+    // token row, zeros past T and H) load while the router runs ----
+    if (tid < E) L.recs[tid] = a.all_recs[tid];
+    {
+        const int col = tid * 8;
+        uint4 v[B_T];
+#pragma unroll
+        for (int u = 0; u < B_T; u++)
+            v[u] = u < T && col < H ? *reinterpret_cast<const uint4*>(a.x + (size_t)u * H + col) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < B_T; u++) *reinterpret_cast<uint4*>(&L.u.x[u * B_XS + col]) = v[u];
+    }
+    for (int t = wave; t < T; t += B_W) {
+        int id = 0;
+        float wt = 0.0f;
+        route_token_regs(a.logits + (size_t)t * E, E, k, lane, id, wt);
+        if (lane < k) {
+            L.ids[t * k + lane] = id;
+            L.w[t * k + lane] = wt;
+        }
+    }
+    __syncthreads();
+    // plan: slots sorted by (expert, slot), experts in id order
+    for (int s = tid; s < A; s += 64 * B_W) {
+        const int e = L.ids[s];
+        int pos = 0;
+        for (int s2 = 0; s2 < A; s2++) {
+            const int e2 = L.ids[s2];
+            pos += (e2 < e) || (e2 == e && s2 < s);
+        }
+        L.sorted[pos] = e;
+        L.slot_assign[s] = pos;
+        L.assign_tok[pos] = s / k;
+    }
+    __syncthreads();
+    for (int p = tid; p < A; p += 64 * B_W) {
+        if (p == 0 || L.sorted[p - 1] != L.sorted[p]) {
+            int idx = 0;
+            for (int q = 1; q <= p; q++) idx += L.sorted[q - 1] != L.sorted[q];
+            L.experts[idx] = L.sorted[p];
+            L.off[idx] = p;
+        }
+        if (p == A - 1) {
+            int n = 1;
+            for (int q = 1; q < A; q++) n += L.sorted[q - 1] != L.sorted[q];
+            L.n_e = n;
+            L.off[n] = A;
+        }
+    }
+    __syncthreads();
+    if (blockIdx.x == 0)
+        for (int s = tid; s < A; s += 64 * B_W) {
+            a.ids[s] = L.ids[s];
+            a.weights[s] = L.w[s];
+        }
+    const int n_e = L.n_e;
+    const int NW = gridDim.x * B_W, gw = blockIdx.x * B_W + wave;
+    const int nksH = (H + 127) >> 7, nksI = (I + 127) >> 7;
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, A * I * 4, BUF_FLAGS);
+    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, A * H * 4, BUF_FLAGS);
+    // ---- phase 1: my items gw, gw + NW, ...; K step q = (my item q / nksH, step q % nksH) ----
+    {
+        const int nrt = (I + 7) >> 3, NG = n_e * nrt;
+        const int mine = gw < NG ? (NG - gw + NW - 1) / NW : 0, nq = mine * nksH;
+        KStep ring[B_DEPTH];
+#pragma unroll
+        for (int d = 0; d < B_DEPTH; d++) {
+            const int n = d / nksH, ks = d - n * nksH;
+            gu_load(a, L, gw + n * NW, ks, d < nq, nrt, lane, ring[d]);
+        }
+        bf32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q0 = 0; q0 < nq; q0 += B_DEPTH) {
+#pragma unroll
+            for (int d = 0; d < B_DEPTH; d++) {
+                const int q = q0 + d, n = q / nksH, ks = q - n * nksH;
+                const int it = gw + n * NW, i = it / nrt, j0 = (it - i * nrt) * 8;
+                const int a0 = L.off[q < nq ? i : 0], nb = L.off[(q < nq ? i : 0) + 1] - a0;
+                gu_mfma(L, ring[d], ks, a0, nb, lane, c);
+                const int qn = q + B_DEPTH, nn = qn / nksH, ksn = qn - nn * nksH;
+                gu_load(a, L, gw + nn * NW, ksn, qn < nq, nrt, lane, ring[d]);
+                if (ks == nksH - 1) {
+                    if (q < nq) gu_store(a, hr, j0, a0, nb, lane, c);
+                    c = bf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+        }
+    }
+    // ---- phase 2: this block's items (slot, 16-row tile) first .. last, slot-major, in
+    // runs of one slot; the first run's first K steps load before the barrier ----
+    const int ntile = (H + B_TILE - 1) / B_TILE, ND = n_e * ntile;
+    const int per = (ND + gridDim.x - 1) / gridDim.x;
+    const int first = min(ND, (int)blockIdx.x * per), last = min(ND, first + per);
+    int r0 = first, i = 0, t0 = 0, t1 = 0, nq = 0;
+    KStep ring[B_DEPTH];
+    // run at r0: slot i, tiles t0 .. t1; this wave's tiles t0 + wave, t0 + wave + B_W, ...
+    // and its K steps q = (tile q / nksI, step q % nksI), the first B_DEPTH of them issued
+    auto start_run = [&]() {
+        const bool any = r0 < last;
+        i = any ? r0 / ntile : 0;
+        t0 = any ? r0 - i * ntile : 0;
+        t1 = any ? min(ntile, t0 + (last - r0)) : 0;
+        nq = t0 + wave < t1 ? (t1 - t0 - wave + B_W - 1) / B_W * nksI : 0;
+#pragma unroll
+        for (int d = 0; d < B_DEPTH; d++) {
+            const int n = d / nksI, ks = d - n * nksI;
+            dn_load(a, L, i, (t0 + wave + n * B_W) * B_TILE, ks, d < nq, lane, ring[d]);
+        }
+    };
+    start_run();
+    wait_mem();  // this wave's h stores are complete before its block arrives
+    grid_barrier_words(a.hdr + WS_BAR / 4, status, B_SPIN);
+    while (r0 < last) {
+        // stage the slot's h: thread tid takes columns 4 tid .. + 4 of every assignment
+        // (zeros past nb and I), all loads in flight before the first conversion
+        {
+            const int a0 = L.off[i], nb = L.off[i + 1] - a0, col = tid * 4;
+            bu32x4 v[B_T];
+#pragma unroll
+            for (int n = 0; n < B_T; n++)
+                v[n] = __builtin_amdgcn_raw_buffer_load_b128(hr, n < nb && col < I ? ((a0 + n) * I + col) * 4 : OOB, 0,
+                                                             BUF_SC1);
+#pragma unroll
+            for (int n = 0; n < B_T; n++) {
+                uint16_t hi[4], lo[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float f = __uint_as_float(v[n][e]);
+                    hi[e] = f32_to_bf16(f);
+                    lo[e] = f32_to_bf16(f - bf16_to_f32(hi[e]));
+                }
+                *reinterpret_cast<uint2*>(&L.u.hh[0][n * B_HS + col]) =
+                    make_uint2(hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16);
+                *reinterpret_cast<uint2*>(&L.u.hh[1][n * B_HS + col]) =
+                    make_uint2(lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16);
+            }
+        }
+        __syncthreads();
+        const int a0 = L.off[i], nb = L.off[i + 1] - a0;
+        bf32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q0 = 0; q0 < nq; q0 += B_DEPTH) {
+#pragma unroll
+            for (int d = 0; d < B_DEPTH; d++) {
+                const int q = q0 + d, n = q / nksI, ks = q - n * nksI;
+                const int tile = t0 + wave + n * B_W;
+                dn_mfma(L, ring[d], ks, lane, c);
+                const int qn = q + B_DEPTH, nn = qn / nksI, ksn = qn - nn * nksI;
+                dn_load(a, L, i, (t0 + wave + nn * B_W) * B_TILE, ksn, qn < nq, lane, ring[d]);
+                if (ks == nksI - 1) {
+                    // y rows tile * 16 + 4 (l / 16) + e of assignment a0 + l % 16
+                    const int n2 = lane & 15, row = tile * B_TILE + 4 * (lane >> 4);
+                    const float yv[4] = {c[0], c[1], c[2], c[3]};
+                    if (q < nq && n2 < nb && row < H) st_dev16(yr, ((a0 + n2) * H + row) * 4, yv);
+                    c = bf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+        }
+        r0 += t1 - t0;
+        __syncthreads();  // every wave is done with this run's h before the next is staged
+        start_run();
+    }
+    // ---- combine: out[t][r .. r + 4] = sum over the token's slots, in slot order, of w y;
+    // one lane per 4 rows of a token, the slots' y loads all in flight ----
+    wait_mem();
+    grid_barrier_words(a.hdr + WS_BAR / 4, status, B_SPIN);
+    const int nq4 = H >> 2;
+    for (int g = gw * 64 + lane; g < T * nq4; g += NW * 64) {
+        const int t = g / nq4, r = (g - t * nq4) * 4;
+        bu32x4 yv[B_KMAX];
+#pragma unroll
+        for (int s = 0; s < B_KMAX; s++)
+            yv[s] = __builtin_amdgcn_raw_buffer_load_b128(
+                yr, s < k ? (L.slot_assign[t * k + s] * H + r) * 4 : OOB, 0, BUF_SC1);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < B_KMAX; s++)
+            if (s < k)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] = fmaf(L.w[t * k + s], __uint_as_float(yv[s][e]), acc[e]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) store_out<ODT>(a.out, (size_t)t * H + r + e, acc[e]);
+    }
+}
+
+// ---- host side -----------------------------------------------------------------------
+
+struct BWs {
+    size_t h, y, total;
+};
+
+static BWs batch_ws(int T, int k, const OomFp8Record& g) {
+    const size_t A = (size_t)T * k;
+    BWs w;
+    w.h = WS_HEADER;
+    w.y = w.h + ((A * g.inter * sizeof(float) + 255) & ~size_t(255));
+    w.total = w.y + ((A * g.hidden * sizeof(float) + 255) & ~size_t(255));
+    return w;
+}
+
+template <int ODT>
+static int batch_grid() {
+    static thread_local int cached_dev = -1, cached = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (dev != cached_dev) {
+        int cus = 0, per = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_batch_kernel<ODT>, 64 * B_W, 0) != hipSuccess)
+            return 0;
+        cached = cus * per;
+        cached_dev = dev;
+    }
+    return cached;
+}
+
+// Widths a multiple of 16 keep every 16-byte access inside its row; x 16-byte aligned.
+bool batch_supported(int T, int E, int k, const OomFp8Record& g, int xdt, const void* x) {
+    return T >= 2 && T <= B_T && k <= B_KMAX && E <= 256 && xdt == OOM_BF16 && g.hidden <= B_HMAX &&
+           g.inter <= B_IMAX && g.hidden % 16 == 0 && g.inter % 16 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+           record_span(g) < OOB &&
+           (int64_t)T * k * std::max(g.hidden, g.inter) * 4 < OOB;
+}
+
+size_t batch_workspace_size(int T, int k, const OomFp8Record& g) { return batch_ws(T, k, g).total; }
+
+int launch_batch(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
+                 const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st) {
+    const BWs w = batch_ws(T, k, g);
+    uint8_t* base = reinterpret_cast<uint8_t*>(ws);
+    BArgs a;
+    a.logits = logits;
+    a.x = reinterpret_cast<const uint16_t*>(x);
+    a.all_recs = all_recs;
+    a.T = T;
+    a.E = E;
+    a.k = k;
+    a.H = (int)g.hidden;
+    a.I = (int)g.inter;
+    a.gw = (int)g.gate_weight;
+    a.gs = (int)g.gate_scale;
+    a.uw = (int)g.up_weight;
+    a.us = (int)g.up_scale;
+    a.dw = (int)g.down_weight;
+    a.ds = (int)g.down_scale;
+    a.rec_bytes = (int)record_span(g);
+    a.ids = ids;
+    a.weights = weights;
+    a.out = out;
+    a.h = reinterpret_cast<float*>(base + w.h);
+    a.y = reinterpret_cast<float*>(base + w.y);
+    a.hdr = reinterpret_cast<uint32_t*>(base);
+    const int grid = odt == OOM_BF16 ? batch_grid<OOM_BF16>() : batch_grid<OOM_F32>();
+    if (grid <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
+    if (odt == OOM_BF16)
+        hipLaunchKernelGGL(moe_batch_kernel<OOM_BF16>, dim3(grid), dim3(64 * B_W), 0, st, a);
+    else
+        hipLaunchKernelGGL(moe_batch_kernel<OOM_F32>, dim3(grid), dim3(64 * B_W), 0, st, a);
+    return launched("oom_moe_decode_fp8");
+}
+
+}  // namespace oom
