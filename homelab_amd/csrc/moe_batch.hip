@@ -33,13 +33,13 @@
 
 namespace oom {
 
-constexpr int B_W = 8;             // waves per block
+constexpr int B_W = 8;             // waves per block: two per SIMD
 constexpr int B_T = 16;            // tokens: one MFMA column tile
 constexpr int B_KMAX = 8;          // router top-k
 constexpr int B_AMAX = B_T * B_KMAX;
 constexpr int B_HMAX = 4096;
 constexpr int B_IMAX = 2048;
-constexpr int B_DEPTH = 8;         // K steps in flight per wave
+constexpr int B_DEPTH = 8;         // K steps in flight per wave (3 loads each)
 constexpr int B_XS = B_HMAX + 8;   // LDS row stride (bf16) of the activations
 constexpr int B_HS = B_IMAX + 8;   // LDS row stride (bf16) of h
 constexpr int B_TILE = 16;         // output rows of a phase-2 item
@@ -64,21 +64,29 @@ struct BArgs {
     uint32_t* hdr;
 };
 
-struct BLds {
+// The activation / h rows come first: their 16-byte LDS reads and writes need 16-byte
+// aligned addresses (row strides are multiples of 16 bytes).
+struct alignas(16) BLds {
+    union {
+        uint16_t x[B_T * B_XS];       // phase 1: the tokens' activations, bf16
+        uint16_t hh[2][B_T * B_HS];   // phase 2: the staged expert's h, hi and lo bf16 terms
+    } u;
     uint64_t recs[256];
+    uint64_t keys[B_W][B_KMAX];  // routing scratch of each wave
+    float p[B_W][B_KMAX];
+    uint32_t mask[256];          // tokens routed to each expert, one bit per token
+    int base[256];               // first assignment of each expert
     int ids[B_AMAX];
     float w[B_AMAX];
-    int sorted[B_AMAX];
     int experts[B_AMAX];
     int off[B_AMAX + 1];
     int assign_tok[B_AMAX];
     int slot_assign[B_AMAX];
     int n_e;
-    union {
-        uint16_t x[B_T * B_XS];       // phase 1: the tokens' activations, bf16
-        uint16_t hh[2][B_T * B_HS];   // phase 2: the staged expert's h, hi and lo bf16 terms
-    } u;
 };
+static_assert(offsetof(BLds, u) == 0 && (B_XS * 2) % 16 == 0 && (B_HS * 2) % 16 == 0 &&
+                  (B_T * B_HS * 2) % 16 == 0,
+              "16-byte LDS accesses need aligned rows");
 
 // One K step of a wave: 32 bytes of this lane's A row and the row's block scale.
 struct KStep {
@@ -99,6 +107,13 @@ __device__ __forceinline__ bbf16x8 lds_bf16x8(const uint16_t* p) {
     return __builtin_bit_cast(bbf16x8, *reinterpret_cast<const uint4*>(p));
 }
 
+// v, once the accumulator is computed: an empty asm that takes c and hands back v keeps
+// whatever uses the result after c's producers.
+__device__ __forceinline__ int after(int v, const bf32x4& c) {
+    asm volatile("" : "+v"(v) : "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]));
+    return v;
+}
+
 // 16 bytes of four floats with a device-coherent store (zeros-cost resource check).
 __device__ __forceinline__ void st_dev16(__amdgpu_buffer_rsrc_t r, int off, const float (&v)[4]) {
     const bu32x4 d = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
@@ -107,34 +122,43 @@ __device__ __forceinline__ void st_dev16(__amdgpu_buffer_rsrc_t r, int off, cons
 
 // ---- phase 1: gate/up ------------------------------------------------------------------
 
-// K step ks of item it (slot it / nrt, intermediate rows 8 (it % nrt) ..): lane l takes
-// row m = l % 16 (gate row j0 + m for m < 8, up row j0 + m - 8 otherwise) and bytes
-// 128 ks + 32 (l / 16) .. + 32, and the block scale of its output rows; zeros past the
-// item list, inter or hidden.
-__device__ __forceinline__ void gu_load(const BArgs& a, const BLds& L, int it, int ks, bool valid, int nrt, int lane,
-                                        KStep& t) {
-    const int i = valid ? it / nrt : 0, rt = valid ? it - i * nrt : 0;
-    const int m = lane & 15, kq = lane >> 4;
-    const int j = rt * 8 + (m & 7);
-    const bool up = m >= 8;
-    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(L.recs[L.experts[i]], valid ? a.rec_bytes : 0);
-    const int col = ks * 128 + 32 * kq;
-    const int base = (up ? a.uw : a.gw) + j * a.H + col;
-    const bool rowok = j < a.I;
-    t.w[0] = ld16(r, rowok && col < a.H ? base : OOB);
-    t.w[1] = ld16(r, rowok && col + 16 < a.H ? base + 16 : OOB);
-    // the scale multiplies this lane's outputs, rows 4 (l / 16) + e: gate rows in lanes
-    // 0..31, up rows in 32..63 (the item's 8 rows share one 128-row block)
-    const int nkb = (a.H + 127) >> 7, j0 = rt * 8;
-    t.s = ldf(r, j0 < a.I && ks * 128 < a.H ? (lane >= 32 ? a.us : a.gs) + ((j0 >> 7) * nkb + ks) * 4 : OOB);
+// An item (slot i, intermediate rows j0 .. j0 + 8) as this lane loads it: lane l takes row
+// m = l % 16 (gate row j0 + m for m < 8, up row j0 + m - 8 otherwise), bytes 32 (l / 16)
+// .. + 32 of each 128-column K step, and the block scale of its output rows (rows
+// 4 (l / 16) + e: gate in lanes 0..31, up in 32..63; the 8 rows share a 128-row block).
+// Past the wave's items the record's range is 0, so every load reads zeros.
+struct GuRow {
+    __amdgpu_buffer_rsrc_t r;
+    int roff, soff;
+    bool ok;  // the lane's row exists
+};
+
+__device__ __forceinline__ GuRow gu_row(const BArgs& a, const BLds& L, int it, bool valid, int nrt, int lane) {
+    const int i = valid ? it / nrt : 0, j0 = valid ? (it - i * nrt) * 8 : 0;
+    const int m = lane & 15, j = j0 + (m & 7), nkb = (a.H + 127) >> 7;
+    GuRow g;
+    g.r = uniform_rsrc(L.recs[L.experts[i]], valid ? a.rec_bytes : 0);
+    g.roff = (m >= 8 ? a.uw : a.gw) + j * a.H + 32 * (lane >> 4);
+    g.soff = (lane >= 32 ? a.us : a.gs) + (j0 >> 7) * nkb * 4;
+    g.ok = j < a.I;
+    return g;
 }
 
-// c += scale * (A . B) over the K step: 4 MFMAs, B = the tokens' activations at the same
-// 32 columns per lane group (column n: assignment a0 + n; past nb the first one's).
-__device__ __forceinline__ void gu_mfma(const BLds& L, const KStep& t, int ks, int a0, int nb, int lane, bf32x4& c) {
-    const int kq = lane >> 4, n = lane & 15;
-    const int tok = L.assign_tok[a0 + (n < nb ? n : 0)];
-    const uint16_t* xr = &L.u.x[tok * B_XS + ks * 128 + 32 * kq];
+// K step ks of an item: zeros past inter and hidden.
+// The scale load waits for `dep`, the accumulator that last used the previous scale, so
+// the new scale takes the old one's register.
+__device__ __forceinline__ void gu_issue(const BArgs& a, const GuRow& g, int ks, int lane, const bf32x4& dep, KStep& t) {
+    const int col = ks * 128 + 32 * (lane >> 4), o = g.roff + ks * 128;
+    t.w[0] = ld16(g.r, g.ok && col < a.H ? o : OOB);
+    t.w[1] = ld16(g.r, g.ok && col + 16 < a.H ? o + 16 : OOB);
+    t.s = ldf(g.r, after(g.soff + ks * 4, dep));
+}
+
+// c += scale * (A . B) over a K step: 4 MFMAs; B is the tokens' activations at the same
+// 32 columns per lane group, from the LDS row offset xo (column n: assignment a0 + n,
+// past nb the first one's).
+__device__ __forceinline__ void gu_mfma(const BLds& L, const KStep& t, int xo, bf32x4& c) {
+    const uint16_t* xr = &L.u.x[xo];
     const uint32_t wd[8] = {t.w[0].x, t.w[0].y, t.w[0].z, t.w[0].w, t.w[1].x, t.w[1].y, t.w[1].z, t.w[1].w};
     bf32x4 cs = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -145,7 +169,7 @@ __device__ __forceinline__ void gu_mfma(const BLds& L, const KStep& t, int ks, i
     for (int e = 0; e < 4; e++) c[e] = fmaf(cs[e], t.s, c[e]);
 }
 
-// End of item (slot i, rows j0 ..): lane l holds rows 4 (l / 16) + e of column n = l % 16;
+// End of an item (rows j0 ..): lane l holds rows 4 (l / 16) + e of column n = l % 16;
 // rows 0..7 (lanes 0..31) are gate, 8..15 (lanes 32..63) up. h = silu(g) * u in lanes
 // 0..31 (v_permlane32_swap brings the up value), 4 consecutive rows per lane.
 __device__ __forceinline__ void gu_store(const BArgs& a, __amdgpu_buffer_rsrc_t hr, int j0, int a0, int nb,
@@ -162,25 +186,35 @@ __device__ __forceinline__ void gu_store(const BArgs& a, __amdgpu_buffer_rsrc_t 
 
 // ---- phase 2: down ---------------------------------------------------------------------
 
-// K step ks of output tile r0 of slot i: lane l takes row r0 + l % 16, bytes
-// 128 ks + 32 (l / 16) .. + 32 of it; the tile's block scale.
-__device__ __forceinline__ void dn_load(const BArgs& a, const BLds& L, int i, int r0, int ks, bool valid, int lane,
-                                        KStep& t) {
-    const int kq = lane >> 4, row = r0 + (lane & 15);
-    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(L.recs[L.experts[valid ? i : 0]], valid ? a.rec_bytes : 0);
-    const int col = ks * 128 + 32 * kq;
-    const int base = a.dw + row * a.I + col;
-    const bool rowok = row < a.H;
-    t.w[0] = ld16(r, rowok && col < a.I ? base : OOB);
-    t.w[1] = ld16(r, rowok && col + 16 < a.I ? base + 16 : OOB);
-    const int nkb = (a.I + 127) >> 7;
-    t.s = ldf(r, r0 < a.H && ks * 128 < a.I ? a.ds + ((r0 >> 7) * nkb + ks) * 4 : OOB);
+// Output tile `tile` (rows 16 tile ..) of the run's slot as this lane loads it: row
+// 16 tile + l % 16, bytes 32 (l / 16) .. + 32 of each K step; the tile's block scale.
+struct DnRow {
+    int roff, soff;
+    bool ok;
+};
+
+__device__ __forceinline__ DnRow dn_row(const BArgs& a, int tile, bool valid, int lane) {
+    const int row = tile * B_TILE + (lane & 15), nkb = (a.I + 127) >> 7;
+    DnRow d;
+    d.roff = a.dw + row * a.I + 32 * (lane >> 4);
+    d.soff = a.ds + ((tile * B_TILE) >> 7) * nkb * 4;
+    d.ok = valid && row < a.H;
+    return d;
 }
 
-__device__ __forceinline__ void dn_mfma(const BLds& L, const KStep& t, int ks, int lane, bf32x4& c) {
-    const int kq = lane >> 4, n = lane & 15;
-    const uint16_t* hi = &L.u.hh[0][n * B_HS + ks * 128 + 32 * kq];
-    const uint16_t* lo = &L.u.hh[1][n * B_HS + ks * 128 + 32 * kq];
+__device__ __forceinline__ void dn_issue(const BArgs& a, __amdgpu_buffer_rsrc_t r, const DnRow& d, int ks, int lane,
+                                         const bf32x4& dep, KStep& t) {
+    const int col = ks * 128 + 32 * (lane >> 4), o = d.roff + ks * 128;
+    t.w[0] = ld16(r, d.ok && col < a.I ? o : OOB);
+    t.w[1] = ld16(r, d.ok && col + 16 < a.I ? o + 16 : OOB);
+    t.s = ldf(r, after(d.soff + ks * 4, dep));
+}
+
+// c += scale * (A . (h_hi + h_lo)) over a K step: 8 MFMAs; ho is the LDS offset of
+// column n = l % 16's h row at this lane's 32 columns of the step.
+__device__ __forceinline__ void dn_mfma(const BLds& L, const KStep& t, int ho, bf32x4& c) {
+    const uint16_t* hi = &L.u.hh[0][ho];
+    const uint16_t* lo = &L.u.hh[1][ho];
     const uint32_t wd[8] = {t.w[0].x, t.w[0].y, t.w[0].z, t.w[0].w, t.w[1].x, t.w[1].y, t.w[1].z, t.w[1].w};
     bf32x4 cs = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -193,18 +227,65 @@ __device__ __forceinline__ void dn_mfma(const BLds& L, const KStep& t, int ks, i
     for (int e = 0; e < 4; e++) c[e] = fmaf(cs[e], t.s, c[e]);
 }
 
-template <int ODT>
+// One token's picks from its keys and the k-th key: pick r (in key order) gets ids[r] and
+// w[r] = p / (sum of the picks' p in pick order), as the reference renormalises
+// (crates/oominf-cuda/kernels/ops.cu:230-294); the token's bit joins each pick's mask.
+template <int EQ>
+__device__ __forceinline__ void batch_picks(const uint64_t (&key)[EQ], uint64_t kth, int k, int lane, uint64_t* keys,
+                                            float* p, int* ids, float* w, uint32_t* mask, int t) {
+    int base = 0;
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        const uint64_t sel = __ballot(key[q] >= kth);
+        if (key[q] >= kth) {
+            const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u));
+            keys[pos] = key[q];
+        }
+        base += (int)__builtin_popcountll(sel);
+    }
+    wave_lds_order();
+    const uint64_t mine = lane < k ? keys[lane] : 0ull;
+    int rank = 0;
+    for (int j = 0; j < k; j++) rank += keys[j] > mine;
+    const float pm = __uint_as_float((uint32_t)(mine >> 8) & 0x7fffffffu);
+    const int e = 255 - (int)(mine & 255u);
+    if (lane < k) {
+        ids[rank] = e;
+        p[rank] = pm;
+        __hip_atomic_fetch_or(&mask[e], 1u << t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    wave_lds_order();
+    float picked = 0.0f;
+    for (int r = 0; r < k; r++) picked += p[r];
+    if (lane < k) w[rank] = pm / picked;
+    wave_lds_order();  // keys and p are free for the wave's next token
+}
+
+template <int EQ, int ODT>
 __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     __shared__ BLds L;
+    constexpr int NT = 64 * B_W, TPW = B_T / B_W;  // threads; tokens routed per wave
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int T = a.T, E = a.E, k = a.k, A = T * k, H = a.H, I = a.I;
     uint32_t* const status = a.hdr + WS_STATUS / 4;
-    // ---- set-up: record table; activations (thread tid: columns 8 tid .. + 8 of every
-    // token row, zeros past T and H) load while the router runs ----
+    // ---- set-up: this wave's tokens' logits (t = wave + B_W j) in flight first ----
+    float lv[TPW][EQ];
+#pragma unroll
+    for (int j = 0; j < TPW; j++)
+#pragma unroll
+        for (int q = 0; q < EQ; q++) {
+            const int t = wave + B_W * j, e = lane + 64 * q;
+            lv[j][q] = t < T && e < E ? a.logits[(size_t)t * E + e] : -INFINITY;
+        }
     if (tid < E) L.recs[tid] = a.all_recs[tid];
-    {
-        const int col = tid * 8;
+    L.mask[tid] = 0u;
+    // activations: thread tid takes columns 8 (tid + NT c) .. + 8 of every token row (zeros
+    // past T and H), 16 loads in flight per pass
+#pragma unroll
+    for (int c = 0; c < B_HMAX / 8 / NT; c++) {
+        const int col = (tid + NT * c) * 8;
         uint4 v[B_T];
 #pragma unroll
         for (int u = 0; u < B_T; u++)
@@ -212,46 +293,68 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
 #pragma unroll
         for (int u = 0; u < B_T; u++) *reinterpret_cast<uint4*>(&L.u.x[u * B_XS + col]) = v[u];
     }
-    for (int t = wave; t < T; t += B_W) {
-        int id = 0;
-        float wt = 0.0f;
-        route_token_regs(a.logits + (size_t)t * E, E, k, lane, id, wt);
-        if (lane < k) {
-            L.ids[t * k + lane] = id;
-            L.w[t * k + lane] = wt;
+    __syncthreads();  // masks are zero
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int t = wave + B_W * j;
+        if (t < T) {
+            uint64_t key[EQ];
+            route_keys<EQ>(lv[j], E, lane, key);
+            const uint64_t kth = radix_kth<EQ>(key, k);
+            batch_picks<EQ>(key, kth, k, lane, L.keys[wave], L.p[wave], &L.ids[t * k], &L.w[t * k], L.mask, t);
         }
     }
     __syncthreads();
-    // plan: slots sorted by (expert, slot), experts in id order
-    for (int s = tid; s < A; s += 64 * B_W) {
-        const int e = L.ids[s];
-        int pos = 0;
-        for (int s2 = 0; s2 < A; s2++) {
-            const int e2 = L.ids[s2];
-            pos += (e2 < e) || (e2 == e && s2 < s);
+    // plan: assignments sorted by (expert, slot); expert e's run starts at the count of
+    // assignments to lower ids, and the token order within it is the mask's bit order
+    if (wave == 0) {
+        uint32_t m[4];
+        int c = 0, pr = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = 4 * lane + j;
+            m[j] = e < E ? L.mask[e] : 0u;
+            c += __builtin_popcount(m[j]);
+            pr += m[j] != 0u;
         }
-        L.sorted[pos] = e;
+        int ic = c, ip = pr;  // inclusive scans over lanes
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int tc = __shfl_up(ic, o, 64), tp = __shfl_up(ip, o, 64);
+            if (lane >= o) {
+                ic += tc;
+                ip += tp;
+            }
+        }
+        int bc = ic - c, bp = ip - pr;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = 4 * lane + j;
+            if (e < E) {
+                L.base[e] = bc;
+                if (m[j] != 0u) {
+                    L.experts[bp] = e;
+                    L.off[bp] = bc;
+                    bp++;
+                }
+                bc += __builtin_popcount(m[j]);
+            }
+        }
+        if (lane == 63) {
+            L.n_e = ip;
+            L.off[ip] = ic;
+        }
+    }
+    __syncthreads();
+    for (int s = tid; s < A; s += NT) {
+        const int t = s / k, e = L.ids[s];
+        const int pos = L.base[e] + __builtin_popcount(L.mask[e] & ((1u << t) - 1u));
         L.slot_assign[s] = pos;
-        L.assign_tok[pos] = s / k;
-    }
-    __syncthreads();
-    for (int p = tid; p < A; p += 64 * B_W) {
-        if (p == 0 || L.sorted[p - 1] != L.sorted[p]) {
-            int idx = 0;
-            for (int q = 1; q <= p; q++) idx += L.sorted[q - 1] != L.sorted[q];
-            L.experts[idx] = L.sorted[p];
-            L.off[idx] = p;
-        }
-        if (p == A - 1) {
-            int n = 1;
-            for (int q = 1; q < A; q++) n += L.sorted[q - 1] != L.sorted[q];
-            L.n_e = n;
-            L.off[n] = A;
-        }
+        L.assign_tok[pos] = t;
     }
     __syncthreads();
     if (blockIdx.x == 0)
-        for (int s = tid; s < A; s += 64 * B_W) {
+        for (int s = tid; s < A; s += NT) {
             a.ids[s] = L.ids[s];
             a.weights[s] = L.w[s];
         }
@@ -260,29 +363,49 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const int nksH = (H + 127) >> 7, nksI = (I + 127) >> 7;
     const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, A * I * 4, BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, A * H * 4, BUF_FLAGS);
-    // ---- phase 1: my items gw, gw + NW, ...; K step q = (my item q / nksH, step q % nksH) ----
+    const int m16 = lane & 15, kq = lane >> 4;
+    // ---- phase 1: my items gw + n NW (n < mine), K steps in order; an issue cursor runs
+    // B_DEPTH steps ahead of the consume cursor ----
     {
         const int nrt = (I + 7) >> 3, NG = n_e * nrt;
         const int mine = gw < NG ? (NG - gw + NW - 1) / NW : 0, nq = mine * nksH;
+        int ni = 0, ksi = 0;
+        GuRow gi = gu_row(a, L, gw, 0 < mine, nrt, lane);
+        auto issue = [&](KStep& t, const bf32x4& dep) {
+            gu_issue(a, gi, ksi, lane, dep, t);
+            if (++ksi == nksH) {
+                ksi = 0;
+                ++ni;
+                gi = gu_row(a, L, gw + ni * NW, ni < mine, nrt, lane);
+            }
+        };
         KStep ring[B_DEPTH];
 #pragma unroll
-        for (int d = 0; d < B_DEPTH; d++) {
-            const int n = d / nksH, ks = d - n * nksH;
-            gu_load(a, L, gw + n * NW, ks, d < nq, nrt, lane, ring[d]);
-        }
+        for (int d = 0; d < B_DEPTH; d++) issue(ring[d], bf32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        int nc = 0, ksc = 0, j0 = 0, a0 = 0, nb = 0, xo = 0;
+        auto con_item = [&]() {
+            const bool valid = nc < mine;
+            const int it = gw + nc * NW, i = valid ? it / nrt : 0;
+            j0 = (it - i * nrt) * 8;
+            a0 = L.off[i];
+            nb = L.off[i + 1] - a0;
+            xo = L.assign_tok[a0 + (m16 < nb ? m16 : 0)] * B_XS + 32 * kq;
+        };
+        con_item();
         bf32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+        // every ring slot is consumed and refilled on every step (steps past nq read zeros
+        // and store nothing), so the slots stay in fixed registers across iterations
         for (int q0 = 0; q0 < nq; q0 += B_DEPTH) {
 #pragma unroll
             for (int d = 0; d < B_DEPTH; d++) {
-                const int q = q0 + d, n = q / nksH, ks = q - n * nksH;
-                const int it = gw + n * NW, i = it / nrt, j0 = (it - i * nrt) * 8;
-                const int a0 = L.off[q < nq ? i : 0], nb = L.off[(q < nq ? i : 0) + 1] - a0;
-                gu_mfma(L, ring[d], ks, a0, nb, lane, c);
-                const int qn = q + B_DEPTH, nn = qn / nksH, ksn = qn - nn * nksH;
-                gu_load(a, L, gw + nn * NW, ksn, qn < nq, nrt, lane, ring[d]);
-                if (ks == nksH - 1) {
-                    if (q < nq) gu_store(a, hr, j0, a0, nb, lane, c);
+                gu_mfma(L, ring[d], xo + ksc * 128, c);
+                issue(ring[d], c);
+                if (++ksc == nksH) {
+                    ksc = 0;
+                    if (nc < mine) gu_store(a, hr, j0, a0, nb, lane, c);
                     c = bf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    ++nc;
+                    con_item();
                 }
             }
         }
@@ -292,67 +415,84 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const int ntile = (H + B_TILE - 1) / B_TILE, ND = n_e * ntile;
     const int per = (ND + gridDim.x - 1) / gridDim.x;
     const int first = min(ND, (int)blockIdx.x * per), last = min(ND, first + per);
-    int r0 = first, i = 0, t0 = 0, t1 = 0, nq = 0;
+    int r0 = first, i = 0, t0 = 0, t1 = 0, mt = 0, nq = 0;
+    // the run at r0: slot i, tiles t0 .. t1; this wave's tiles t0 + wave + B_W m (m < mt),
+    // K steps in order, issued B_DEPTH ahead of their use
+    __amdgpu_buffer_rsrc_t rr = uniform_rsrc(0, 0);
+    int mi = 0, ksi = 0;
+    DnRow di = dn_row(a, 0, false, lane);
+    auto issue = [&](KStep& t, const bf32x4& dep) {
+        dn_issue(a, rr, di, ksi, lane, dep, t);
+        if (++ksi == nksI) {
+            ksi = 0;
+            ++mi;
+            di = dn_row(a, t0 + wave + mi * B_W, mi < mt, lane);
+        }
+    };
     KStep ring[B_DEPTH];
-    // run at r0: slot i, tiles t0 .. t1; this wave's tiles t0 + wave, t0 + wave + B_W, ...
-    // and its K steps q = (tile q / nksI, step q % nksI), the first B_DEPTH of them issued
     auto start_run = [&]() {
         const bool any = r0 < last;
         i = any ? r0 / ntile : 0;
         t0 = any ? r0 - i * ntile : 0;
         t1 = any ? min(ntile, t0 + (last - r0)) : 0;
-        nq = t0 + wave < t1 ? (t1 - t0 - wave + B_W - 1) / B_W * nksI : 0;
+        mt = t0 + wave < t1 ? (t1 - t0 - wave + B_W - 1) / B_W : 0;
+        nq = mt * nksI;
+        rr = uniform_rsrc(L.recs[L.experts[i]], any ? a.rec_bytes : 0);
+        mi = 0;
+        ksi = 0;
+        di = dn_row(a, t0 + wave, 0 < mt, lane);
 #pragma unroll
-        for (int d = 0; d < B_DEPTH; d++) {
-            const int n = d / nksI, ks = d - n * nksI;
-            dn_load(a, L, i, (t0 + wave + n * B_W) * B_TILE, ks, d < nq, lane, ring[d]);
-        }
+        for (int d = 0; d < B_DEPTH; d++) issue(ring[d], bf32x4{0.0f, 0.0f, 0.0f, 0.0f});
     };
     start_run();
     wait_mem();  // this wave's h stores are complete before its block arrives
     grid_barrier_words(a.hdr + WS_BAR / 4, status, B_SPIN);
     while (r0 < last) {
-        // stage the slot's h: thread tid takes columns 4 tid .. + 4 of every assignment
-        // (zeros past nb and I), all loads in flight before the first conversion
+        // stage the slot's h: thread tid takes columns 4 (tid + NT c) .. + 4 of every
+        // assignment (zeros past nb and I), 16 loads in flight per pass
         {
-            const int a0 = L.off[i], nb = L.off[i + 1] - a0, col = tid * 4;
-            bu32x4 v[B_T];
+            const int a0 = L.off[i], nb = L.off[i + 1] - a0;
 #pragma unroll
-            for (int n = 0; n < B_T; n++)
-                v[n] = __builtin_amdgcn_raw_buffer_load_b128(hr, n < nb && col < I ? ((a0 + n) * I + col) * 4 : OOB, 0,
-                                                             BUF_SC1);
+            for (int c = 0; c < B_IMAX / 4 / NT; c++) {
+                const int col = (tid + NT * c) * 4;
+                bu32x4 v[B_T];
 #pragma unroll
-            for (int n = 0; n < B_T; n++) {
-                uint16_t hi[4], lo[4];
+                for (int n = 0; n < B_T; n++)
+                    v[n] = __builtin_amdgcn_raw_buffer_load_b128(hr, n < nb && col < I ? ((a0 + n) * I + col) * 4 : OOB,
+                                                                 0, BUF_SC1);
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float f = __uint_as_float(v[n][e]);
-                    hi[e] = f32_to_bf16(f);
-                    lo[e] = f32_to_bf16(f - bf16_to_f32(hi[e]));
+                for (int n = 0; n < B_T; n++) {
+                    uint16_t hi[4], lo[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float f = __uint_as_float(v[n][e]);
+                        hi[e] = f32_to_bf16(f);
+                        lo[e] = f32_to_bf16(f - bf16_to_f32(hi[e]));
+                    }
+                    *reinterpret_cast<uint2*>(&L.u.hh[0][n * B_HS + col]) =
+                        make_uint2(hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16);
+                    *reinterpret_cast<uint2*>(&L.u.hh[1][n * B_HS + col]) =
+                        make_uint2(lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16);
                 }
-                *reinterpret_cast<uint2*>(&L.u.hh[0][n * B_HS + col]) =
-                    make_uint2(hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16);
-                *reinterpret_cast<uint2*>(&L.u.hh[1][n * B_HS + col]) =
-                    make_uint2(lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16);
             }
         }
         __syncthreads();
-        const int a0 = L.off[i], nb = L.off[i + 1] - a0;
+        const int a0 = L.off[i], nb = L.off[i + 1] - a0, ho = m16 * B_HS + 32 * kq;
+        int mc = 0, ksc = 0;
         bf32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int q0 = 0; q0 < nq; q0 += B_DEPTH) {
 #pragma unroll
             for (int d = 0; d < B_DEPTH; d++) {
-                const int q = q0 + d, n = q / nksI, ks = q - n * nksI;
-                const int tile = t0 + wave + n * B_W;
-                dn_mfma(L, ring[d], ks, lane, c);
-                const int qn = q + B_DEPTH, nn = qn / nksI, ksn = qn - nn * nksI;
-                dn_load(a, L, i, (t0 + wave + nn * B_W) * B_TILE, ksn, qn < nq, lane, ring[d]);
-                if (ks == nksI - 1) {
-                    // y rows tile * 16 + 4 (l / 16) + e of assignment a0 + l % 16
-                    const int n2 = lane & 15, row = tile * B_TILE + 4 * (lane >> 4);
+                dn_mfma(L, ring[d], ho + ksc * 128, c);
+                issue(ring[d], c);
+                if (++ksc == nksI) {
+                    // y rows 16 tile + 4 (l / 16) + e of assignment a0 + l % 16
+                    ksc = 0;
+                    const int row = (t0 + wave + mc * B_W) * B_TILE + 4 * kq;
                     const float yv[4] = {c[0], c[1], c[2], c[3]};
-                    if (q < nq && n2 < nb && row < H) st_dev16(yr, ((a0 + n2) * H + row) * 4, yv);
+                    if (mc < mt && m16 < nb && row < H) st_dev16(yr, ((a0 + m16) * H + row) * 4, yv);
                     c = bf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    ++mc;
                 }
             }
         }
@@ -398,7 +538,7 @@ static BWs batch_ws(int T, int k, const OomFp8Record& g) {
     return w;
 }
 
-template <int ODT>
+template <int EQ, int ODT>
 static int batch_grid() {
     static thread_local int cached_dev = -1, cached = 0;
     int dev = 0;
@@ -406,12 +546,20 @@ static int batch_grid() {
     if (dev != cached_dev) {
         int cus = 0, per = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_batch_kernel<ODT>, 64 * B_W, 0) != hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_batch_kernel<EQ, ODT>, 64 * B_W, 0) != hipSuccess)
             return 0;
         cached = cus * per;
         cached_dev = dev;
     }
     return cached;
+}
+
+template <int EQ, int ODT>
+static int launch_batch_t(const BArgs& a, hipStream_t st) {
+    const int grid = batch_grid<EQ, ODT>();
+    if (grid <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
+    hipLaunchKernelGGL((moe_batch_kernel<EQ, ODT>), dim3(grid), dim3(64 * B_W), 0, st, a);
+    return launched("oom_moe_decode_fp8");
 }
 
 // Widths a multiple of 16 keep every 16-byte access inside its row; x 16-byte aligned.
@@ -450,13 +598,8 @@ int launch_batch(const float* logits, const void* x, const uint64_t* all_recs, i
     a.h = reinterpret_cast<float*>(base + w.h);
     a.y = reinterpret_cast<float*>(base + w.y);
     a.hdr = reinterpret_cast<uint32_t*>(base);
-    const int grid = odt == OOM_BF16 ? batch_grid<OOM_BF16>() : batch_grid<OOM_F32>();
-    if (grid <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
-    if (odt == OOM_BF16)
-        hipLaunchKernelGGL(moe_batch_kernel<OOM_BF16>, dim3(grid), dim3(64 * B_W), 0, st, a);
-    else
-        hipLaunchKernelGGL(moe_batch_kernel<OOM_F32>, dim3(grid), dim3(64 * B_W), 0, st, a);
-    return launched("oom_moe_decode_fp8");
+    if (a.E <= 128) return odt == OOM_BF16 ? launch_batch_t<2, OOM_BF16>(a, st) : launch_batch_t<2, OOM_F32>(a, st);
+    return odt == OOM_BF16 ? launch_batch_t<4, OOM_BF16>(a, st) : launch_batch_t<4, OOM_F32>(a, st);
 }
 
 }  // namespace oom

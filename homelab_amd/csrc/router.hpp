@@ -165,20 +165,17 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, in
 // in pick order), as the reference renormalises (crates/oominf-cuda/kernels/ops.cu:230-294).
 // Written to LDS: experts[i] (ids ascending), ids[r] and w[r] (pick order) and
 // slot_assign[r] (the id-order position of pick r). keys and p are k-entry LDS scratch.
+// Keys of one token's experts from its logits (lane l holds expert l + 64 q in lv[q]):
+// the softmax with the reference's 256-thread block sum (virtual thread lane + 64 q holds
+// expert lane + 64 q; groups of 32 threads absent here (q >= EQ) add zeros, which leaves
+// the sum's bits as route_token_regs computes them), then key = 1 << 39 | p's bits << 8 |
+// (255 - id) for a real expert, 0 past E.
 template <int EQ>
-__device__ __forceinline__ void route_select(const float* __restrict__ l, int E, int k, int lane, uint64_t* keys,
-                                             float* p, int* experts, int* ids, float* w, int* slot_assign) {
-    float lv[EQ];
+__device__ __forceinline__ void route_keys(const float (&lv)[EQ], int E, int lane, uint64_t (&key)[EQ]) {
     float m = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < EQ; q++) {
-        lv[q] = lane + 64 * q < E ? l[lane + 64 * q] : -INFINITY;
-        m = fmaxf(m, lv[q]);
-    }
+    for (int q = 0; q < EQ; q++) m = fmaxf(m, lv[q]);
     m = wave_max(m);
-    // the reference's 256-thread block sum: virtual thread lane + 64 q holds expert
-    // lane + 64 q; groups of 32 threads absent here (q >= EQ) add zeros, which leaves
-    // the sum's bits as route_token_regs computes them
     float ex[EQ], w8[8];
 #pragma unroll
     for (int g = 0; g < 8; g++) w8[g] = 0.0f;
@@ -190,13 +187,18 @@ __device__ __forceinline__ void route_select(const float* __restrict__ l, int E,
         w8[2 * q + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
     }
     const float sum = ((w8[0] + w8[4]) + (w8[2] + w8[6])) + ((w8[1] + w8[5]) + (w8[3] + w8[7]));
-    uint64_t key[EQ];
 #pragma unroll
     for (int q = 0; q < EQ; q++) {
         const int e = lane + 64 * q;
         key[q] = e < E ? (1ull << 39) | ((uint64_t)__float_as_uint(ex[q] / sum) << 8) | (uint64_t)(255 - e) : 0ull;
     }
-    // radix descent: every real key reaches 1 << 39, so at least E >= k keys do
+}
+
+// The k-th largest of the wave's keys (k <= the number of real keys) by a radix descent
+// on ballots: each step keeps a candidate bit if at least k keys reach the candidate, and
+// the descent stops when exactly k do. Every real key reaches 1 << 39.
+template <int EQ>
+__device__ __forceinline__ uint64_t radix_kth(const uint64_t (&key)[EQ], int k) {
     uint64_t kth = 1ull << 39;
     for (int b = 38; b >= 0; b--) {
         const uint64_t cand = kth | (1ull << b);
@@ -208,6 +210,18 @@ __device__ __forceinline__ void route_select(const float* __restrict__ l, int E,
             if (cnt == k) break;
         }
     }
+    return kth;
+}
+
+template <int EQ>
+__device__ __forceinline__ void route_select(const float* __restrict__ l, int E, int k, int lane, uint64_t* keys,
+                                             float* p, int* experts, int* ids, float* w, int* slot_assign) {
+    float lv[EQ];
+#pragma unroll
+    for (int q = 0; q < EQ; q++) lv[q] = lane + 64 * q < E ? l[lane + 64 * q] : -INFINITY;
+    uint64_t key[EQ];
+    route_keys<EQ>(lv, E, lane, key);
+    const uint64_t kth = radix_kth<EQ>(key, k);
     // the picks in id order: lane order within q, q ascending (expert lane + 64 q)
     int base = 0;
 #pragma unroll
