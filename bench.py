@@ -217,7 +217,8 @@ def bench_decode(args, T, zipf, config):
                    "batch": T, "experts": E, "top_k": k, "hidden": H, "inter": I,
                    "distinct_experts_per_step": float(distinct.mean())},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
-                     "traffic": measured_traffic(config), "kernel": "moe_decode_fused_kernel (oom_moe_decode_fp8)",
+                     "traffic": measured_traffic(config),
+                     "kernel": ("moe_decode_fused_kernel" if T == 1 else "moe_batch_kernel") + " (oom_moe_decode_fp8)",
                      "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
     }
     if not args.no_cpu:
