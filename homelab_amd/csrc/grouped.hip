@@ -27,7 +27,6 @@ namespace oom {
 constexpr int GBM = 128;         // assignments per block tile
 constexpr int GBN = 128;         // outputs per block tile (one 128-row weight scale block)
 constexpr int GBK = 128;         // K step (one scale block)
-constexpr int GPITCH = 144;      // LDS row pitch in bytes
 constexpr int GTHREADS = 512;    // 8 waves: 4 x 2 of 32 x 64
 constexpr int G_BUF_FLAGS = 0x00020000;
 
@@ -120,108 +119,222 @@ __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __re
     if (tid == 0) *ntiles = carry_s;
 }
 
-// One K step of a block tile: global -> registers (issued early), registers -> LDS.
+constexpr int G_OOB = 0x7ffffff0;  // past every resource here (extents stay below 0x7fff0000): loads read 0
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// LDS image of a tile (rows x 128 bytes of one K step) as 16-byte chunks: chunk c of row
+// r sits at position 8 r + (c ^ f(r)), f(r) = (r & 7) ^ ((r >> 3) & 1). An MFMA operand
+// read takes one chunk column of 16 rows: any 8 consecutive of them (r = 8q .. 8q + 7)
+// land in 8 different 16-byte bank groups of a 128-byte line, and all 16 in 16 different
+// groups of a 256-byte line (f is a bijection on each 8 rows, and rows r, r + 8 differ in
+// f's low bit, rows of one parity pair with a distinct f).
+__device__ __forceinline__ int chunk_key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int chunk_pos(int r, int c) { return 8 * r + (c ^ chunk_key(r)); }
+
+// The inverse for the loads: position p of the tile holds row p / 8, chunk (p % 8) ^ f.
+__device__ __forceinline__ void pos_chunk(int p, int& r, int& c) {
+    r = p >> 3;
+    c = (p & 7) ^ chunk_key(r);
+}
+
+// One 16-byte load per lane straight into LDS: lane l's bytes land at lds + 16 l.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, off, 0, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void* lds, int off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 4, off, 0, 0, 0);
+}
+
+// Loads a wave issues per stage (every wave the same number, so one wait count fits all).
 template <int NB>
-struct GStage {
-    uint4 a[2];
-    uint4 b[NB][2];
+constexpr int g_loads_per_stage() { return 2 + 2 * NB + 2; }
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding): this wave's loads but the newest n have
+// completed, and its LDS accesses.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+}
+
+// A workgroup barrier with no memory fence: the loop's only LDS writes are direct-to-LDS
+// loads, and each wave waits for its own before arriving, so after the barrier every
+// wave's loads of the stage have landed. (__syncthreads's release fence would wait for
+// every load in flight, the next stages' too.) The signal fences keep the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void g_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// The per-thread sources of a stage: A chunks (activation rows gathered by assignment),
+// B chunks (weight rows), the activation group scale of tile row 16 wave + lane (lanes
+// < 16, x_group 128) and the weight block scales (lanes < NB).
+template <int NB>
+struct GSrc {
+    __amdgpu_buffer_rsrc_t xr, wr, xsr, sr;
+    int xo[2], wo[NB][2];  // step-0 byte offsets
+    int xso, so;           // step-0 byte offsets of this lane's scales (G_OOB: none)
 };
 
-constexpr int G_OOB = 0x7ffffff0;  // past a weight resource (whose extent stays below 0x7fff0000): loads read 0
-
-__device__ __forceinline__ uint4 g_ld16(__amdgpu_buffer_rsrc_t r, int off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
-}
-
-// Step kb's activation and weight chunks of this thread. kb < 0 (past the last step):
-// the weight loads take an offset outside their resource (which spans exactly the
-// record's weight parts), so they read zeros without a memory access; the activation
-// resource has no tight bound (the row count is the caller's), so those loads re-read
-// the thread's step-0 chunk, an in-range address, and the data is dropped.
+// Stage of step kb into LDS: the operands into stage buffer `sb` (A tile, then NB B tiles),
+// the scales into `scx` and `scw` (64 words per wave). kb >= nkb: every load reads zeros
+// (offsets past their resources), which keeps each wave's load count fixed.
 template <int NB>
-__device__ __forceinline__ void gstage_load(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr, const int (&xo)[2],
-                                            const int (&wo)[NB][2], int kb, GStage<NB>& st) {
+__device__ __forceinline__ void g_issue(const GSrc<NB>& s, int kb, int nkb, uint8_t* sb, float* scx, float* scw,
+                                        int wave) {
+    const bool ok = kb < nkb;
     const int k0 = kb * GBK;
 #pragma unroll
-    for (int j = 0; j < 2; j++) st.a[j] = g_ld16(xr, kb >= 0 ? xo[j] + k0 : xo[j]);
-#pragma unroll
-    for (int m = 0; m < NB; m++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) st.b[m][j] = g_ld16(wr, kb >= 0 ? wo[m][j] + k0 : G_OOB);
-}
-
-template <int NB>
-__device__ __forceinline__ void gstage_store(const GStage<NB>& st, uint8_t* alds, uint8_t* blds, int tid) {
-    const int r = tid >> 3, c16 = (tid & 7) * 16;
-#pragma unroll
-    for (int j = 0; j < 2; j++) *reinterpret_cast<uint4*>(alds + (r + 64 * j) * GPITCH + c16) = st.a[j];
+    for (int j = 0; j < 2; j++) dma16(s.xr, sb + (2 * wave + j) * 1024, ok ? s.xo[j] + k0 : G_OOB);
 #pragma unroll
     for (int m = 0; m < NB; m++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
-            *reinterpret_cast<uint4*>(blds + (m * GBN + r + 64 * j) * GPITCH + c16) = st.b[m][j];
+            dma16(s.wr, sb + GBM * GBK + m * GBN * GBK + (2 * wave + j) * 1024, ok ? s.wo[m][j] + k0 : G_OOB);
+    // the scales, into the wave's 64-word slots (lane l writes word l): lanes 0..15 the
+    // group scales of tile rows 16 wave + l, lanes 0 .. NB the weight block scales; the
+    // other lanes read zeros past their resource. Every lane runs both loads, so each
+    // wave's count of loads in flight is the same on every path.
+    dma4(s.xsr, scx + 64 * wave, ok && s.xso != G_OOB ? s.xso + 4 * kb : G_OOB);
+    dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * kb : G_OOB);
 }
 
-// 32 bytes of row `row` at K offset 32 (lane / 16): an MFMA operand (A: row = M index,
-// B: row = N index; both layouts take k = 32 (lane / 16) + byte).
+// 32 bytes of tile row `row` at K offset 32 (lane / 16): an MFMA operand (A: row = M
+// index, B: row = N index; both layouts take k = 32 (lane / 16) + byte).
 __device__ __forceinline__ gi32x8 gop(const uint8_t* base, int row, int lane) {
-    const uint8_t* p = base + row * GPITCH + 32 * (lane >> 4);
-    const uint4 lo = *reinterpret_cast<const uint4*>(p), hi = *reinterpret_cast<const uint4*>(p + 16);
+    const int c = 2 * (lane >> 4);
+    const uint4 lo = *reinterpret_cast<const uint4*>(base + 16 * chunk_pos(row, c));
+    const uint4 hi = *reinterpret_cast<const uint4*>(base + 16 * chunk_pos(row, c + 1));
     gi32x8 v;
     v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
     v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
     return v;
 }
 
+// One K step on the matrix cores from a stage buffer: acc += the block sums scaled by the
+// weight's block scale (and the row's activation group scale).
+template <int NB>
+__device__ __forceinline__ void g_step(const uint8_t* sb, const float* scx, const float* scw, bool xgrp, int wm,
+                                       int wn, int wave, int lane, float (&acc)[NB][2][4][4]) {
+    // tile row r's group scale is word 64 (r / 16) + r % 16 of scx; the wave's weight
+    // scales words 64 wave + m of scw
+    float xsk[2][4];
+    if (xgrp) {
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) xsk[ms][e] = scx[64 * (2 * wm + ms) + 4 * (lane >> 4) + e];
+    }
+    float wsk[NB];
+#pragma unroll
+    for (int m = 0; m < NB; m++) wsk[m] = scw[64 * wave + m];
+    gi32x8 aop[2];
+#pragma unroll
+    for (int ms = 0; ms < 2; ms++) aop[ms] = gop(sb, 32 * wm + 16 * ms + (lane & 15), lane);
+#pragma unroll
+    for (int m = 0; m < NB; m++)
+#pragma unroll
+        for (int ns = 0; ns < 4; ns++) {
+            const gi32x8 bop = gop(sb + GBM * GBK + m * GBN * GBK, 64 * wn + 16 * ns + (lane & 15), lane);
+#pragma unroll
+            for (int ms = 0; ms < 2; ms++) {
+                const gf32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const gf32x4 blk =
+                    __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop[ms], bop, z, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float sc = xgrp ? wsk[m] * xsk[ms][e] : wsk[m];
+                    acc[m][ms][ns][e] = fmaf(blk[e], sc, acc[m][ms][ns][e]);
+                }
+            }
+        }
+}
+
 // MODE 0: y = scaled xq . W^T. MODE 1: gate and up (NB = 2), h = silu(g) * u quantised.
+//
+// K steps stream through LDS stage buffers filled by direct-to-LDS buffer loads. Three
+// buffers (gate/up: one block per CU): at step kb a wave waits for its own loads of stage
+// kb (kb + 1's may still be in flight), the block synchronises (every wave's loads of kb
+// have landed, and every wave is done reading the buffer stage kb + 2 takes), stage
+// kb + 2 is issued, and step kb runs on the matrix cores while kb + 1 and kb + 2 load.
+// Two buffers (down: two blocks per CU, which overlap each other's waits): stage kb + 1
+// is issued at step kb.
+//
+// Tiles from the device tile table go to XCDs in runs: the hardware sends block L (x
+// fastest) to XCD L % 8, and XCD x takes work items x C .. x C + C of the W = NT * MT
+// (N-tile, table tile) items, table tile fastest. So the blocks an XCD runs together walk
+// the M-tiles of one N-tile, and an expert's weight tile is fetched once and then served
+// from that XCD's L2.
 template <int MODE>
 __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     constexpr int NB = MODE == 1 ? 2 : 1;
-    __shared__ __align__(16) uint8_t alds[GBM * GPITCH];
-    __shared__ __align__(16) uint8_t blds[NB * GBN * GPITCH];
+    constexpr int NST = MODE == 1 ? 3 : 2;               // LDS stage buffers
+    constexpr int SBYTES = GBM * GBK + NB * GBN * GBK;  // one stage: A tile and NB B tiles
+    constexpr int LPS = g_loads_per_stage<NB>();
+    // each stage its own LDS object: the compiler's wait for direct-to-LDS loads then
+    // covers only the loads into the buffer a read touches
+    // a stage: the A tile, NB B tiles, then the activation and weight scales (64 words per
+    // wave each)
+    constexpr int STOT = SBYTES + 2 * GTHREADS * 4;
+    __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT], sb2[NST == 3 ? STOT : 16];
     __shared__ float rowmax[GBM][2];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;  // rows 32 wm .. + 32, columns 64 wn .. + 64
     // ---- which tile ----
-    int i, m0;
+    int i, m0, n0;
     if (g.tiles) {
-        const int mt = blockIdx.y;
-        if (mt >= *g.ntiles) return;
+        const int NT = (int)gridDim.x, MT = *g.ntiles, W = NT * MT;
+        const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), C = (W + 7) / 8;
+        if ((L >> 3) >= C) return;
+        const int w = (L & 7) * C + (L >> 3);
+        if (w >= W) return;
+        const int nt = w / MT, mt = w - nt * MT;
         i = g.tiles[2 * mt];
         m0 = g.tiles[2 * mt + 1];
+        n0 = nt * GBN;
     } else {
         i = blockIdx.z;
         m0 = blockIdx.y * GBM;
+        n0 = blockIdx.x * GBN;
     }
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
-    const int n0 = blockIdx.x * GBN;
     const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
     const int nkb = (int)(g.K / GBK);
-    // this thread's staging chunks: activation rows r and r + 64 of the tile (rows past
-    // the expert's range repeat its first), weight rows r and r + 64, 16 bytes at c16
-    const __amdgpu_buffer_rsrc_t xr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.xq), (short)0, 0x7fffffff, G_BUF_FLAGS);
+    const bool xgrp = g.x_group != 0;
+    // ---- this thread's sources: load j of the A (and each B) tile covers positions
+    // (2 wave + j) 64 + lane, i.e. chunk c of tile row r (rows past the expert's range
+    // repeat its first assignment) ----
+    GSrc<NB> src;
+    src.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.xq), (short)0, 0x7fff0000, G_BUF_FLAGS);
     const int wbytes = (int)(max(g.w_off, NB == 2 ? g.w2_off : g.w_off) + g.N * g.K);  // end of the weight parts
-    const __amdgpu_buffer_rsrc_t wr =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, wbytes, G_BUF_FLAGS);
-    int xo[2], wo[NB][2];
-    {
-        const int r = tid >> 3, c16 = (tid & 7) * 16;
+    src.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, wbytes, G_BUF_FLAGS);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            int a = a0 + m0 + r + 64 * j;
-            if (a >= a1) a = a0;
-            xo[j] = (int)((g.rows ? g.rows[a] : a) * g.K) + c16;
+    for (int j = 0; j < 2; j++) {
+        int r, c;
+        pos_chunk((2 * wave + j) * 64 + lane, r, c);
+        int a = a0 + m0 + r;
+        if (a >= a1) a = a0;
+        src.xo[j] = (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c;
 #pragma unroll
-            for (int m = 0; m < NB; m++)
-                wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r + 64 * j) * g.K) + c16;
-        }
+        for (int m = 0; m < NB; m++)
+            src.wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r) * g.K) + 16 * c;
     }
-    const float* ws0 = reinterpret_cast<const float*>(rec + g.s_off) + (int64_t)(n0 / 128) * nkb;
-    const float* ws1 = reinterpret_cast<const float*>(rec + g.s2_off) + (int64_t)(n0 / 128) * nkb;
+    // scales: lane l < 16 of wave w loads tile row 16 w + l's group scale (x_group 128),
+    // lane m < NB the block scale of weight matrix m, once per K step
+    src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
+    src.xsr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.xs), (short)0, xgrp ? 0x7fff0000 : 0,
+                                                G_BUF_FLAGS);
+    src.xso = G_OOB;
+    if (xgrp && lane < 16) {
+        const int a = min(a0 + m0 + 16 * wave + lane, a1 - 1);
+        src.xso = (int)((g.rows ? g.rows[a] : a) * nkb * 4);
+    }
+    src.so = lane < NB ? (int)((lane == 0 ? g.s_off : g.s2_off) + (int64_t)(n0 / 128) * nkb * 4) : G_OOB;
     // this lane's output rows (per 16-row M subtile ms, element e): assignment index
     int arow_out[2][4];
 #pragma unroll
@@ -237,49 +350,38 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
             for (int ns = 0; ns < 4; ns++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = 0.0f;
-    GStage<NB> st;
-    gstage_load<NB>(xr, wr, xo, wo, 0, st);
-    for (int kb = 0; kb < nkb; kb++) {
-        __syncthreads();  // the previous step's operand reads are done
-        gstage_store<NB>(st, alds, blds, tid);
-        __syncthreads();
-        gstage_load<NB>(xr, wr, xo, wo, kb + 1 < nkb ? kb + 1 : -1, st);
-        // per-row activation group scales of this step (x_group 128)
-        float xsk[2][4];
-        if (g.x_group) {
-#pragma unroll
-            for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int a = min(arow_out[ms][e], a1 - 1);
-                    const int64_t xr = g.rows ? g.rows[a] : a;
-                    xsk[ms][e] = g.xs[xr * nkb + kb];
-                }
-        }
-        float wsk[NB];
-        wsk[0] = ws0[kb];
-        if constexpr (NB == 2) wsk[1] = ws1[kb];
-        gi32x8 aop[2];
-#pragma unroll
-        for (int ms = 0; ms < 2; ms++) aop[ms] = gop(alds, 32 * wm + 16 * ms + (lane & 15), lane);
-#pragma unroll
-        for (int m = 0; m < NB; m++)
-#pragma unroll
-            for (int ns = 0; ns < 4; ns++) {
-                const gi32x8 bop = gop(blds + m * GBN * GPITCH, 64 * wn + 16 * ns + (lane & 15), lane);
-#pragma unroll
-                for (int ms = 0; ms < 2; ms++) {
-                    const gf32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                    const gf32x4 blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop[ms], bop, z, 0, 0, 0, 127,
-                                                                                       0, 127);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const float s = g.x_group ? wsk[m] * xsk[ms][e] : wsk[m];
-                        acc[m][ms][ns][e] = fmaf(blk[e], s, acc[m][ms][ns][e]);
-                    }
-                }
-            }
+#define G_SX(B) reinterpret_cast<float*>((B) + SBYTES)
+#define G_SW(B) reinterpret_cast<float*>((B) + SBYTES + GTHREADS * 4)
+    // one step on stage buffer SB while stage kb + NST - 1 goes into NSB (WAIT: this
+    // wave's loads newer than stage kb, which may still be in flight)
+#define G_STEP(SB, NSB, WAIT)                                                                       \
+    {                                                                                               \
+        wait_vm<WAIT>();                                                                            \
+        g_barrier();                                                                                \
+        g_issue<NB>(src, kb + NST - 1, nkb, NSB, G_SX(NSB), G_SW(NSB), wave);                       \
+        g_step<NB>(SB, G_SX(SB), G_SW(SB), xgrp, wm, wn, wave, lane, acc);                          \
+        if (++kb == nkb) break;                                                                     \
     }
+    int kb = 0;
+    g_issue<NB>(src, 0, nkb, sb0, G_SX(sb0), G_SW(sb0), wave);
+    if constexpr (NST == 3) {
+        g_issue<NB>(src, 1, nkb, sb1, G_SX(sb1), G_SW(sb1), wave);
+        for (;;) {
+            G_STEP(sb0, sb2, LPS)
+            G_STEP(sb1, sb0, LPS)
+            G_STEP(sb2, sb1, LPS)
+        }
+    } else {
+        for (;;) {
+            G_STEP(sb0, sb1, 0)
+            G_STEP(sb1, sb0, 0)
+        }
+    }
+#undef G_SX
+#undef G_SW
+#undef G_STEP
+    wait_vm<0>();  // the zero-filled stages past the end have landed before LDS is reused
+    __syncthreads();
     // ---- epilogue ----
     if constexpr (MODE == 0) {
 #pragma unroll
@@ -493,7 +595,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     a.s2_off = geo->up_scale;
     a.hq = hq;
     a.hs = hs;
-    if (int rc = launch_grouped(a, 1, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles, 1), st)) return rc;
+    // 8 spare rows of blocks: the XCD-run order needs the grid to cover 8 ceil(W / 8) slots
+    if (int rc = launch_grouped(a, 1, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles + 8, 1), st)) return rc;
     GArgs d{};
     d.recs = recs;
     d.off = pv.off();
@@ -510,6 +613,6 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     d.w2_off = geo->down_weight;
     d.s2_off = geo->down_scale;
     d.y = y;
-    if (int rc = launch_grouped(d, 0, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles, 1), st)) return rc;
+    if (int rc = launch_grouped(d, 0, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles + 8, 1), st)) return rc;
     return launch_combine(y, pv.slot_assign(), weights, out, out_dtype, T, (int)geo->hidden, k, st);
 }
