@@ -123,8 +123,9 @@ int oom_moe_plan(const int32_t* ids, int T, int E, int k, const uint64_t* all_re
  * step for all their tokens. x [T, hidden] in x_dtype; out [T, hidden] in
  * out_dtype; ids i32 [T, k] and weights f32 [T, k] are written as by
  * oom_router_topk. Steps with T * k <= 512, E <= 256, hidden <= 4096 and inter <= 2048 run
- * as one persistent kernel; larger steps as router, plan, gate/up, down and combine
- * launches. The fused equivalent of Moe::forward's routed part
+ * as one persistent kernel (2..16 tokens with bf16 x, k <= 8 and 16-byte aligned x: the
+ * products on bf16 matrix cores; otherwise on the vector ALUs); larger steps as router,
+ * plan, gate/up, down and combine launches. The fused equivalent of Moe::forward's routed part
  * (crates/oominf-models-qwen/src/moe.rs:290-366: router_topk, begin_routed,
  * finish_routed, run_group, moe_combine_slots). */
 size_t oom_moe_decode_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo);
