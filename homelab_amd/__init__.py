@@ -39,6 +39,11 @@ SIGNATURES = {
     "oom_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
     "oom_gemv_fp8_workspace_size": (SZ, [I32, I64, I64]),
     "oom_gemv_fp8": (I32, [P, I32, P, P, I32, P, I32, I32, I64, I64, P, SZ, P]),
+    "oom_gemv_bf16_workspace_size": (SZ, [I32, I64, I64]),
+    "oom_gemv_bf16": (I32, [P, I32, P, P, I32, I32, I64, I64, P, SZ, P]),
+    "oom_moe_combine_shared": (I32, [P, P, P, P, I32, I32, I32, P]),
+    "oom_moe_layer_decode_fp8_workspace_size": (SZ, [I32, I32, I32, P, P]),
+    "oom_moe_layer_decode_fp8": (I32, [P, I32, P, P, I32, I32, I32, P, P, P, P, P, P, P, I32, P, SZ, P]),
     "oom_moe_gate_up_fp8": (I32, [P, P, P, I32, P, I32, P, P, P]),
     "oom_moe_down_fp8": (I32, [P, P, I32, P, P, P, P]),
     "oom_moe_combine_slots": (I32, [P, P, P, P, I32, I32, I32, I32, P]),
@@ -170,6 +175,42 @@ def moe_plan_size(T: int, E: int, k: int) -> int:
 def moe_plan(ids, E: int, all_recs, plan, recs, stream=None) -> None:
     T, k = ids.shape
     check(lib().oom_moe_plan(_ptr(ids), T, E, k, _ptr(all_recs), _ptr(plan), _ptr(recs), _stream(stream)))
+
+
+def gemv_bf16_workspace_size(T: int, N: int, K: int) -> int:
+    return int(lib().oom_gemv_bf16_workspace_size(T, N, K))
+
+
+def gemv_bf16(x, w, y, ws=None, stream=None) -> None:
+    """y[t, n] = sum_k x[t, k] * w[n, k]; w a bf16 tensor [N, K]."""
+    T, K = x.shape
+    N = w.shape[0]
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    check(lib().oom_gemv_bf16(_ptr(x), _dtype_code(x), _ptr(w), _ptr(y), _dtype_code(y), T, N, K, _ptr(ws), ws_bytes,
+                              _stream(stream)))
+
+
+def moe_combine_shared(routed, shared, gate_logit, out, stream=None) -> None:
+    T, H = routed.shape
+    check(lib().oom_moe_combine_shared(_ptr(routed), _ptr(shared), _ptr(gate_logit), _ptr(out), _dtype_code(out), T,
+                                       H, _stream(stream)))
+
+
+def moe_layer_decode_fp8_workspace_size(T: int, E: int, k: int, geo: Fp8Record, shared_geo: Fp8Record) -> int:
+    return int(lib().oom_moe_layer_decode_fp8_workspace_size(T, E, k, ctypes.byref(geo), ctypes.byref(shared_geo)))
+
+
+def moe_layer_decode_fp8(x, router_w, all_recs, k: int, geo: Fp8Record, shared_rec, shared_geo: Fp8Record,
+                         shared_gate_w, ids, weights, out, ws, stream=None) -> None:
+    """One decode MoE layer: router GEMV (bf16 router_w [E, H]), routed experts, shared
+    expert (its record address in the device tensor shared_rec [1]) gated by
+    sigmoid(x . shared_gate_w)."""
+    T = x.shape[0]
+    E = router_w.shape[0]
+    check(lib().oom_moe_layer_decode_fp8(_ptr(x), _dtype_code(x), _ptr(router_w), _ptr(all_recs), T, E, k,
+                                         ctypes.byref(geo), _ptr(shared_rec), ctypes.byref(shared_geo),
+                                         _ptr(shared_gate_w), _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out),
+                                         _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
 
 
 def moe_decode_fp8_workspace_size(T: int, E: int, k: int, geo: Fp8Record) -> int:

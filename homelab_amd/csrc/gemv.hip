@@ -15,14 +15,20 @@
 //     butterfly (R * T - 1 + log2(64 / (R * T)) exchanges);
 //   - splits > 1 write fp32 partials [splits, T, N]; the last block of a row tile
 //     (a ticket per tile, reset after use) adds them in split order, so the result
-//     does not depend on block timing (crates/oominf-cuda/kernels/ops.cu:421-439).
+//     does not depend on block timing (crates/oominf-cuda/kernels/ops.cu:421-439);
+//   - the workspace holds the tickets first, in an area sized for the most tiles any
+//     T can have at this N (rows / 8), then the partials: a workspace left by a call
+//     of another T or K still has zero tickets where this call looks (partials are
+//     written before they are read), so calls with one N share a workspace.
 #include "common.hpp"
 
 namespace oom {
 
 constexpr int GEMV_WAVES = 4;
 
-template <int T, int R, int KCH, int SL, int XDT, int YDT>
+// WB: the weights are bf16 [N, K] (no scales): a lane's 16 columns of a chunk are two
+// 16-byte loads, converted exactly to fp32.
+template <int T, int R, int KCH, int SL, int XDT, int YDT, bool WB = false>
 __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ x, const uint8_t* __restrict__ q,
                                                        const float* __restrict__ scale, void* __restrict__ y,
                                                        float* __restrict__ partial, uint32_t* __restrict__ tickets,
@@ -49,14 +55,18 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
 #pragma unroll
     for (int i = 0; i < T * R; i++) acc[i] = 0.0f;
 
-    uint4 w[R][KCH];
+    constexpr int NW = WB ? 2 : 1;  // 16-byte loads per lane per (row, chunk)
+    uint4 w[R][KCH][NW];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         int row = min(row0 + r, N - 1);
 #pragma unroll
         for (int c = 0; c < KCH; c++) {
             int col = c * 1024 + lane * 16;
-            w[r][c] = col < kl ? *reinterpret_cast<const uint4*>(q + (size_t)row * K + k0 + col) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int h = 0; h < NW; h++)
+                w[r][c][h] = col < kl ? *reinterpret_cast<const uint4*>(q + ((size_t)row * K + k0 + col) * NW + 16 * h)
+                                      : make_uint4(0, 0, 0, 0);
         }
     }
 #pragma unroll
@@ -66,13 +76,25 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
 #pragma unroll
         for (int r = 0; r < R; r++) {
             int row = min(row0 + r, N - 1);
-            if constexpr (SL == OOM_SCALE_ROW) sc[r] = 1.0f;
+            if constexpr (WB || SL == OOM_SCALE_ROW) sc[r] = 1.0f;
             else if constexpr (SL == OOM_SCALE_1X128) sc[r] = col < K ? scale[(size_t)row * nkb + (col >> 7)] : 0.0f;
             else sc[r] = col < K ? scale[(size_t)(row >> 7) * nkb + (col >> 7)] : 0.0f;
         }
         float wf[R][16];
 #pragma unroll
-        for (int r = 0; r < R; r++) e4m3x16(w[r][c], wf[r]);
+        for (int r = 0; r < R; r++) {
+            if constexpr (WB) {
+                const uint32_t u[8] = {w[r][c][0].x, w[r][c][0].y, w[r][c][0].z, w[r][c][0].w,
+                                       w[r][c][NW - 1].x, w[r][c][NW - 1].y, w[r][c][NW - 1].z, w[r][c][NW - 1].w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    wf[r][2 * i] = __uint_as_float(u[i] << 16);
+                    wf[r][2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+                }
+            } else {
+                e4m3x16(w[r][c][0], wf[r]);
+            }
+        }
 #pragma unroll
         for (int t = 0; t < T; t++) {
             float xv[16];
@@ -98,7 +120,7 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
     const bool writer = (lane % (64 / (T * R))) == 0;
     const int t = g / R, r = g % R, row = row0 + r;
     if (writer && row < N && t < tn) {
-        if constexpr (SL == OOM_SCALE_ROW) tot *= scale[row];
+        if constexpr (!WB && SL == OOM_SCALE_ROW) tot *= scale[row];
         if (splits == 1) store_out<YDT>(y, (size_t)t * N + row, tot);
         else partial[((size_t)split * T + t) * N + row] = tot;
     }
@@ -127,13 +149,13 @@ struct GemvPlan {
     size_t lds;
 };
 
-static GemvPlan gemv_plan(int T, int64_t N, int64_t K) {
+static GemvPlan gemv_plan(int T, int64_t N, int64_t K, bool wb = false) {
     GemvPlan p;
     p.tp = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16;
     p.R = p.tp >= 8 ? 2 : 4;
     // x of one split in LDS: tp * kch * 4 KiB <= 64 KiB
     int kch_max = std::max(1, 16 / p.tp);
-    kch_max = std::min(kch_max, 4);
+    kch_max = std::min(kch_max, wb ? 2 : 4);  // bf16 rows take twice the registers per chunk
     int kchunks = (int)cdiv(K, 1024);
     p.tiles = (int)cdiv(N, (int64_t)GEMV_WAVES * p.R);
     // enough blocks to cover the CUs (>= 512 blocks), but a split never shorter than 1 KiB
@@ -146,14 +168,14 @@ static GemvPlan gemv_plan(int T, int64_t N, int64_t K) {
     return p;
 }
 
-template <int T, int R, int KCH>
+template <int T, int R, int KCH, bool WB>
 static void launch_gemv(const GemvPlan& p, int sl, int xdt, int ydt, const void* x, const uint8_t* q, const float* s,
                         void* y, float* part, uint32_t* tk, int tn, int N, int K, hipStream_t st) {
     dim3 grid(p.tiles, p.splits), block(256);
 #define GEMV_CASE(SL, XD, YD)                                                                                     \
     if (sl == SL && xdt == XD && ydt == YD) {                                                                     \
-        hipLaunchKernelGGL((gemv_fp8_kernel<T, R, KCH, SL, XD, YD>), grid, block, p.lds, st, x, q, s, y, part, tk, tn, \
-                           N, K);                                                                                 \
+        hipLaunchKernelGGL((gemv_fp8_kernel<T, R, KCH, SL, XD, YD, WB>), grid, block, p.lds, st, x, q, s, y, part, tk, \
+                           tn, N, K);                                                                             \
         return;                                                                                                   \
     }
 #define GEMV_DT(SL)                   \
@@ -162,33 +184,42 @@ static void launch_gemv(const GemvPlan& p, int sl, int xdt, int ydt, const void*
     GEMV_CASE(SL, OOM_BF16, OOM_F32)  \
     GEMV_CASE(SL, OOM_BF16, OOM_BF16)
     GEMV_DT(OOM_SCALE_ROW)
-    GEMV_DT(OOM_SCALE_1X128)
-    GEMV_DT(OOM_SCALE_128X128)
+    if constexpr (!WB) {
+        GEMV_DT(OOM_SCALE_1X128)
+        GEMV_DT(OOM_SCALE_128X128)
+    }
 #undef GEMV_DT
 #undef GEMV_CASE
 }
 
-template <int T, int R>
+template <int T, int R, bool WB = false>
 static void launch_gemv_k(const GemvPlan& p, int sl, int xdt, int ydt, const void* x, const uint8_t* q,
                           const float* s, void* y, float* part, uint32_t* tk, int tn, int N, int K, hipStream_t st) {
     switch (p.kch) {
-        case 1: launch_gemv<T, R, 1>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
-        case 2: launch_gemv<T, R, 2>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
+        case 1: launch_gemv<T, R, 1, WB>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
+        case 2: launch_gemv<T, R, 2, WB>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
         default:
-            if constexpr (T <= 4) launch_gemv<T, R, 4>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st);
+            if constexpr (T <= 4 && !WB) launch_gemv<T, R, 4, WB>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st);
             break;
     }
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// Bytes of the ticket area at the start of a GEMV workspace: one ticket per row tile at the
+// smallest tile (two rows per wave, 8 rows), whatever T is.
+static size_t gemv_ticket_bytes(int64_t N) { return align256((size_t)cdiv(N, (int64_t)GEMV_WAVES * 2) * sizeof(uint32_t)); }
+
+static size_t gemv_ws_bytes(const GemvPlan& p, int64_t N) {
+    if (p.splits == 1) return 0;
+    return gemv_ticket_bytes(N) + (size_t)p.splits * p.tp * N * sizeof(float);
+}
+
 }  // namespace oom
 
 extern "C" size_t oom_gemv_fp8_workspace_size(int T, int64_t N, int64_t K) {
     if (T < 1 || N < 1 || K < 1) return 0;
-    oom::GemvPlan p = oom::gemv_plan(T, N, K);
-    if (p.splits == 1) return 0;
-    return oom::align256((size_t)p.splits * p.tp * N * sizeof(float)) + (size_t)p.tiles * sizeof(uint32_t);
+    return oom::gemv_ws_bytes(oom::gemv_plan(T, N, K), N);
 }
 
 extern "C" int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const float* scale, int scale_layout,
@@ -211,8 +242,8 @@ extern "C" int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const 
         if (ws_bytes < need || ws == nullptr)
             return fail(OOM_ERR_WORKSPACE, "oom_gemv_fp8: workspace smaller than oom_gemv_fp8_workspace_size()");
         OOM_REQUIRE(aligned(ws, 16), "oom_gemv_fp8: workspace must be 16-byte aligned");
-        part = reinterpret_cast<float*>(ws);
-        tk = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(ws) + align256((size_t)p.splits * p.tp * N * 4));
+        tk = reinterpret_cast<uint32_t*>(ws);
+        part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + gemv_ticket_bytes(N));
     }
     hipStream_t st = as_stream(stream);
     int n = (int)N, k = (int)K;
@@ -224,4 +255,43 @@ extern "C" int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const 
         default: launch_gemv_k<16, 2>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
     }
     return launched("oom_gemv_fp8");
+}
+
+extern "C" size_t oom_gemv_bf16_workspace_size(int T, int64_t N, int64_t K) {
+    if (T < 1 || N < 1 || K < 1) return 0;
+    return oom::gemv_ws_bytes(oom::gemv_plan(T, N, K, true), N);
+}
+
+extern "C" int oom_gemv_bf16(const void* x, int x_dtype, const uint16_t* w, void* y, int y_dtype, int T, int64_t N,
+                             int64_t K, void* ws, size_t ws_bytes, void* stream) {
+    using namespace oom;
+    OOM_REQUIRE(T >= 1 && T <= 16, "oom_gemv_bf16: T must be 1..16");
+    OOM_REQUIRE(N >= 1 && K >= 16 && K % 16 == 0, "oom_gemv_bf16: K must be a positive multiple of 16");
+    OOM_REQUIRE(N <= INT32_MAX && K <= INT32_MAX && N * K <= ((int64_t)1 << 39), "oom_gemv_bf16: shape too large");
+    OOM_REQUIRE(x && w && y, "oom_gemv_bf16: null buffer");
+    OOM_REQUIRE(aligned(w, 16), "oom_gemv_bf16: weights must be 16-byte aligned");
+    OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_gemv_bf16: x_dtype");
+    OOM_REQUIRE(y_dtype == OOM_F32 || y_dtype == OOM_BF16, "oom_gemv_bf16: y_dtype");
+    GemvPlan p = gemv_plan(T, N, K, true);
+    float* part = nullptr;
+    uint32_t* tk = nullptr;
+    if (p.splits > 1) {
+        size_t need = oom_gemv_bf16_workspace_size(T, N, K);
+        if (ws_bytes < need || ws == nullptr)
+            return fail(OOM_ERR_WORKSPACE, "oom_gemv_bf16: workspace smaller than oom_gemv_bf16_workspace_size()");
+        OOM_REQUIRE(aligned(ws, 16), "oom_gemv_bf16: workspace must be 16-byte aligned");
+        tk = reinterpret_cast<uint32_t*>(ws);
+        part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + gemv_ticket_bytes(N));
+    }
+    hipStream_t st = as_stream(stream);
+    const int n = (int)N, k = (int)K;
+    const uint8_t* q = reinterpret_cast<const uint8_t*>(w);
+    switch (p.tp) {
+        case 1: launch_gemv_k<1, 4, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
+        case 2: launch_gemv_k<2, 4, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
+        case 4: launch_gemv_k<4, 4, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
+        case 8: launch_gemv_k<8, 2, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
+        default: launch_gemv_k<16, 2, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
+    }
+    return launched("oom_gemv_bf16");
 }

@@ -12,7 +12,9 @@
  *   - allocates nothing: scratch comes from a caller workspace whose size the
  *     matching *_workspace_size() returns. A workspace must be zero-filled once
  *     before its first use (oom_workspace_init); calls leave it ready for the next
- *     call. Calls sharing one workspace must be ordered (one stream).
+ *     call of the same entry point (any T up to the size it was made for; for the
+ *     GEMVs, the same N: their split tickets sit in an area sized by N). Calls
+ *     sharing one workspace must be ordered (one stream).
  *   - is deterministic: the same inputs give the same bits.
  * Activations are fp32 or bf16 (OOM_F32 / OOM_BF16); accumulation is fp32.
  */
@@ -84,6 +86,14 @@ size_t oom_gemv_fp8_workspace_size(int T, int64_t N, int64_t K);
 int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const float* scale, int scale_layout, void* y,
                  int y_dtype, int T, int64_t N, int64_t K, void* ws, size_t ws_bytes, void* stream);
 
+/* Decode GEMV over bf16 weights: y[t, n] = sum_k x[t, k] * w[n, k] (fp32 accumulate) for
+ * t < T <= 16. x [T, K] in x_dtype; w bf16 [N, K] (16-byte aligned, K % 16 == 0); y [T, N]
+ * in y_dtype. Replaces Linear::gemm_bf16 at decode sizes (crates/oominf-core/src/backend.rs:
+ * 222-234; crates/oominf-cuda/kernels/ops.cu:329-440,568-576): the router GEMV. */
+size_t oom_gemv_bf16_workspace_size(int T, int64_t N, int64_t K);
+int oom_gemv_bf16(const void* x, int x_dtype, const uint16_t* w, void* y, int y_dtype, int T, int64_t N, int64_t K,
+                  void* ws, size_t ws_bytes, void* stream);
+
 /* Routed-expert gate/up + SwiGLU over FP8 records read in place:
  * h[a, j] = silu(x[assign_tok[a]] . Wg_e[j]) * (x[assign_tok[a]] . Wu_e[j]) for the
  * assignments a in [off[i], off[i+1]) of expert i < n_experts, whose record starts
@@ -132,6 +142,28 @@ size_t oom_moe_decode_fp8_workspace_size(int T, int E, int k, const OomFp8Record
 int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T, int E,
                        int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
                        void* ws, size_t ws_bytes, void* stream);
+
+/* The shared expert's gated add: out[t, c] = routed[t, c] + sigmoid(gate_logit[t]) *
+ * shared[t, c], sigmoid(v) = 1 / (1 + e^-v); routed and shared f32 [T, H], gate_logit f32
+ * [T]; out [T, H] in out_dtype. Replaces Elementwise::moe_combine
+ * (crates/oominf-core/src/backend.rs:909-917; crates/oominf-cuda/kernels/ops.cu:310-316). */
+int oom_moe_combine_shared(const float* routed, const float* shared, const float* gate_logit, void* out,
+                           int out_dtype, int T, int H, void* stream);
+
+/* One decode MoE layer with no host synchronisation: logits = x Wr^T over bf16 router
+ * weights router_w [E, hidden]; the routed step of oom_moe_decode_fp8 (ids, weights written
+ * as there); the shared expert, an FP8 record (device address at shared_rec[0], geometry
+ * shared_geo with the same hidden) run as one expert with weight 1; its gate logit
+ * x . shared_gate_w (bf16 [hidden]); out = routed + sigmoid(gate logit) * shared, in
+ * out_dtype. T <= 16; one workspace made for T serves every step of 1..T tokens. The
+ * device half of Moe::forward with every routed expert resident
+ * (crates/oominf-models-qwen/src/moe.rs:254-366) and Moe::shared (moe.rs:498-527). */
+size_t oom_moe_layer_decode_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo,
+                                               const OomFp8Record* shared_geo);
+int oom_moe_layer_decode_fp8(const void* x, int x_dtype, const uint16_t* router_w, const uint64_t* all_recs, int T,
+                             int E, int k, const OomFp8Record* geo, const uint64_t* shared_rec,
+                             const OomFp8Record* shared_geo, const uint16_t* shared_gate_w, int32_t* ids,
+                             float* weights, void* out, int out_dtype, void* ws, size_t ws_bytes, void* stream);
 
 /* Per-row e4m3 quantisation of activations: scale[r] = max_c |x[r, c]| / 448 (1 for an
  * all-zero row), q[r, c] = e4m3(x[r, c] / scale[r]) rounded to nearest even and

@@ -84,6 +84,9 @@ def lib() -> ctypes.CDLL:
             "oracle_router_topk": (None, [P, I32, I32, I32, P, P]),
             "oracle_router_probs": (None, [P, I32, I32, P]),
             "oracle_gemv_fp8": (None, [P, I32, P, P, I32, I64, I64, P]),
+            "oracle_gemv_bf16": (None, [P, I32, P, I64, I64, P]),
+            "oracle_moe_combine_shared": (None, [P, P, P, P, I32, I32]),
+            "oracle_moe_layer_decode_fp8": (I32, [P, I32, P, P, I32, I32, P, P, P, P, P, P, P, P, P]),
             "oracle_moe_plan": (I32, [P, I32, I32, I32, P, P, P, P]),
             "oracle_moe_gate_up_fp8": (None, [P, P, P, I32, P, P, P]),
             "oracle_moe_down_fp8": (None, [P, P, I32, P, P, P]),
@@ -240,6 +243,47 @@ def gemv_fp8(x: np.ndarray, q: np.ndarray, scale: np.ndarray, layout: int) -> np
     lib().oracle_gemv_fp8(_p(x), T, _p(np.ascontiguousarray(q)), _p(np.ascontiguousarray(scale, dtype=np.float32)),
                           layout, N, K, _p(y))
     return y
+
+
+def gemv_bf16(x: np.ndarray, w_bits: np.ndarray) -> np.ndarray:
+    """y[t, n] = sum_k x[t, k] * bf16(w[n, k]) (w_bits uint16 [N, K])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, K = x.shape
+    N = w_bits.shape[0]
+    y = np.empty((T, N), dtype=np.float32)
+    lib().oracle_gemv_bf16(_p(x), T, _p(np.ascontiguousarray(w_bits, dtype=np.uint16)), N, K, _p(y))
+    return y
+
+
+def moe_combine_shared(routed: np.ndarray, shared: np.ndarray, gate: np.ndarray) -> np.ndarray:
+    routed = np.ascontiguousarray(routed, dtype=np.float32)
+    T, H = routed.shape
+    out = np.empty((T, H), dtype=np.float32)
+    lib().oracle_moe_combine_shared(_p(routed), _p(np.ascontiguousarray(shared, dtype=np.float32)),
+                                    _p(np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)), _p(out), T, H)
+    return out
+
+
+def moe_layer_decode(x: np.ndarray, router_w_bits: np.ndarray, all_recs, k: int, geo: Fp8Record, shared_rec,
+                     shared_geo: Fp8Record, gate_w_bits: np.ndarray):
+    """(logits, gate, ids, weights, out f32) of one decode MoE layer (router GEMV, routed
+    experts, shared expert gated by sigmoid(x . gate_w))."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    E = router_w_bits.shape[0]
+    logits = np.empty((T, E), dtype=np.float32)
+    gate = np.empty((T, 1), dtype=np.float32)
+    ids = np.empty((T, k), dtype=np.int32)
+    w = np.empty((T, k), dtype=np.float32)
+    out = np.empty((T, geo.hidden), dtype=np.float32)
+    table = _ptrs(all_recs)
+    rc = lib().oracle_moe_layer_decode_fp8(_p(x), T, _p(np.ascontiguousarray(router_w_bits, dtype=np.uint16)),
+                                           _p(table), E, k, ctypes.byref(geo), _p(np.ascontiguousarray(shared_rec)),
+                                           ctypes.byref(shared_geo),
+                                           _p(np.ascontiguousarray(gate_w_bits, dtype=np.uint16)), _p(logits),
+                                           _p(gate), _p(ids), _p(w), _p(out))
+    assert rc == 0
+    return logits, gate, ids, w, out
 
 
 def moe_plan(ids: np.ndarray, E: int):

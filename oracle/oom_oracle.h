@@ -104,6 +104,10 @@ void oracle_router_probs(const float* logits, int T, int E, float* p);
 void oracle_gemv_fp8(const float* x, int T, const uint8_t* q, const float* scale, int layout, int64_t N,
                      int64_t K, float* y);
 
+/* y[t, n] = sum_k x[t, k] * bf16(w[n, k]), fp32, k ascending (the router GEMV).
+ * crates/oominf-cuda/kernels/ops.cu:329-440 (gemv_impl<T, false>). */
+void oracle_gemv_bf16(const float* x, int T, const uint16_t* w, int64_t N, int64_t K, float* y);
+
 /* ---- routed experts ---------------------------------------------------- */
 
 /* Routing plan of one step with every expert resident: slots t*k+s grouped by
@@ -187,4 +191,19 @@ int oracle_host_has_avx512(void);
 #ifdef __cplusplus
 }
 #endif
+
+/* out[t, c] = routed[t, c] + sigmoid(gate[t]) * shared[t, c], sigmoid(v) = 1 / (1 + expf(-v)).
+ * crates/oominf-cuda/kernels/ops.cu:10,310-316 (moe_combine). */
+void oracle_moe_combine_shared(const float* routed, const float* shared, const float* gate, float* out, int T, int H);
+
+/* One decode MoE layer: logits = x Wr^T (bf16 router_w [E, H]), the routed step as
+ * oracle_moe_decode_fp8, the shared expert (record shared_rec, geometry sgeo) as one
+ * expert of weight 1, gate = x . gate_w (bf16 [H]), out = routed + sigmoid(gate) * shared.
+ * crates/oominf-models-qwen/src/moe.rs:254-366 (all routed experts resident) and :498-527.
+ * Returns 0 or -1. */
+int oracle_moe_layer_decode_fp8(const float* x, int T, const uint16_t* router_w, const uint8_t* const* all_recs,
+                                int E, int k, const OomFp8Record* geo, const uint8_t* shared_rec,
+                                const OomFp8Record* sgeo, const uint16_t* gate_w, float* logits, float* gate,
+                                int32_t* ids, float* weights, float* out);
+
 #endif

@@ -101,6 +101,23 @@ void oracle_gemv_fp8(const float* x, int T, const uint8_t* q, const float* scale
         }
 }
 
+/* ---- dense bf16 GEMV (the router) ---------------------------------------------- */
+
+/* ops.cu:329-440 (gemv_impl<T, false>): acc += x * bf16(w), fp32, k ascending. */
+void oracle_gemv_bf16(const float* x, int T, const uint16_t* w, int64_t N, int64_t K, float* y) {
+    for (int t = 0; t < T; t++)
+        for (int64_t n = 0; n < N; n++) {
+            float acc = 0.0f;
+            for (int64_t c = 0; c < K; c++) {
+                uint32_t bits = (uint32_t)w[n * K + c] << 16;
+                float wf;
+                memcpy(&wf, &bits, sizeof(wf));
+                acc += x[(size_t)t * K + c] * wf;
+            }
+            y[(size_t)t * N + n] = acc;
+        }
+}
+
 /* ---- routed experts ---------------------------------------------------------- */
 
 int oracle_moe_plan(const int32_t* ids, int T, int k, int E, int32_t* experts, int32_t* off, int32_t* assign_tok,
@@ -347,4 +364,42 @@ void oracle_attn_decode_paged(const uint16_t* q, const uint16_t* k_pages, const 
     free(qf);
     free(acc);
     free(vrow);
+}
+
+/* ---- the shared expert and the whole decode layer --------------------------------- */
+
+/* ops.cu:10,310-316: out = routed + sigmoid(gate[t]) * shared, sigmoid(v) = 1 / (1 + expf(-v)). */
+void oracle_moe_combine_shared(const float* routed, const float* shared, const float* gate, float* out, int T, int H) {
+    for (int t = 0; t < T; t++) {
+        const float sg = 1.0f / (1.0f + expf(-gate[t]));
+        for (int c = 0; c < H; c++) out[(size_t)t * H + c] = routed[(size_t)t * H + c] + sg * shared[(size_t)t * H + c];
+    }
+}
+
+/* moe.rs:254-366 with every routed expert resident and moe.rs:498-527 (the shared
+ * expert: gemm_w of the stacked gate/up, silu_mul_rows, gemm_w of down; its gate logit by
+ * gemm_w; moe_combine). logits [T, E] and gate [T] are written too. */
+int oracle_moe_layer_decode_fp8(const float* x, int T, const uint16_t* router_w, const uint8_t* const* all_recs,
+                                int E, int k, const OomFp8Record* geo, const uint8_t* shared_rec,
+                                const OomFp8Record* sgeo, const uint16_t* gate_w, float* logits, float* gate,
+                                int32_t* ids, float* weights, float* out) {
+    const int64_t H = geo->hidden;
+    oracle_gemv_bf16(x, T, router_w, E, H, logits);
+    oracle_gemv_bf16(x, T, gate_w, 1, H, gate);
+    float* routed = (float*)malloc(sizeof(float) * (size_t)T * H);
+    float* shared = (float*)malloc(sizeof(float) * (size_t)T * H);
+    int32_t* sids = (int32_t*)malloc(sizeof(int32_t) * (size_t)T);
+    float* sw = (float*)malloc(sizeof(float) * (size_t)T);
+    int rc = oracle_moe_decode_fp8(logits, x, all_recs, T, E, k, geo, ids, weights, routed);
+    if (rc == 0) {
+        /* the shared expert: one expert, weight 1 */
+        const uint8_t* srecs[1] = {shared_rec};
+        rc = oracle_moe_decode_fp8(gate, x, srecs, T, 1, 1, sgeo, sids, sw, shared);
+    }
+    if (rc == 0) oracle_moe_combine_shared(routed, shared, gate, out, T, (int)H);
+    free(routed);
+    free(shared);
+    free(sids);
+    free(sw);
+    return rc;
 }

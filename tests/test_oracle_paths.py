@@ -287,3 +287,67 @@ def test_attention_is_a_convex_combination_and_ignores_page_order():
     for h in range(H):
         rows = vf[phys, np.arange(kv_len) % 16, h // 4].astype(np.float64)
         np.testing.assert_allclose(out3[h], rows.mean(0), atol=2e-6)
+
+
+# ---- the router GEMV (bf16 weights), the shared expert's gated add, the whole layer ----
+
+@pytest.mark.parametrize("T,N,K", [(1, 128, 4096), (3, 17, 512), (16, 8, 1024)])
+def test_gemv_bf16_matches_f64(T, N, K):
+    """The reference's GEMV gate (crates/oominf-cuda/tests/gemv.rs:171-181): max |got - want| / sqrt(K) < 1e-5
+    against f64 over the same bf16 weights."""
+    w = oracle.gaussian_bf16((N, K), 31 + N, 0.02)
+    x = oracle.gaussian(T * K, 32 + K).reshape(T, K).astype(np.float32)
+    got = oracle.gemv_bf16(x, w)
+    want = x.astype(np.float64) @ oracle.bf16_to_f32(w).astype(np.float64).T
+    assert np.abs(got - want).max() / np.sqrt(K) < 1e-5
+
+
+def test_gemv_bf16_closed_form():
+    """w = bf16 1.0 (0x3f80) everywhere: y = sum_k x (exact for small integers); a row of
+    bf16 -2.0 (0xc000) gives -2 sum_k x; bf16 2^-133 (0x0001, a subnormal) times 2^133 is 1."""
+    T, K = 2, 256
+    x = np.arange(T * K, dtype=np.float32).reshape(T, K) % 7 - 3
+    w = np.full((3, K), 0x3F80, dtype=np.uint16)
+    w[1, :] = 0xC000
+    w[2, :] = 0
+    w[2, 0] = 0x0001
+    y = oracle.gemv_bf16(x, w)
+    np.testing.assert_array_equal(y[:, 0], x.sum(axis=1))
+    np.testing.assert_array_equal(y[:, 1], -2.0 * x.sum(axis=1))
+    np.testing.assert_array_equal(y[:, 2], x[:, 0] * np.float32(2.0 ** -133))
+
+
+def test_combine_shared_special_gates():
+    """sigmoid(0) = 1/2 exactly, sigmoid(+inf) = 1, sigmoid(-inf) = 0: out = routed + s * shared."""
+    rng = np.random.default_rng(3)
+    routed = rng.standard_normal((3, 40)).astype(np.float32)
+    shared = rng.standard_normal((3, 40)).astype(np.float32)
+    gate = np.array([0.0, np.inf, -np.inf], dtype=np.float32)
+    out = oracle.moe_combine_shared(routed, shared, gate)
+    np.testing.assert_array_equal(out[0], routed[0] + np.float32(0.5) * shared[0])
+    np.testing.assert_array_equal(out[1], routed[1] + shared[1])
+    np.testing.assert_array_equal(out[2], routed[2])
+
+
+def test_layer_composition_closed_form():
+    """Zero router weights: every logit 0, so the picks are experts 0..k-1 (ties to the lower
+    id) with weights 1/k; zero gate weights: gate 0, so out = routed + shared / 2, where routed
+    is the decode step over experts 0..k-1 and shared the shared record's FFN at weight 1."""
+    E, k, H, I, SI, T = 12, 4, 256, 128, 256, 3
+    geo, sgeo = oracle.record_geometry(H, I), oracle.record_geometry(H, SI)
+    recs = synth.expert_records(geo, 61, E)
+    srec = synth.expert_records(sgeo, 62, 1)[0]
+    x = oracle.bf16_to_f32(synth.activations_bf16(63, T, H))
+    rw = np.zeros((E, H), dtype=np.uint16)
+    gw = np.zeros((1, H), dtype=np.uint16)
+    logits, gate, ids, w, out = oracle.moe_layer_decode(x, rw, recs, k, geo, srec, sgeo, gw)
+    assert (logits == 0).all() and (gate == 0).all()
+    np.testing.assert_array_equal(ids, np.tile(np.arange(k, dtype=np.int32), (T, 1)))
+    np.testing.assert_array_equal(w, np.full((T, k), 1.0 / k, dtype=np.float32))
+    _, _, routed = oracle.moe_decode(np.zeros((T, E), np.float32), x, recs, k, geo)
+    sids, sw, shared = oracle.moe_decode(np.zeros((T, 1), np.float32), x, [srec], 1, sgeo)
+    assert (sids == 0).all() and (sw == 1.0).all()
+    np.testing.assert_array_equal(out, routed + np.float32(0.5) * shared)
+    # the shared FFN against f64 over the dequantised record (weight 1, one token at a time)
+    f64 = synth.f64_moe((np.zeros((T, 1), np.int32), np.ones((T, 1), np.float32)), x, [srec], sgeo)
+    assert np.abs(shared - f64).max() <= 2e-5 * np.abs(f64).max()
