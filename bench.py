@@ -8,7 +8,8 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 (2 x 2.42 GB) alternate between steps so weights stream from HBM, not from the
 256 MB Infinity Cache.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config decode1|decode16|gemv]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--config decode1|decode16|layer1|layer16|attn|prefill|copy]
 
 Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
 kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
@@ -330,6 +331,135 @@ def bench_attn(args):
     return res
 
 
+def cpu_baseline_layer(host_recs, shared_rec, rw_bits, gw_bits, geo, sgeo, E, k, T, budget_s=10.0):
+    """The reference CPU path of a whole decode MoE layer (oracle restatement of
+    crates/oominf-cpu): router GEMV over bf16 weights, top-k, plan, HostExperts for the
+    routed experts and the shared expert, the shared gate GEMV, slot-order combine and the
+    sigmoid-gated add, fresh activations each step, for about `budget_s` seconds.
+    Returns (us_per_token, cores, steps)."""
+    import numpy as np
+
+    import oracle
+
+    cores = usable_cores()
+    rng = np.random.default_rng(6)
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        x = oracle.bf16_to_f32(oracle.bf16_from_f32(rng.standard_normal((T, geo.hidden)).astype(np.float32)))
+        logits = oracle.gemv_bf16(x, rw_bits)
+        ids, w = oracle.router_topk(logits, k)
+        experts, off, tok, slot = oracle.moe_plan(ids, E)
+        jobs = [tok[off[i]:off[i + 1]] for i in range(len(experts))]
+        y = oracle.host_experts(geo, [host_recs[e] for e in experts], jobs, x, cores)
+        routed = oracle.moe_combine_slots(y, slot, w)
+        shared = oracle.host_experts(sgeo, [shared_rec], [np.arange(T, dtype=np.int32)], x, cores)
+        gate = oracle.gemv_bf16(x, gw_bits)
+        oracle.moe_combine_shared(routed, shared, gate)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and steps >= 3:
+            break
+    return el / steps / T * 1e6, cores, steps
+
+
+def bench_layer(args, T, config):
+    """A whole decode MoE layer per step through oom_moe_layer_decode_fp8: router GEMV over
+    bf16 weights [128, 4096] from N(0, 0.02), top-8, the routed experts of the decode
+    workload (hidden 4096, inter 1536, e4m3 128x128-block-scaled), one shared expert of the
+    same geometry with a sigmoid gate over bf16 weights [4096], bf16 x from N(0, 1) fresh
+    each step. Two sets of every weight alternate between steps so all of them stream
+    from HBM."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    E, k, H, I, SI = 128, 8, 4096, 1536, 1536
+    geo, sgeo = hip.record_geometry(H, I), hip.record_geometry(H, SI)
+    stride, sstride = hip.record_stride(geo), hip.record_stride(sgeo)
+    log(f"bench: layer T={T} E={E} k={k} H={H} I={I} shared inter {SI}; building 2 expert sets of "
+        f"{E * stride / 1e9:.2f} GB")
+    sets = [make_expert_set(E, geo, stride, 1234 + s, torch) for s in range(2)]
+    addrs = [torch.tensor([b.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
+             for b in sets]
+    shared = make_expert_set(2, sgeo, sstride, 777, torch)
+    saddrs = [torch.tensor([shared.data_ptr() + s * sstride], dtype=torch.int64, device="cuda") for s in range(2)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(98)
+    rws = [(torch.randn((E, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16) for _ in range(2)]
+    gws = [(torch.randn((1, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16) for _ in range(2)]
+    n = args.warmup + args.steps
+    xs = torch.randn((n, T, H), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ids = torch.empty((n, T, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n, T, k), dtype=torch.float32, device="cuda")
+    ws = torch.zeros(hip.moe_layer_decode_fp8_workspace_size(T, E, k, geo, sgeo), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        s = i % 2
+        hip.moe_layer_decode_fp8(xs[i], rws[s], addrs[s], k, geo, saddrs[s], sgeo, gws[s], ids[i], wts[i], out, ws,
+                                 stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(args.warmup, n):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    # algorithmic bytes: each distinct routed expert once, the shared expert, the router
+    # and gate weights, x and out
+    idn = ids[args.warmup:].cpu().numpy()
+    distinct = np.array([len(np.unique(s_)) for s_ in idn])
+    per_expert = 3 * H * I + 3 * (H // 128) * (I // 128) * 4
+    per_shared = 3 * H * SI + 3 * (H // 128) * (SI // 128) * 4
+    bytes_step = float(distinct.mean()) * per_expert + per_shared + (E + 1) * H * 2 + 2 * T * H * 2
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    res = {
+        "metric": METRIC,
+        "value": ms * 1e3 / T,
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 expert weights, bf16 router/gate weights and activations, fp32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": f"whole decode MoE layer, batch {T}: bf16 router GEMV 128 x 4096, 128 experts top-8, "
+                               "hidden 4096, inter 1536, plus one shared expert (inter 1536) with a sigmoid gate; "
+                               "e4m3 128x128-block-scaled expert weights from N(0,0.02), bf16 x fresh each step; "
+                               "2 sets of all weights alternate past the MALL",
+                   "batch": T, "experts": E, "top_k": k, "hidden": H, "inter": I, "shared_inter": SI,
+                   "distinct_experts_per_step": float(distinct.mean())},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": measured_traffic(config),
+                     "kernel": "oom_moe_layer_decode_fp8 step (router and gate GEMVs, routed and shared decode "
+                               "kernels, gated combine)",
+                     "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
+    }
+    if not args.no_cpu:
+        import oracle
+
+        host = sets[0].cpu().numpy()
+        ogeo, osgeo = oracle.record_geometry(H, I), oracle.record_geometry(H, SI)
+        rw_bits = rws[0].view(torch.int16).cpu().numpy().view(np.uint16)
+        gw_bits = gws[0].view(torch.int16).cpu().numpy().view(np.uint16)
+        us, cores, nsteps = cpu_baseline_layer([host[e] for e in range(E)], shared[0].cpu().numpy(), rw_bits, gw_bits,
+                                               ogeo, osgeo, E, k, T, args.cpu_seconds)
+        res["cpu_baseline"] = {"value": us, "unit": "us/token", "cores": cores, "kind": "port",
+                               "sample": f"{nsteps} steps of the same batch-{T} whole decode MoE layer (fresh x), "
+                                         f"oracle restatement of the reference CPU path on {cpu_model()}"}
+    return res
+
+
 PEAK_FP8_TFLOPS = 5000.0
 
 
@@ -429,7 +559,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "attn", "prefill", "copy"])
+    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "attn", "prefill",
+                                                            "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -451,6 +582,8 @@ def main():
         res = bench_prefill(args)
     elif args.config == "decode1":
         res = bench_decode(args, 1, None, args.config)
+    elif args.config in ("layer1", "layer16"):
+        res = bench_layer(args, 1 if args.config == "layer1" else 16, args.config)
     else:
         res = bench_decode(args, 16, 1.1, args.config)
     print(json.dumps(res), flush=True)

@@ -195,11 +195,17 @@ __device__ __forceinline__ float wave_sum_multi(float (&v)[N], int lane) {
     for (int o = TOP; o >= 1; o >>= 1) {
         if (count > 1) {
             const int half = count / 2;
-            const bool upper = (lane & o) != 0;
+            // lanes with bit o set send the lower half; the choice is a bit blend through a
+            // mask the compiler cannot see through: written as `upper ? v[i] : v[i + half]`
+            // it becomes one read of v at a lane-varying index, lowered to a compare and
+            // select over every element of v
+            uint32_t m = (lane & o) ? ~0u : 0u;
+            asm("" : "+v"(m));
 #pragma unroll
             for (int i = 0; i < half; i++) {
-                float send = upper ? v[i] : v[i + half];
-                float keep = upper ? v[i + half] : v[i];
+                const uint32_t lo = __float_as_uint(v[i]), hi = __float_as_uint(v[i + half]);
+                const float send = __uint_as_float((lo & m) | (hi & ~m));
+                const float keep = __uint_as_float((hi & m) | (lo & ~m));
                 v[i] = keep + lane_xor_n(send, o, lane);
             }
             count = half;

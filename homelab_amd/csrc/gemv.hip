@@ -39,22 +39,9 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
     const int klen = KCH * 1024;
     const int k0 = split * klen;
     const int kl = min(K, k0 + klen) - k0;
-    // stage x[t, k0 .. k0 + kl) in lane order (zeros past kl and for padded tokens)
-    float* xs = reinterpret_cast<float*>(xs4);
-    for (int i = threadIdx.x; i < T * klen; i += blockDim.x) {
-        int t = i / klen, kk = i - t * klen;
-        int c = kk >> 10, w = kk & 1023, l = w >> 4, j = w & 15;
-        float v = (t < tn && kk < kl) ? load_act<XDT>(x, (size_t)t * K + k0 + kk) : 0.0f;
-        xs[(((t * KCH + c) * 4 + (j >> 2)) * 64 + l) * 4 + (j & 3)] = v;
-    }
-    __syncthreads();
-
     const int row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
     const int nkb = (K + 127) >> 7;
-    float acc[T * R];
-#pragma unroll
-    for (int i = 0; i < T * R; i++) acc[i] = 0.0f;
-
+    // the weights first: their loads are in flight while x is staged
     constexpr int NW = WB ? 2 : 1;  // 16-byte loads per lane per (row, chunk)
     uint4 w[R][KCH][NW];
 #pragma unroll
@@ -69,6 +56,57 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
                                       : make_uint4(0, 0, 0, 0);
         }
     }
+
+    // stage x[t, k0 .. k0 + kl) in lane order (zeros past kl and for padded tokens): element
+    // kk = c * 1024 + 16 l + j of token t sits at float index
+    // (((t * KCH + c) * 4 + j / 4) * 64 + l) * 4 + j % 4
+    float* xs = reinterpret_cast<float*>(xs4);
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        // 16-byte loads (8 bf16 or 4 f32 of one lane's 16 columns), all issued before the
+        // first LDS store; K % 16 == 0 keeps a load inside one row and on one side of kl
+        constexpr int EPL = XDT == OOM_BF16 ? 8 : 4;
+        constexpr int NV = T * KCH * 1024 / EPL;
+        constexpr int NLD = (NV + 255) / 256;
+        uint4 v[NLD];
+#pragma unroll
+        for (int n = 0; n < NLD; n++) {
+            const int i = threadIdx.x + 256 * n;
+            const int t = i * EPL / klen, kk = i * EPL - t * klen;
+            const bool ok = i < NV && t < tn && kk < kl;
+            const size_t e = (size_t)t * K + k0 + kk;
+            v[n] = ok ? *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + e * (XDT == OOM_BF16 ? 2 : 4))
+                      : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int n = 0; n < NLD; n++) {
+            const int i = threadIdx.x + 256 * n;
+            if (i >= NV) break;
+            const int t = i * EPL / klen, kk = i * EPL - t * klen;
+            const int c = kk >> 10, l = (kk & 1023) >> 4, j = kk & 15;
+            float4* dst = &xs4[((t * KCH + c) * 4 + (j >> 2)) * 64 + l];
+            if constexpr (XDT == OOM_BF16) {
+                dst[0] = make_float4(__uint_as_float(v[n].x << 16), __uint_as_float(v[n].x & 0xffff0000u),
+                                     __uint_as_float(v[n].y << 16), __uint_as_float(v[n].y & 0xffff0000u));
+                dst[64] = make_float4(__uint_as_float(v[n].z << 16), __uint_as_float(v[n].z & 0xffff0000u),
+                                      __uint_as_float(v[n].w << 16), __uint_as_float(v[n].w & 0xffff0000u));
+            } else {
+                dst[0] = make_float4(__uint_as_float(v[n].x), __uint_as_float(v[n].y), __uint_as_float(v[n].z),
+                                     __uint_as_float(v[n].w));
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < T * klen; i += blockDim.x) {
+            int t = i / klen, kk = i - t * klen;
+            int c = kk >> 10, l = (kk & 1023) >> 4, j = kk & 15;
+            float v = (t < tn && kk < kl) ? load_act<XDT>(x, (size_t)t * K + k0 + kk) : 0.0f;
+            xs[(((t * KCH + c) * 4 + (j >> 2)) * 64 + l) * 4 + (j & 3)] = v;
+        }
+    }
+    __syncthreads();
+
+    float acc[T * R];
+#pragma unroll
+    for (int i = 0; i < T * R; i++) acc[i] = 0.0f;
 #pragma unroll
     for (int c = 0; c < KCH; c++) {
         int col = k0 + c * 1024 + lane * 16;
