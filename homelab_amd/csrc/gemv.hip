@@ -16,8 +16,11 @@
 //   - splits > 1 write fp32 partials [splits, T, N]; the last block of a row tile
 //     (a ticket per tile, reset after use) adds them in split order, so the result
 //     does not depend on block timing (crates/oominf-cuda/kernels/ops.cu:421-439);
+//   - bf16 rows with few rows (N <= 512) and few tokens (T <= 4) take one row a wave and
+//     up to 4 chunks a block, so a K of 4096 needs no split: the latency of the ticketed
+//     sum is most of such a call;
 //   - the workspace holds the tickets first, in an area sized for the most tiles any
-//     T can have at this N (rows / 8), then the partials: a workspace left by a call
+//     T can have at this N (rows / 4), then the partials: a workspace left by a call
 //     of another T or K still has zero tickets where this call looks (partials are
 //     written before they are read), so calls with one N share a workspace.
 #include "common.hpp"
@@ -191,10 +194,19 @@ static GemvPlan gemv_plan(int T, int64_t N, int64_t K, bool wb = false) {
     GemvPlan p;
     p.tp = T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 16;
     p.R = p.tp >= 8 ? 2 : 4;
+    int kchunks = (int)cdiv(K, 1024);
+    if (wb && p.tp <= 4 && N <= 512) {
+        // one row a wave, up to 4 chunks (x of a split: tp * 4 * 4 KiB <= 64 KiB)
+        p.R = 1;
+        p.tiles = (int)cdiv(N, (int64_t)GEMV_WAVES);
+        p.kch = kchunks <= 1 ? 1 : kchunks <= 2 ? 2 : 4;
+        p.splits = (int)cdiv(kchunks, p.kch);
+        p.lds = (size_t)p.tp * p.kch * 1024 * sizeof(float);
+        return p;
+    }
     // x of one split in LDS: tp * kch * 4 KiB <= 64 KiB
     int kch_max = std::max(1, 16 / p.tp);
     kch_max = std::min(kch_max, wb ? 2 : 4);  // bf16 rows take twice the registers per chunk
-    int kchunks = (int)cdiv(K, 1024);
     p.tiles = (int)cdiv(N, (int64_t)GEMV_WAVES * p.R);
     // enough blocks to cover the CUs (>= 512 blocks), but a split never shorter than 1 KiB
     int want = (int)std::max<int64_t>(1, cdiv(512, p.tiles));
@@ -237,7 +249,8 @@ static void launch_gemv_k(const GemvPlan& p, int sl, int xdt, int ydt, const voi
         case 1: launch_gemv<T, R, 1, WB>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
         case 2: launch_gemv<T, R, 2, WB>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st); break;
         default:
-            if constexpr (T <= 4 && !WB) launch_gemv<T, R, 4, WB>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st);
+            if constexpr (T <= 4 && (!WB || R == 1))
+                launch_gemv<T, R, 4, WB>(p, sl, xdt, ydt, x, q, s, y, part, tk, tn, N, K, st);
             break;
     }
 }
@@ -245,8 +258,8 @@ static void launch_gemv_k(const GemvPlan& p, int sl, int xdt, int ydt, const voi
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Bytes of the ticket area at the start of a GEMV workspace: one ticket per row tile at the
-// smallest tile (two rows per wave, 8 rows), whatever T is.
-static size_t gemv_ticket_bytes(int64_t N) { return align256((size_t)cdiv(N, (int64_t)GEMV_WAVES * 2) * sizeof(uint32_t)); }
+// smallest tile (one row per wave, 4 rows), whatever T is.
+static size_t gemv_ticket_bytes(int64_t N) { return align256((size_t)cdiv(N, (int64_t)GEMV_WAVES) * sizeof(uint32_t)); }
 
 static size_t gemv_ws_bytes(const GemvPlan& p, int64_t N) {
     if (p.splits == 1) return 0;
@@ -325,9 +338,16 @@ extern "C" int oom_gemv_bf16(const void* x, int x_dtype, const uint16_t* w, void
     const int n = (int)N, k = (int)K;
     const uint8_t* q = reinterpret_cast<const uint8_t*>(w);
     switch (p.tp) {
-        case 1: launch_gemv_k<1, 4, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
-        case 2: launch_gemv_k<2, 4, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
-        case 4: launch_gemv_k<4, 4, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
+#define GEMV_BF16_T(TP)                                                                                          \
+    if (p.R == 1)                                                                                                \
+        launch_gemv_k<TP, 1, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st);   \
+    else                                                                                                         \
+        launch_gemv_k<TP, 4, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st);   \
+    break;
+        case 1: GEMV_BF16_T(1)
+        case 2: GEMV_BF16_T(2)
+        case 4: GEMV_BF16_T(4)
+#undef GEMV_BF16_T
         case 8: launch_gemv_k<8, 2, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
         default: launch_gemv_k<16, 2, true>(p, OOM_SCALE_ROW, x_dtype, y_dtype, x, q, nullptr, y, part, tk, T, n, k, st); break;
     }

@@ -4,8 +4,13 @@
 // half of Moe::forward (crates/oominf-models-qwen/src/moe.rs:254-366) with every routed
 // expert resident, and Moe::shared (moe.rs:498-527).
 //
-// The shared expert is an FP8 record of the routed experts' format (gate, up, down with
-// 128 x 128 block scales, hidden x shared_inter). It runs through the same one-launch decode
+// One token with bf16 activations and a shared expert of the routed geometry takes two
+// launches: the router GEMV, then the one-token decode kernel with the shared expert as one
+// more plan slot (its gate/up rows beside the routed ones, one row pair of each down tile
+// per wave) and the gate logit and gated add inside it.
+//
+// Otherwise the shared expert is an FP8 record of the routed experts' format (gate, up, down
+// with 128 x 128 block scales, hidden x shared_inter). It runs through the same one-launch decode
 // step as a single expert with top-1 routing: softmax over one logit is exactly 1, so the
 // step computes down(silu(x Wg^T) * (x Wu^T)) with weight 1, which is the reference's
 // gemm_w(gate_up) -> silu_mul_rows -> gemm_w(down) (moe.rs:507-513) in the same fp32
@@ -22,6 +27,10 @@ extern "C" size_t oom_gemv_bf16_workspace_size(int T, int64_t N, int64_t K);
 
 namespace oom {
 int check_geo(const OomFp8Record* g, const char* who);
+bool fused_shared_supported(int T, int E, int k, const OomFp8Record& g, const OomFp8Record& sg, int xdt);
+int launch_fused_shared(const float* logits, const void* x, const uint64_t* all_recs, int E, int k,
+                        const OomFp8Record& g, const uint64_t* shared_rec, const uint16_t* gate_w, float* gate,
+                        int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st);
 
 // out[t, c] = routed[t, c] + sigmoid(gate[t]) * shared[t, c], sigmoid(v) = 1 / (1 + e^-v)
 // (crates/oominf-cuda/kernels/ops.cu:10,310-316). Four columns per thread.
@@ -138,9 +147,13 @@ extern "C" int oom_moe_layer_decode_fp8(const void* x, int x_dtype, const uint16
     const int64_t H = geo->hidden;
     // router logits [T, E] and the shared expert's gate logit [T] (Moe::forward's gemm_w of
     // the router, moe.rs:290-298; Moe::shared's gate, moe.rs:515-524)
+    OOM_REQUIRE(k >= 1 && k <= 32 && E >= k && E <= 8192, "oom_moe_layer_decode_fp8: router top-k > 32 or experts > 8192");
     if (int rc = oom_gemv_bf16(x, x_dtype, router_w, logits, OOM_F32, T, E, H, base + w.rgemv, w.ggemv - w.rgemv,
                                stream))
         return rc;
+    if (fused_shared_supported(T, E, k, *geo, *shared_geo, x_dtype))
+        return launch_fused_shared(logits, x, all_recs, E, k, *geo, shared_rec, shared_gate_w, gate, ids, weights, out,
+                                   out_dtype, dws, as_stream(stream));
     if (int rc = oom_gemv_bf16(x, x_dtype, shared_gate_w, gate, OOM_F32, T, 1, H, base + w.ggemv, w.decode - w.ggemv,
                                stream))
         return rc;

@@ -21,6 +21,11 @@
 //    b, b + G, ... for every expert (two expert slots per wave), so a tile's expert rows
 //    meet in LDS and the slot-order combine needs no y buffer, ticket or second trip
 //    to memory.
+//  * With a shared expert (one token, the whole decode layer): the shared record is plan
+//    slot k, so its gate/up rows are phase-1 items like the routed ones; in phase 2 each
+//    wave also takes one row pair of the shared expert's 16-row tile, and the combine adds
+//    sigmoid(gate) times the shared row after the routed slot sum. The gate logit
+//    x . gate_w is one wave's dot product during routing (x is already in its registers).
 // Weights, scales and activations load through buffer resources: a lane or an item
 // past the end reads zeros (out-of-range offset, or an empty resource) without a
 // branch or a memory access. Counters see one arrival per block (barrier) or per
@@ -60,6 +65,11 @@ struct FusedArgs {
     uint32_t* status;    // 1 if a wait gave up (results invalid)
     int h_bytes;         // bytes of h (bounds of its buffer resource)
     int rec_bytes;       // bytes of a record up to the end of its last part
+    // the shared expert (one token, SH): its record address at shared_rec[0] (same geometry
+    // as the routed records), the bf16 gate row [H], and where the gate logit is handed over
+    const uint64_t* shared_rec;
+    const uint16_t* gate_w;
+    float* gate;
 };
 
 // 16 consecutive activations of row `row` starting at column `col`, as fp32.
@@ -88,7 +98,7 @@ __device__ __forceinline__ void load16(const void* base, size_t off, float* v) {
 }
 
 struct PlanLds {
-    uint64_t recs[F_EMAX];  // all_recs, read once per block
+    uint64_t recs[F_EMAX + 1];  // all_recs, read once per block (+ the shared expert's record)
     uint64_t keys[FW1];     // one-token routing scratch (route_select)
     float p[FW1];
     int n_e;
@@ -470,6 +480,79 @@ __device__ __forceinline__ float down1_rows(const Down1<DCH>& d, const float (&h
     return wave_sum_multi<FD1_NP, 16>(acc, lane);
 }
 
+// One row pair of the shared expert's down tile: row 16 tile + 2 w + (lane >= 32) for wave
+// w, DCH chunks of 512 columns (lane l % 32 takes 16 columns of each), read through the
+// record of plan slot `slot` (the shared expert).
+template <int DCH>
+struct DownPair {
+    uint4 w[DCH];
+    float s[DCH];
+};
+
+template <int DCH>
+__device__ __forceinline__ void down_pair_load(const FusedArgs& a, const PlanLds& pl, int slot, int tile, int wave,
+                                               bool valid, int lane, DownPair<DCH>& d) {
+    const int H = (int)a.H, I = (int)a.I, nkb = (I + 127) >> 7;
+    const int row = tile * 2 * FD1_NP + 2 * wave + (lane >> 5), l = lane & 31;
+    const bool ok = valid && row < H;
+    const __amdgpu_buffer_rsrc_t r = rec_rsrc(pl, slot, ok ? a.rec_bytes : 0);
+#pragma unroll
+    for (int c = 0; c < DCH; c++) {
+        const int col = c * 512 + l * 16;
+        d.w[c] = ld16(r, ok && col < I ? (int)a.dw + row * I + col : OOB);
+        d.s[c] = ldf(r, ok && col < I ? (int)a.ds + ((row >> 7) * nkb + (col >> 7)) * 4 : OOB);
+    }
+}
+
+// The pair's row totals: row 2 w in every lane of the lower half, row 2 w + 1 in the upper.
+template <int DCH>
+__device__ __forceinline__ float down_pair_row(const DownPair<DCH>& d, const float (&hv)[DCH][16], int lane) {
+    float s[1] = {0.0f};
+#pragma unroll
+    for (int c = 0; c < DCH; c++) {
+        float f[16];
+        e4m3x16(d.w[c], f);
+        float q0 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) q0 = fmaf(f[q], hv[c][q], q0);
+        s[0] = fmaf(q0, d.s[c], s[0]);
+    }
+    return wave_sum_multi<1, 16>(s, lane);
+}
+
+// The shared expert's gate logit x . gate_w (bf16 [H]) from the token's activations in
+// registers: lane l's 16 columns of each chunk, summed over the wave.
+template <int XDT>
+__device__ __forceinline__ float gate_dot(const FusedArgs& a, const XRow<XDT>& xr, int lane) {
+    const int H = (int)a.H;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.gate_w), (short)0,
+                                                                      H * 2, BUF_FLAGS);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int col = c * 1024 + lane * 16;
+        const int off = col < H ? col * 2 : OOB;
+        const uint4 g0 = ld16(r, off), g1 = ld16(r, off + 16);
+        const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        float p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float x0, x1;
+            if constexpr (XDT == OOM_BF16) {
+                x0 = __uint_as_float(xr.w[c][i] << 16);
+                x1 = __uint_as_float(xr.w[c][i] & 0xffff0000u);
+            } else {
+                x0 = xr.v[c][2 * i];
+                x1 = xr.v[c][2 * i + 1];
+            }
+            p = fmaf(__uint_as_float(gw[i] << 16), x0, p);
+            p = fmaf(__uint_as_float(gw[i] & 0xffff0000u), x1, p);
+        }
+        acc += p;
+    }
+    return wave_sum(acc);
+}
+
 // Grid-wide barrier over the workspace header's barrier words (stream.hpp). Used once per kernel.
 __device__ __forceinline__ void grid_barrier(const FusedArgs& a) { grid_barrier_words(a.bar, a.status, F_SPIN_LIMIT); }
 
@@ -508,8 +591,9 @@ __device__ __forceinline__ void plan_wave(PlanLds& pl, int A, int k, int lane) {
     }
 }
 
-template <int TG, int DCH, int EQ, int XDT, int ODT>
+template <int TG, int DCH, int EQ, int XDT, int ODT, bool SH = false>
 __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused_kernel(FusedArgs a) {
+    static_assert(!SH || TG == 1, "the shared expert rides the one-token kernel");
     constexpr int WB = TG == 1 ? FW1 : FW;  // waves per block
     __shared__ PlanLds pl;
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
@@ -517,6 +601,9 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
     const int T = a.T, E = a.E, k = a.k, A = T * k;
     // the record table and (one token) the activations load while the router runs
     if (tid < E) pl.recs[tid] = a.all_recs[tid];
+    if constexpr (SH) {
+        if (tid == E) pl.recs[E] = a.shared_rec[0];
+    }
     XRow<XDT> xr;
     if constexpr (TG == 1) xrow_load<XDT>(a.x, (int)a.H, lane, xr);
     // ---- routing and plan: slots sorted by (expert, slot), experts in id order ----
@@ -534,6 +621,18 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
                 pl.n_e = k;
                 pl.off[k] = k;
                 pl.claims = 0u;
+                if constexpr (SH) {
+                    // plan slot k: the shared expert (record E of the table), h row k
+                    pl.experts[k] = E;
+                    pl.off[k + 1] = k + 1;
+                }
+            }
+        }
+        if constexpr (SH) {
+            // while wave 0 routes, wave 1 of block 0 takes the shared expert's gate logit
+            if (blockIdx.x == 0 && wave == 1) {
+                const float g = gate_dot<XDT>(a, xr, lane);
+                if (lane == 0) st_dev(a.gate, g);
             }
         }
     } else {
@@ -590,7 +689,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
     if constexpr (TG == 1) {
         // ---- phase 1, one token: item it = (expert it / I, row it % I); the next item's
         // loads are in flight while the current one is reduced ----
-        const int NG = n_e * (int)a.I;
+        const int NG = (n_e + (SH ? 1 : 0)) * (int)a.I;  // the shared expert's rows last
         // Block b owns items b WB + c % WB + (c / WB) NW (c = 0, 1, ...); its waves claim
         // them in that order from a counter in LDS, so a wave that gets fewer issue slots
         // (the second wave of a SIMD) takes fewer items than its partner.
@@ -623,13 +722,31 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
         // ---- phase 2, one token: the slot's h once, then per tile the 16 rows of each
         // expert into LDS and the slot-order combine by wave 0 ----
         __shared__ float ylds[FW1][2 * FD1_NP];
+        __shared__ float ysh[2 * FD1_NP];
         float h0[DCH][16];
         down1_h<DCH>(a, pl.off[s0 < n_e ? s0 : 0], s0 < n_e, lane, h0);
+        float hs[DCH][16];
+        float sg = 0.0f;
+        DownPair<DCH> p0;
+        if constexpr (SH) {
+            // the shared row pair's weights load after the barrier (3 loads a lane), out of
+            // phase 1's register budget
+            down_pair_load<DCH>(a, pl, k, tb0, wave, tb0 < tiles1, lane, p0);
+            down1_h<DCH>(a, k, true, lane, hs);
+            if (wave == 0) sg = 1.0f / (1.0f + expf(-ld_dev(a.gate)));  // sigmoid (ops.cu:10)
+        }
         const int prow = 2 * ((lane & 31) >> 2) + (lane >> 5);  // this lane group's row in the tile
         for (int tb = tb0; tb < tiles1; tb += gridDim.x) {
-            if (tb != tb0) down1_load<DCH>(a, pl, s0, tb, s0 < n_e, lane, d0);
+            if (tb != tb0) {
+                down1_load<DCH>(a, pl, s0, tb, s0 < n_e, lane, d0);
+                if constexpr (SH) down_pair_load<DCH>(a, pl, k, tb, wave, true, lane, p0);
+            }
             const float y0 = down1_rows<DCH>(d0, h0, lane);
             if ((lane & 3) == 0) ylds[s0][prow] = y0;
+            if constexpr (SH) {
+                const float ys = down_pair_row<DCH>(p0, hs, lane);
+                if ((lane & 31) == 0) ysh[2 * wave + (lane >> 5)] = ys;
+            }
             __syncthreads();
             // out[r] = sum over slots in order of w[s] * y[slot_assign[s]][r]; with one
             // token, assignment i is expert slot i
@@ -637,6 +754,9 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             if (wave == 0 && lane < 2 * FD1_NP && r < (int)a.H) {
                 float acc = 0.0f;
                 for (int s = 0; s < k; s++) acc = fmaf(pl.w[s], ylds[pl.slot_assign[s]][lane], acc);
+                // the shared expert after the routed sum: routed + sigmoid(gate) * shared
+                // (moe_combine, ops.cu:310-316)
+                if constexpr (SH) acc = acc + sg * ysh[lane];
                 store_out<ODT>(a.out, r, acc);
             }
             __syncthreads();
@@ -675,7 +795,7 @@ static FusedWs fused_ws(int T, int E, int k, const OomFp8Record& g) {
     FusedWs w;
     size_t A = (size_t)T * k;
     w.h = WS_HEADER;
-    w.y = w.h + al256(A * (size_t)g.inter * sizeof(float));
+    w.y = w.h + al256((A + 1) * (size_t)g.inter * sizeof(float));  // + a shared expert's h row
     w.total = w.y + al256(A * (size_t)g.hidden * sizeof(float));
     return w;
 }
@@ -688,39 +808,40 @@ bool fused_supported(int T, int E, int k, const OomFp8Record& g) {
 size_t fused_workspace_size(int T, int E, int k, const OomFp8Record& g) { return fused_ws(T, E, k, g).total; }
 
 // Blocks of the fused kernel that fit on the device at once (all must be resident).
-template <int TG, int DCH, int EQ, int XDT, int ODT>
+template <int TG, int DCH, int EQ, int XDT, int ODT, bool SH>
 static int resident_blocks(int dev, size_t lds) {
     int cus = 0, per = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT, SH>,
                                                      TG == 1 ? 64 * FW1 : 64 * FW, lds) !=
         hipSuccess)
         return 0;
     return cus * per;
 }
 
-template <int TG, int DCH, int EQ, int XDT, int ODT>
+template <int TG, int DCH, int EQ, int XDT, int ODT, bool SH = false>
 static int launch_fused_t(const FusedArgs& a, size_t lds, hipStream_t st) {
     static thread_local int cached_dev = -1, cached_blocks = 0;
     static thread_local size_t cached_lds = 0;
     int dev = 0;
     (void)hipGetDevice(&dev);
     if (dev != cached_dev || lds != cached_lds) {
-        cached_blocks = resident_blocks<TG, DCH, EQ, XDT, ODT>(dev, lds);
+        cached_blocks = resident_blocks<TG, DCH, EQ, XDT, ODT, SH>(dev, lds);
         cached_dev = dev;
         cached_lds = lds;
     }
     if (cached_blocks <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
     // never more waves than items (at most min(E, A) experts' worth)
     const int wb = TG == 1 ? FW1 : FW;
-    const int64_t items = (int64_t)std::min(a.E, a.T * a.k) * (cdiv(a.I, TG == 1 ? 1 : FG_R) + cdiv(a.H, FD_R));
+    const int64_t items =
+        ((int64_t)std::min(a.E, a.T * a.k) + (SH ? 1 : 0)) * (cdiv(a.I, TG == 1 ? 1 : FG_R) + cdiv(a.H, FD_R));
     const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, cdiv(items, wb)));
-    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT>), dim3(blocks), dim3(64 * wb), lds, st, a);
+    hipLaunchKernelGGL((moe_decode_fused_kernel<TG, DCH, EQ, XDT, ODT, SH>), dim3(blocks), dim3(64 * wb), lds, st, a);
     return launched("oom_moe_decode_fp8");
 }
 
-int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* all_recs, int T, int E, int k,
-                 const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st) {
+static FusedArgs fused_args(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
+                            const OomFp8Record& g, int32_t* ids, float* weights, void* out, void* ws) {
     FusedWs w = fused_ws(T, E, k, g);
     uint8_t* base = reinterpret_cast<uint8_t*>(ws);
     FusedArgs a;
@@ -748,6 +869,15 @@ int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* al
     a.status = reinterpret_cast<uint32_t*>(base + WS_STATUS);
     a.h_bytes = (int)((size_t)T * k * g.inter * sizeof(float));
     a.rec_bytes = (int)record_span(g);
+    a.shared_rec = nullptr;
+    a.gate_w = nullptr;
+    a.gate = nullptr;
+    return a;
+}
+
+int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* all_recs, int T, int E, int k,
+                 const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st) {
+    const FusedArgs a = fused_args(logits, x, all_recs, T, E, k, g, ids, weights, out, ws);
     const size_t lds = 0;
 #define FUSED_CASE(TG, DCH, EQ)                                                                               \
     if (xdt == OOM_BF16 && odt == OOM_BF16) return launch_fused_t<TG, DCH, EQ, OOM_BF16, OOM_BF16>(a, lds, st); \
@@ -778,6 +908,46 @@ int launch_fused(const float* logits, const void* x, int xdt, const uint64_t* al
         FUSED_CASE(4, 0, 4)
     }
 #undef FUSED_CASE
+}
+
+// One token through the one-token kernel with a shared expert of the routed geometry as
+// plan slot k: out = sum_s w_s y_s + sigmoid(x . gate_w) * y_shared. The gate logit is
+// handed over at `gate` (device memory the caller owns). bf16 activations only.
+bool fused_shared_supported(int T, int E, int k, const OomFp8Record& g, const OomFp8Record& sg, int xdt) {
+    // inter <= 1536: with 2048 the two h rows and a down tile pass the register budget
+    return T == 1 && k <= FW1 && xdt == OOM_BF16 && g.inter <= 1536 && fused_supported(T, E, k, g) &&
+           g.hidden == sg.hidden &&
+           g.inter == sg.inter && g.gate_weight == sg.gate_weight && g.gate_scale == sg.gate_scale &&
+           g.up_weight == sg.up_weight && g.up_scale == sg.up_scale && g.down_weight == sg.down_weight &&
+           g.down_scale == sg.down_scale;
+}
+
+int launch_fused_shared(const float* logits, const void* x, const uint64_t* all_recs, int E, int k,
+                        const OomFp8Record& g, const uint64_t* shared_rec, const uint16_t* gate_w, float* gate,
+                        int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st) {
+    FusedArgs a = fused_args(logits, x, all_recs, 1, E, k, g, ids, weights, out, ws);
+    a.shared_rec = shared_rec;
+    a.gate_w = gate_w;
+    a.gate = gate;
+    a.h_bytes = (int)((size_t)(k + 1) * g.inter * sizeof(float));
+    const size_t lds = 0;
+#define FUSED_SH_CASE(DCH, EQ)                                                                                  \
+    return odt == OOM_BF16 ? launch_fused_t<1, DCH, EQ, OOM_BF16, OOM_BF16, true>(a, lds, st)                  \
+                           : launch_fused_t<1, DCH, EQ, OOM_BF16, OOM_F32, true>(a, lds, st);
+    if (E <= 128) {
+        if (g.inter <= 1024) {
+            FUSED_SH_CASE(2, 2)
+        } else {
+            FUSED_SH_CASE(3, 2)
+        }
+    } else {
+        if (g.inter <= 1024) {
+            FUSED_SH_CASE(2, 4)
+        } else {
+            FUSED_SH_CASE(3, 4)
+        }
+    }
+#undef FUSED_SH_CASE
 }
 
 }  // namespace oom

@@ -129,7 +129,9 @@ def test_combine_shared_parity(hip):
 
 
 @pytest.mark.parametrize("T,E,k,H,I,SI,xf32", [
-    (1, 128, 8, 4096, 1536, 1536, False),   # the benchmark's layer shape, one token
+    (1, 128, 8, 4096, 1536, 1536, False),   # the benchmark's layer shape, one token (shared expert in the kernel)
+    (1, 200, 6, 1024, 512, 512, False),     # one token, E > 128, k < 8: waves with only the shared rows
+    (1, 64, 8, 2048, 1024, 2048, False),    # one token, a wider shared expert: its own launch
     (16, 128, 8, 4096, 1536, 1536, False),  # 16 tokens (the matrix-core routed and shared steps)
     (4, 64, 6, 1024, 512, 768, False),      # a shared expert wider than the routed ones
     (3, 16, 4, 256, 128, 256, True),        # f32 activations (the general one-launch kernel)
@@ -180,12 +182,14 @@ def test_layer_decode_matches_oracle(hip, T, E, k, H, I, SI, xf32):
             assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
 
 
-def test_layer_batch_sizes_share_a_workspace(hip):
+@pytest.mark.parametrize("SI", [768, 512])
+def test_layer_batch_sizes_share_a_workspace(hip, SI):
     """Layer steps of 16, 1, 5, 16 and 2 tokens on one workspace made for 16, with no
-    synchronisation between them (a decode batch that shrinks and grows)."""
+    synchronisation between them (a decode batch that shrinks and grows); with SI = inter
+    the one-token steps carry the shared expert inside the decode kernel."""
     import torch
 
-    E, k, H, I, SI = 64, 8, 1024, 512, 768
+    E, k, H, I = 64, 8, 1024, 512
     geo, sgeo = oracle.record_geometry(H, I), oracle.record_geometry(H, SI)
     rw = oracle.gaussian_bf16((E, H), 981, 0.02)
     gw = oracle.gaussian_bf16((1, H), 982, 0.02)
