@@ -51,6 +51,10 @@ SIGNATURES = {
     "oom_moe_plan": (I32, [P, I32, I32, I32, P, P, P, P]),
     "oom_moe_decode_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
     "oom_moe_decode_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
+    "oom_moe_gate_up_nvfp4": (I32, [P, P, P, I32, P, I32, P, P, P]),
+    "oom_moe_down_nvfp4": (I32, [P, P, I32, P, P, P, P]),
+    "oom_moe_decode_nvfp4_workspace_size": (SZ, [I32, I32, I32, P]),
+    "oom_moe_decode_nvfp4": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
     "oom_quantize_rows_fp8": (I32, [P, I32, I64, I64, P, P, P]),
     "oom_moe_grouped_gemm_fp8": (I32, [P, P, P, I32, I32, P, P, I32, P, I64, I64, I64, I64, P]),
     "oom_moe_prefill_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
@@ -126,6 +130,38 @@ def record_geometry(hidden: int, inter: int) -> Fp8Record:
 def record_stride(geo: Fp8Record) -> int:
     end = geo.down_scale + ((geo.hidden + 127) // 128) * ((geo.inter + 127) // 128) * 4
     return (end + 4095) // 4096 * 4096
+
+
+class Nvfp4Record(ctypes.Structure):
+    """OomNvfp4Record of include/oom_hip.h: part offsets of an NVFP4 expert record and the
+    float indices of its three weight_scale_2 scalars."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "hidden", "inter", "gate_weight", "gate_scale", "up_weight", "up_scale", "down_weight", "down_scale")] + [
+        ("scale2", ctypes.c_int64 * 3)]
+
+
+def nvfp4_geometry(hidden: int, inter: int) -> Nvfp4Record:
+    """The nvfp4-modelopt-g16 record as released (docs/dev/format.md:111-118): a 256-byte
+    part of six f32 scalars (weight_scale_2 of gate, up, down at floats 0, 2, 4), then
+    gate.weight, gate.weight_scale, up.weight, up.weight_scale, down.weight,
+    down.weight_scale, each part 256-byte aligned."""
+    def al(v):
+        return (v + 255) // 256 * 256
+    o = 256
+    gw = o; o = al(o + inter * hidden // 2)
+    gs = o; o = al(o + inter * hidden // 16)
+    uw = o; o = al(o + inter * hidden // 2)
+    us = o; o = al(o + inter * hidden // 16)
+    dw = o; o = al(o + hidden * inter // 2)
+    ds = o
+    g = Nvfp4Record(hidden, inter, gw, gs, uw, us, dw, ds)
+    g.scale2[0], g.scale2[1], g.scale2[2] = 0, 2, 4
+    return g
+
+
+def nvfp4_stride(geo: Nvfp4Record) -> int:
+    return (geo.down_scale + geo.hidden * geo.inter // 16 + 4095) // 4096 * 4096
 
 
 # ---- entry points (torch tensors in, results in the given output tensors) ----------
@@ -222,6 +258,27 @@ def moe_decode_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, ou
     check(lib().oom_moe_decode_fp8(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k, ctypes.byref(geo),
                                    _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
                                    ws.numel() * ws.element_size(), _stream(stream)))
+
+
+def moe_gate_up_nvfp4(recs, off, assign_tok, n_experts: int, x, h, geo: Nvfp4Record, stream=None) -> None:
+    check(lib().oom_moe_gate_up_nvfp4(_ptr(recs), _ptr(off), _ptr(assign_tok), n_experts, _ptr(x), _dtype_code(x),
+                                      _ptr(h), ctypes.byref(geo), _stream(stream)))
+
+
+def moe_down_nvfp4(recs, off, n_experts: int, h, y, geo: Nvfp4Record, stream=None) -> None:
+    check(lib().oom_moe_down_nvfp4(_ptr(recs), _ptr(off), n_experts, _ptr(h), _ptr(y), ctypes.byref(geo),
+                                   _stream(stream)))
+
+
+def moe_decode_nvfp4_workspace_size(T: int, E: int, k: int, geo: Nvfp4Record) -> int:
+    return int(lib().oom_moe_decode_nvfp4_workspace_size(T, E, k, ctypes.byref(geo)))
+
+
+def moe_decode_nvfp4(logits, x, all_recs, k: int, geo: Nvfp4Record, ids, weights, out, ws, stream=None) -> None:
+    T, E = logits.shape
+    check(lib().oom_moe_decode_nvfp4(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k,
+                                     ctypes.byref(geo), _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out),
+                                     _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
 
 
 def attn_decode_workspace_size(kv_len: int, heads: int, kv_heads: int, d: int) -> int:

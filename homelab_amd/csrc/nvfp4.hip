@@ -1,0 +1,442 @@
+// Routed experts over NVFP4 records (layout nvfp4-modelopt-g16, OomNvfp4Record) read in
+// place: gate/up + SwiGLU, down, and the one-call decode step over them.
+//
+// A weight is w = e2m1(code) * (e4m3(scale) * scale_2) (crates/oominf-cuda/kernels/moe.cu:17-45;
+// crates/oominf-cpu/src/kernel.rs:76-98): two codes per byte, low nibble first, one e4m3
+// scale byte per 16 inputs, one fp32 scale_2 per projection in the record's scalars part.
+//
+// Layout of the work (gfx950, wave64):
+//   - a lane's 16-byte load holds 32 codes of one row: columns 1024 c + 32 l .. + 32 of
+//     1024-column chunk c, l = lane % 32, two scale groups of 16;
+//   - a wave streams two rows at a time, one per half (lanes 0..31 row 2p, 32..63 row
+//     2p + 1), so a 640-column down row keeps 20 of each 32 lanes busy, not 20 of 64;
+//   - the codes convert exactly to fp32 with v_cvt_scalef32_pk_f32_fp4 (scale 1), each
+//     group's 16 products sum in fp32 and are scaled once by e4m3(scale) * scale_2, so
+//     only the summation order differs from the reference's per-weight decode;
+//   - the inputs of a pass (x rows of up to TB assignments, or h rows) sit in LDS as fp32
+//     in the same lane order (float4 i of lane l's 32 columns of chunk c of row t at
+//     ((t * CH + c) * 8 + i) * 32 + l), staged with 16-byte loads all in flight before
+//     the first store; both halves read the same words;
+//   - gate/up: a block of 4 waves x 2 row pairs = 16 intermediate rows of one expert;
+//     down: 4 waves x 4 row pairs = 32 output rows; grid (row blocks, experts), and a
+//     block past the step's expert count (read from the device plan) returns at once;
+//   - a scale group past the row's end reads as scale 0 (its codes would pair with the
+//     next row's bytes and zero inputs), and loads past the record read zeros.
+#include "router.hpp"
+#include "stream.hpp"
+
+extern "C" int oom_router_topk(const float* logits, int32_t* ids, float* weights, int T, int E, int k, void* stream);
+extern "C" int oom_moe_plan(const int32_t* ids, int T, int E, int k, const uint64_t* all_recs, int32_t* plan,
+                            uint64_t* recs, void* stream);
+
+namespace oom {
+
+int launch_combine(const float* y, const int32_t* slot, const float* w, void* out, int odt, int T, int H, int k,
+                   hipStream_t st);
+
+constexpr int N4_WAVES = 4;
+constexpr int N4_GP = 2;  // gate/up row pairs per wave
+constexpr int N4_DP = 4;  // down row pairs per wave
+constexpr int N4_TB = 2;  // assignments per pass
+constexpr int N4_KMAX = 4096;
+
+struct Rec4 {
+    int H, I;
+    int gw, gs, uw, us, dw, ds;
+    int s2g, s2u, s2d;  // byte offsets of the three weight_scale_2 floats
+    int bytes;          // record span: end of its last part
+};
+
+static int64_t rec4_span(const OomNvfp4Record& g) {
+    const int64_t H = g.hidden, I = g.inter;
+    int64_t e = std::max({g.gate_weight + I * H / 2, g.gate_scale + I * H / 16, g.up_weight + I * H / 2,
+                          g.up_scale + I * H / 16, g.down_weight + H * I / 2, g.down_scale + H * I / 16});
+    for (int p = 0; p < 3; p++) e = std::max(e, (g.scale2[p] + 1) * 4);
+    return e;
+}
+
+static Rec4 rec4_of(const OomNvfp4Record& g) {
+    return Rec4{(int)g.hidden,         (int)g.inter,         (int)g.gate_weight,   (int)g.gate_scale,
+                (int)g.up_weight,      (int)g.up_scale,      (int)g.down_weight,   (int)g.down_scale,
+                (int)(g.scale2[0] * 4), (int)(g.scale2[1] * 4), (int)(g.scale2[2] * 4), (int)rec4_span(g)};
+}
+
+// The 32 E2M1 codes of a 16-byte piece to fp32, exactly: byte b holds columns 2b (low
+// nibble) and 2b + 1.
+__device__ __forceinline__ void e2m1x32(const uint4& v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const auto p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 0);
+        const auto p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 1);
+        const auto p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 2);
+        const auto p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 3);
+        f[8 * i + 0] = p0[0];
+        f[8 * i + 1] = p0[1];
+        f[8 * i + 2] = p1[0];
+        f[8 * i + 3] = p1[1];
+        f[8 * i + 4] = p2[0];
+        f[8 * i + 5] = p2[1];
+        f[8 * i + 6] = p3[0];
+        f[8 * i + 7] = p3[1];
+    }
+}
+
+__device__ __forceinline__ uint32_t ldb(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
+__device__ __forceinline__ float e4m3_byte(uint32_t b) { return __builtin_amdgcn_cvt_f32_fp8((int)b, 0); }
+
+// Stages rows row_of(t) (t < nb) of src (width K, element type DT) into LDS in the lane
+// order above; zeros past K and for t >= nb.
+template <int DT, typename RowOf>
+__device__ __forceinline__ void stage4(float4* xs4, const void* src, int K, int CH, int nb, RowOf row_of) {
+    constexpr int EPL = DT == OOM_BF16 ? 8 : 4;  // elements per 16-byte load
+    constexpr int ES = DT == OOM_BF16 ? 2 : 4;
+    const int span = CH * 1024, nvec = N4_TB * span / EPL;
+    for (int base = 0; base < nvec; base += 256 * 4) {
+        uint4 v[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const int i = base + (int)threadIdx.x + 256 * n;
+            const int t = i * EPL / span, kk = i * EPL - t * span;
+            const bool ok = i < nvec && t < nb && kk < K;
+            v[n] = ok ? *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(src) +
+                                                        ((size_t)row_of(t) * K + kk) * ES)
+                      : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const int i = base + (int)threadIdx.x + 256 * n;
+            if (i >= nvec) break;
+            const int t = i * EPL / span, kk = i * EPL - t * span;
+            const int c = kk >> 10, l = (kk & 1023) >> 5, j = kk & 31;
+            float4* dst = &xs4[((t * CH + c) * 8 + (j >> 2)) * 32 + l];
+            if constexpr (DT == OOM_BF16) {
+                dst[0] = make_float4(__uint_as_float(v[n].x << 16), __uint_as_float(v[n].x & 0xffff0000u),
+                                     __uint_as_float(v[n].y << 16), __uint_as_float(v[n].y & 0xffff0000u));
+                dst[32] = make_float4(__uint_as_float(v[n].z << 16), __uint_as_float(v[n].z & 0xffff0000u),
+                                      __uint_as_float(v[n].w << 16), __uint_as_float(v[n].w & 0xffff0000u));
+            } else {
+                dst[0] = make_float4(__uint_as_float(v[n].x), __uint_as_float(v[n].y), __uint_as_float(v[n].z),
+                                     __uint_as_float(v[n].w));
+            }
+        }
+    }
+}
+
+// The two group sums of one 32-column piece against staged row t: (cols 0..15, 16..31).
+__device__ __forceinline__ void piece_dot(const float* f, const float4* xs4, int t, int CH, int c, int l, float& p0,
+                                          float& p1) {
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = xs4[((t * CH + c) * 8 + i) * 32 + l];
+        x[4 * i] = v.x;
+        x[4 * i + 1] = v.y;
+        x[4 * i + 2] = v.z;
+        x[4 * i + 3] = v.w;
+    }
+    p0 = 0.0f;
+    p1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        p0 = fmaf(f[i], x[i], p0);
+        p1 = fmaf(f[16 + i], x[16 + i], p1);
+    }
+}
+
+// One gate/up pass over TB staged tokens (nb real): the wave's rows j0 + 2p + half.
+template <int TB>
+__device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amdgpu_buffer_rsrc_t r, float s2g,
+                                         float s2u, int j0, int lane, int nb, int a0, float* h) {
+    const int H = g.H, I = g.I, CH = (H + 1023) >> 10, hg = H >> 4;
+    const int half = lane >> 5, l = lane & 31;
+    float acc[2 * TB * N4_GP];  // [gate|up][t][p]
+#pragma unroll
+    for (int i = 0; i < 2 * TB * N4_GP; i++) acc[i] = 0.0f;
+    for (int c0 = 0; c0 < CH; c0 += 2) {
+        uint4 wg[N4_GP][2], wu[N4_GP][2];
+        uint32_t bg[N4_GP][2][2], bu[N4_GP][2][2];
+#pragma unroll
+        for (int p = 0; p < N4_GP; p++) {
+            const int j = j0 + 2 * p + half;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int col = (c0 + c) * 1024 + 32 * l;
+                const bool ok = j < I && c0 + c < CH && col < H;
+                wg[p][c] = ld16(r, ok ? g.gw + j * (H >> 1) + (col >> 1) : OOB);
+                wu[p][c] = ld16(r, ok ? g.uw + j * (H >> 1) + (col >> 1) : OOB);
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const bool okq = ok && (col >> 4) + q < hg;
+                    bg[p][c][q] = ldb(r, okq ? g.gs + j * hg + (col >> 4) + q : OOB);
+                    bu[p][c][q] = ldb(r, okq ? g.us + j * hg + (col >> 4) + q : OOB);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            if (c0 + c >= CH) break;
+            const int col = (c0 + c) * 1024 + 32 * l;
+#pragma unroll
+            for (int p = 0; p < N4_GP; p++) {
+                float sg[2], su[2];
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const bool okq = (col >> 4) + q < hg;  // a group past the row's end scales to 0
+                    sg[q] = okq ? e4m3_byte(bg[p][c][q]) * s2g : 0.0f;
+                    su[q] = okq ? e4m3_byte(bu[p][c][q]) * s2u : 0.0f;
+                }
+                float fg[32], fu[32];
+                e2m1x32(wg[p][c], fg);
+                e2m1x32(wu[p][c], fu);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    float g0, g1, u0, u1;
+                    piece_dot(fg, xs4, t, CH, c0 + c, l, g0, g1);
+                    piece_dot(fu, xs4, t, CH, c0 + c, l, u0, u1);
+                    float& ag = acc[(0 * TB + t) * N4_GP + p];
+                    float& au = acc[(1 * TB + t) * N4_GP + p];
+                    ag = fmaf(g1, sg[1], fmaf(g0, sg[0], ag));
+                    au = fmaf(u1, su[1], fmaf(u0, su[0], au));
+                }
+            }
+        }
+    }
+    // value v = (gu * TB + t) * GP + p ends in sub-group v of each half; its up sum sits
+    // 16 lanes on, in the same half
+    constexpr int NV = 2 * TB * N4_GP, GROUP = 32 / NV;
+    const float tot = wave_sum_multi<NV, 16>(acc, lane);
+    const float up = __shfl(tot, (lane & 32) | ((lane + 16) & 31), 64);
+    const int v = l / GROUP;
+    if (l % GROUP == 0 && v < NV / 2) {
+        const int t = v / N4_GP, j = j0 + 2 * (v % N4_GP) + half;
+        if (t < nb && j < I) h[(size_t)(a0 + t) * I + j] = siluf(tot) * up;
+    }
+}
+
+template <int XDT>
+__global__ void __launch_bounds__(256) moe_gate_up_nvfp4_kernel(const uint64_t* __restrict__ recs,
+                                                                const int32_t* __restrict__ off,
+                                                                const int32_t* __restrict__ assign_tok,
+                                                                const void* __restrict__ x, float* __restrict__ h,
+                                                                Rec4 g, const int32_t* __restrict__ n_e_dev) {
+    extern __shared__ float4 xs4[];
+    const int e = blockIdx.y;
+    if (n_e_dev && e >= *n_e_dev) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs[e], g.bytes);
+    const float s2g = ldf(r, g.s2g), s2u = ldf(r, g.s2u);
+    const int j0 = (blockIdx.x * N4_WAVES + wave) * 2 * N4_GP;
+    const int CH = (g.H + 1023) >> 10;
+    const int a_begin = off[e], a_end = off[e + 1];
+    for (int a0 = a_begin; a0 < a_end; a0 += N4_TB) {
+        const int nb = min(N4_TB, a_end - a0);
+        __syncthreads();
+        stage4<XDT>(xs4, x, g.H, CH, nb, [&](int t) { return assign_tok[a0 + t]; });
+        __syncthreads();
+        if (nb == 1) gu4_pass<1>(xs4, g, r, s2g, s2u, j0, lane, nb, a0, h);
+        else gu4_pass<2>(xs4, g, r, s2g, s2u, j0, lane, nb, a0, h);
+    }
+}
+
+// One down pass over TB staged h rows (nb real): the wave's output rows r0 + 2p + half.
+template <int TB>
+__device__ __forceinline__ void dn4_pass(const float4* xs4, const Rec4& g, __amdgpu_buffer_rsrc_t r, float s2,
+                                         int r0, int lane, int nb, int a0, float* y) {
+    const int H = g.H, I = g.I, CH = (I + 1023) >> 10, ig = I >> 4;
+    const int half = lane >> 5, l = lane & 31;
+    float acc[TB * N4_DP];
+#pragma unroll
+    for (int i = 0; i < TB * N4_DP; i++) acc[i] = 0.0f;
+    for (int c0 = 0; c0 < CH; c0 += 2) {
+        uint4 wd[N4_DP][2];
+        uint32_t bd[N4_DP][2][2];
+#pragma unroll
+        for (int p = 0; p < N4_DP; p++) {
+            const int row = r0 + 2 * p + half;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int col = (c0 + c) * 1024 + 32 * l;
+                const bool ok = row < H && c0 + c < CH && col < I;
+                wd[p][c] = ld16(r, ok ? g.dw + row * (I >> 1) + (col >> 1) : OOB);
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+                    bd[p][c][q] = ldb(r, ok && (col >> 4) + q < ig ? g.ds + row * ig + (col >> 4) + q : OOB);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            if (c0 + c >= CH) break;
+            const int col = (c0 + c) * 1024 + 32 * l;
+#pragma unroll
+            for (int p = 0; p < N4_DP; p++) {
+                float sd[2];
+#pragma unroll
+                for (int q = 0; q < 2; q++) sd[q] = (col >> 4) + q < ig ? e4m3_byte(bd[p][c][q]) * s2 : 0.0f;
+                float f[32];
+                e2m1x32(wd[p][c], f);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    float p0, p1;
+                    piece_dot(f, xs4, t, CH, c0 + c, l, p0, p1);
+                    float& a = acc[t * N4_DP + p];
+                    a = fmaf(p1, sd[1], fmaf(p0, sd[0], a));
+                }
+            }
+        }
+    }
+    constexpr int NV = TB * N4_DP, GROUP = 32 / NV;
+    const float tot = wave_sum_multi<NV, 16>(acc, lane);
+    const int v = l / GROUP;
+    if (l % GROUP == 0) {
+        const int t = v / N4_DP, row = r0 + 2 * (v % N4_DP) + half;
+        if (t < nb && row < H) y[(size_t)(a0 + t) * H + row] = tot;
+    }
+}
+
+__global__ void __launch_bounds__(256) moe_down_nvfp4_kernel(const uint64_t* __restrict__ recs,
+                                                             const int32_t* __restrict__ off,
+                                                             const float* __restrict__ h, float* __restrict__ y,
+                                                             Rec4 g, const int32_t* __restrict__ n_e_dev) {
+    extern __shared__ float4 xs4[];
+    const int e = blockIdx.y;
+    if (n_e_dev && e >= *n_e_dev) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs[e], g.bytes);
+    const float s2 = ldf(r, g.s2d);
+    const int r0 = (blockIdx.x * N4_WAVES + wave) * 2 * N4_DP;
+    const int CH = (g.I + 1023) >> 10;
+    const int a_begin = off[e], a_end = off[e + 1];
+    for (int a0 = a_begin; a0 < a_end; a0 += N4_TB) {
+        const int nb = min(N4_TB, a_end - a0);
+        __syncthreads();
+        stage4<OOM_F32>(xs4, h, g.I, CH, nb, [&](int t) { return a0 + t; });
+        __syncthreads();
+        if (nb == 1) dn4_pass<1>(xs4, g, r, s2, r0, lane, nb, a0, y);
+        else dn4_pass<2>(xs4, g, r, s2, r0, lane, nb, a0, y);
+    }
+}
+
+static int check_geo4(const OomNvfp4Record* geo, const char* who) {
+    if (!geo) return fail(OOM_ERR_ARG, std::string(who) + ": null geometry");
+    const OomNvfp4Record& g = *geo;
+    bool ok = g.hidden >= 16 && g.inter >= 16 && g.hidden % 16 == 0 && g.inter % 16 == 0 && g.hidden <= N4_KMAX &&
+              g.inter <= N4_KMAX && g.gate_weight >= 0 && g.up_weight >= 0 && g.down_weight >= 0 &&
+              g.gate_scale >= 0 && g.up_scale >= 0 && g.down_scale >= 0 && g.gate_weight % 16 == 0 &&
+              g.up_weight % 16 == 0 && g.down_weight % 16 == 0;
+    for (int p = 0; p < 3; p++) ok = ok && g.scale2[p] >= 0;
+    ok = ok && rec4_span(g) < OOB;
+    if (!ok)
+        return fail(OOM_ERR_ARG, std::string(who) +
+                                     ": widths must be multiples of 16 and at most 4096, weight parts 16-byte "
+                                     "aligned (buffer too small or shape unsupported)");
+    return OOM_OK;
+}
+
+static size_t stage_lds(int64_t width) { return (size_t)N4_TB * cdiv(width, 1024) * 1024 * sizeof(float); }
+
+static int launch_gate_up4(const uint64_t* recs, const int32_t* off, const int32_t* tok, int grid_e, const void* x,
+                           int xdt, float* h, const OomNvfp4Record& geo, const int32_t* n_e_dev, hipStream_t st) {
+    const Rec4 g = rec4_of(geo);
+    const dim3 grid((unsigned)cdiv(geo.inter, N4_WAVES * 2 * N4_GP), (unsigned)grid_e);
+    const size_t lds = stage_lds(geo.hidden);
+    if (xdt == OOM_BF16)
+        hipLaunchKernelGGL((moe_gate_up_nvfp4_kernel<OOM_BF16>), grid, dim3(256), lds, st, recs, off, tok, x, h, g,
+                           n_e_dev);
+    else
+        hipLaunchKernelGGL((moe_gate_up_nvfp4_kernel<OOM_F32>), grid, dim3(256), lds, st, recs, off, tok, x, h, g,
+                           n_e_dev);
+    return launched("oom_moe_gate_up_nvfp4");
+}
+
+static int launch_down4(const uint64_t* recs, const int32_t* off, int grid_e, const float* h, float* y,
+                        const OomNvfp4Record& geo, const int32_t* n_e_dev, hipStream_t st) {
+    const Rec4 g = rec4_of(geo);
+    const dim3 grid((unsigned)cdiv(geo.hidden, N4_WAVES * 2 * N4_DP), (unsigned)grid_e);
+    hipLaunchKernelGGL(moe_down_nvfp4_kernel, grid, dim3(256), stage_lds(geo.inter), st, recs, off, h, y, g, n_e_dev);
+    return launched("oom_moe_down_nvfp4");
+}
+
+// Workspace of oom_moe_decode_nvfp4: plan | recs | h | y.
+struct Decode4Ws {
+    size_t plan, recs, h, y, total;
+};
+
+static size_t a256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static Decode4Ws decode4_ws(int T, int E, int k, const OomNvfp4Record& g) {
+    Decode4Ws w;
+    const size_t A = (size_t)T * k;
+    w.plan = 0;
+    w.recs = a256(PlanView::size(E, (int)A) * sizeof(int32_t));
+    w.h = w.recs + a256(std::min<size_t>(E, A) * sizeof(uint64_t));
+    w.y = w.h + a256(A * (size_t)g.inter * sizeof(float));
+    w.total = w.y + a256(A * (size_t)g.hidden * sizeof(float));
+    return w;
+}
+
+}  // namespace oom
+
+extern "C" int oom_moe_gate_up_nvfp4(const uint64_t* recs, const int32_t* off, const int32_t* assign_tok,
+                                     int n_experts, const void* x, int x_dtype, float* h, const OomNvfp4Record* geo,
+                                     void* stream) {
+    using namespace oom;
+    if (int rc = check_geo4(geo, "oom_moe_gate_up_nvfp4")) return rc;
+    OOM_REQUIRE(n_experts >= 0 && n_experts <= 65535, "oom_moe_gate_up_nvfp4: n_experts");
+    OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_moe_gate_up_nvfp4: x_dtype");
+    if (n_experts == 0) return OOM_OK;
+    OOM_REQUIRE(recs && off && assign_tok && x && h, "oom_moe_gate_up_nvfp4: null buffer");
+    OOM_REQUIRE(aligned(x, 16), "oom_moe_gate_up_nvfp4: x must be 16-byte aligned");
+    return launch_gate_up4(recs, off, assign_tok, n_experts, x, x_dtype, h, *geo, nullptr, as_stream(stream));
+}
+
+extern "C" int oom_moe_down_nvfp4(const uint64_t* recs, const int32_t* off, int n_experts, const float* h, float* y,
+                                  const OomNvfp4Record* geo, void* stream) {
+    using namespace oom;
+    if (int rc = check_geo4(geo, "oom_moe_down_nvfp4")) return rc;
+    OOM_REQUIRE(n_experts >= 0 && n_experts <= 65535, "oom_moe_down_nvfp4: n_experts");
+    if (n_experts == 0) return OOM_OK;
+    OOM_REQUIRE(recs && off && h && y, "oom_moe_down_nvfp4: null buffer");
+    OOM_REQUIRE(aligned(h, 16), "oom_moe_down_nvfp4: h must be 16-byte aligned");
+    return launch_down4(recs, off, n_experts, h, y, *geo, nullptr, as_stream(stream));
+}
+
+extern "C" size_t oom_moe_decode_nvfp4_workspace_size(int T, int E, int k, const OomNvfp4Record* geo) {
+    if (!geo || T < 1 || E < 1 || k < 1) return 0;
+    return oom::decode4_ws(T, E, k, *geo).total;
+}
+
+extern "C" int oom_moe_decode_nvfp4(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T,
+                                    int E, int k, const OomNvfp4Record* geo, int32_t* ids, float* weights, void* out,
+                                    int out_dtype, void* ws, size_t ws_bytes, void* stream) {
+    using namespace oom;
+    if (int rc = check_geo4(geo, "oom_moe_decode_nvfp4")) return rc;
+    OOM_REQUIRE(T >= 1 && (int64_t)T * k <= (1 << 24), "oom_moe_decode_nvfp4: T must be >= 1 and T * k <= 2^24");
+    OOM_REQUIRE(k >= 1 && k <= 32 && E >= k && E <= 8192, "oom_moe_decode_nvfp4: router top-k > 32 or experts > 8192");
+    OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_moe_decode_nvfp4: x_dtype");
+    OOM_REQUIRE(out_dtype == OOM_F32 || out_dtype == OOM_BF16, "oom_moe_decode_nvfp4: out_dtype");
+    OOM_REQUIRE(logits && x && all_recs && ids && weights && out, "oom_moe_decode_nvfp4: null buffer");
+    OOM_REQUIRE(aligned(x, 16), "oom_moe_decode_nvfp4: x must be 16-byte aligned");
+    const Decode4Ws w = decode4_ws(T, E, k, *geo);
+    if (!ws || ws_bytes < w.total)
+        return fail(OOM_ERR_WORKSPACE,
+                    "oom_moe_decode_nvfp4: workspace smaller than oom_moe_decode_nvfp4_workspace_size()");
+    OOM_REQUIRE(aligned(ws, 256), "oom_moe_decode_nvfp4: workspace must be 256-byte aligned");
+    uint8_t* base = reinterpret_cast<uint8_t*>(ws);
+    int32_t* plan = reinterpret_cast<int32_t*>(base + w.plan);
+    uint64_t* recs = reinterpret_cast<uint64_t*>(base + w.recs);
+    float* h = reinterpret_cast<float*>(base + w.h);
+    float* y = reinterpret_cast<float*>(base + w.y);
+    hipStream_t st = as_stream(stream);
+    const int A = T * k;
+    const PlanView pv{plan, E, A};
+    if (int rc = oom_router_topk(logits, ids, weights, T, E, k, stream)) return rc;
+    if (int rc = oom_moe_plan(ids, T, E, k, all_recs, plan, recs, stream)) return rc;
+    const int grid_e = std::min(E, A);
+    if (int rc = launch_gate_up4(recs, pv.off(), pv.assign_tok(), grid_e, x, x_dtype, h, *geo, pv.n_e(), st)) return rc;
+    if (int rc = launch_down4(recs, pv.off(), grid_e, h, y, *geo, pv.n_e(), st)) return rc;
+    return launch_combine(y, pv.slot_assign(), weights, out, out_dtype, T, (int)geo->hidden, k, st);
+}

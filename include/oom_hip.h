@@ -70,6 +70,24 @@ const char* oom_last_error(void);
  * hipMemset node, so it is safe inside graph capture). */
 int oom_workspace_init(void* ws, size_t bytes, void* stream);
 
+/* Byte offsets of the parts of an NVFP4 expert record (layout nvfp4-modelopt-g16,
+ * docs/dev/format.md:63-68,111-118): weights two E2M1 codes per byte, row-major, low
+ * nibble first (gate/up [inter, hidden], down [hidden, inter]); weight_scale one e4m3
+ * byte per 16 inputs, row-major; scale2[p] the index, in floats from the record start, of
+ * projection p's weight_scale_2 (gate, up, down). Weight w = e2m1(code) *
+ * (e4m3(scale) * scale_2). Mirrors Nvfp4Record (crates/oominf-core/src/backend.rs:783-796). */
+typedef struct OomNvfp4Record {
+    int64_t hidden;
+    int64_t inter;
+    int64_t gate_weight;
+    int64_t gate_scale;
+    int64_t up_weight;
+    int64_t up_scale;
+    int64_t down_weight;
+    int64_t down_scale;
+    int64_t scale2[3];
+} OomNvfp4Record;
+
 /* Router: softmax over E logits per token, top k (ties to the lower id), weights
  * renormalised over the k picks, in pick order. logits f32 [T, E]; ids i32 [T, k];
  * weights f32 [T, k]. k <= 32, E <= 8192.
@@ -164,6 +182,29 @@ int oom_moe_layer_decode_fp8(const void* x, int x_dtype, const uint16_t* router_
                              int E, int k, const OomFp8Record* geo, const uint64_t* shared_rec,
                              const OomFp8Record* shared_geo, const uint16_t* shared_gate_w, int32_t* ids,
                              float* weights, void* out, int out_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/* Routed-expert gate/up + SwiGLU over NVFP4 records read in place: as
+ * oom_moe_gate_up_fp8, weights decoded as e2m1(code) * (e4m3(scale) * scale_2), fp32
+ * accumulate. hidden and inter multiples of 16, hidden <= 4096; x 16-byte aligned.
+ * Replaces Experts::moe_gate_up (crates/oominf-core/src/backend.rs:825-836;
+ * crates/oominf-cuda/src/experts.rs:43-93; crates/oominf-cuda/kernels/moe.cu:52-106). */
+int oom_moe_gate_up_nvfp4(const uint64_t* recs, const int32_t* off, const int32_t* assign_tok, int n_experts,
+                          const void* x, int x_dtype, float* h, const OomNvfp4Record* geo, void* stream);
+
+/* Down projection over NVFP4 records: y[a, r] = h[a] . Wd_e[r]; h f32 [A, inter]
+ * (inter <= 4096); y f32 [A, hidden]. Replaces Experts::moe_down (backend.rs:859-868;
+ * experts.rs:174-209; moe.cu:108-151). */
+int oom_moe_down_nvfp4(const uint64_t* recs, const int32_t* off, int n_experts, const float* h, float* y,
+                       const OomNvfp4Record* geo, void* stream);
+
+/* One decode MoE FFN step over NVFP4 records with no host synchronisation: router
+ * top-k, device routing plan, gate/up + SwiGLU, down and slot-order weighted combine, as
+ * oom_moe_decode_fp8 (same arguments, NVFP4 geometry). The routed part of Moe::forward
+ * (crates/oominf-models-qwen/src/moe.rs:290-366) on the released record format. */
+size_t oom_moe_decode_nvfp4_workspace_size(int T, int E, int k, const OomNvfp4Record* geo);
+int oom_moe_decode_nvfp4(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T, int E,
+                         int k, const OomNvfp4Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
+                         void* ws, size_t ws_bytes, void* stream);
 
 /* Per-row e4m3 quantisation of activations: scale[r] = max_c |x[r, c]| / 448 (1 for an
  * all-zero row), q[r, c] = e4m3(x[r, c] / scale[r]) rounded to nearest even and

@@ -54,6 +54,45 @@ def record_geometry(hidden: int, inter: int) -> Fp8Record:
     return Fp8Record(hidden, inter, gw, gs, uw, us, dw, ds)
 
 
+class Nvfp4Record(ctypes.Structure):
+    """OomNvfp4Record of include/oom_hip.h: byte offsets of an NVFP4 expert record's parts
+    and the float indices of the three weight_scale_2 scalars."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "hidden", "inter", "gate_weight", "gate_scale", "up_weight", "up_scale", "down_weight", "down_scale")] + [
+        ("scale2", ctypes.c_int64 * 3)]
+
+
+def nvfp4_geometry(hidden: int, inter: int) -> Nvfp4Record:
+    """The nvfp4-modelopt-g16 record of docs/dev/format.md:111-118: a 256-byte part of six
+    f32 scalars (gate/up/down weight_scale_2 at floats 0, 2, 4, each followed by its
+    input_scale), then gate.weight [inter, hidden / 2], gate.weight_scale [inter,
+    hidden / 16], up.*, down.weight [hidden, inter / 2], down.weight_scale [hidden,
+    inter / 16], each part 256-byte aligned."""
+    def al(v):
+        return (v + 255) // 256 * 256
+    o = 256
+    gw = o; o = al(o + inter * hidden // 2)
+    gs = o; o = al(o + inter * hidden // 16)
+    uw = o; o = al(o + inter * hidden // 2)
+    us = o; o = al(o + inter * hidden // 16)
+    dw = o; o = al(o + hidden * inter // 2)
+    ds = o
+    g = Nvfp4Record(hidden, inter, gw, gs, uw, us, dw, ds)
+    g.scale2[0], g.scale2[1], g.scale2[2] = 0, 2, 4
+    return g
+
+
+def nvfp4_size(geo: Nvfp4Record) -> int:
+    """Bytes of an NVFP4 record up to the end of its last part."""
+    return geo.down_scale + geo.hidden * geo.inter // 16
+
+
+def nvfp4_stride(geo: Nvfp4Record) -> int:
+    """Record size rounded up to 4096 bytes (ALIGN, docs/dev/format.md:37)."""
+    return (nvfp4_size(geo) + 4095) // 4096 * 4096
+
+
 def record_stride(geo: Fp8Record) -> int:
     """Record size rounded up to 4096 bytes (ALIGN, docs/dev/format.md:37)."""
     end = geo.down_scale + ((geo.hidden + 127) // 128) * ((geo.inter + 127) // 128) * 4
@@ -92,6 +131,11 @@ def lib() -> ctypes.CDLL:
             "oracle_moe_down_fp8": (None, [P, P, I32, P, P, P]),
             "oracle_moe_combine_slots": (None, [P, P, P, P, I32, I32, I32]),
             "oracle_moe_decode_fp8": (I32, [P, P, P, I32, I32, I32, P, P, P, P]),
+            "oracle_e2m1_to_f32": (F, [ctypes.c_uint8]),
+            "oracle_nvfp4_rows": (None, [P, P, F, I64, I64, P, I32, P]),
+            "oracle_moe_gate_up_nvfp4": (None, [P, P, P, I32, P, P, P]),
+            "oracle_moe_down_nvfp4": (None, [P, P, I32, P, P, P]),
+            "oracle_moe_decode_nvfp4": (I32, [P, P, P, I32, I32, I32, P, P, P, P]),
             "oracle_grouped_gemm_fp8": (None, [P, P, P, I32, P, P, I32, P, I64, I64, I64, I64]),
             "oracle_moe_prefill_fp8": (I32, [P, P, P, I32, I32, I32, P, P, P, P]),
             "oracle_attn_decode_paged": (None, [P, P, P, P, I32, I32, I32, I32, I32, F, P]),
@@ -110,7 +154,9 @@ def _p(a: np.ndarray | None):
     if a is None:
         return None
     assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
-    return ctypes.c_void_p(a.ctypes.data)
+    # a pointer object that holds a reference to `a`: an array made inline for one call
+    # (a dtype conversion, an address table) stays alive until the call returns
+    return a.ctypes.data_as(ctypes.c_void_p)
 
 
 def _ptrs(arrs) -> np.ndarray:
@@ -342,6 +388,56 @@ def moe_decode(logits: np.ndarray, x: np.ndarray, all_recs, k: int, geo: Fp8Reco
     out = np.empty((T, geo.hidden), dtype=np.float32)
     table = _ptrs(all_recs)
     rc = lib().oracle_moe_decode_fp8(_p(logits), _p(x), _p(table), T, E, k, ctypes.byref(geo), _p(ids), _p(w), _p(out))
+    assert rc == 0
+    return ids, w, out
+
+
+def e2m1_to_f32(code: int) -> float:
+    return float(lib().oracle_e2m1_to_f32(code))
+
+
+def nvfp4_rows(packed: np.ndarray, scales: np.ndarray, s2: float, x: np.ndarray) -> np.ndarray:
+    """y [T, rows] of one NVFP4 matrix (packed [rows, cols / 2], scales [rows, cols / 16])."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, half = packed.shape
+    T = x.shape[0]
+    y = np.empty((T, rows), dtype=np.float32)
+    lib().oracle_nvfp4_rows(_p(packed), _p(scales), s2, rows, 2 * half, _p(x), T, _p(y))
+    return y
+
+
+def moe_gate_up_nvfp4(recs, off, assign_tok, x: np.ndarray, geo: Nvfp4Record) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    h = np.empty((int(off[-1]), geo.inter), dtype=np.float32)
+    table = _ptrs(recs)
+    lib().oracle_moe_gate_up_nvfp4(_p(table), _p(np.ascontiguousarray(off, dtype=np.int32)),
+                                   _p(np.ascontiguousarray(assign_tok, dtype=np.int32)), len(recs), _p(x), _p(h),
+                                   ctypes.byref(geo))
+    return h
+
+
+def moe_down_nvfp4(recs, off, h: np.ndarray, geo: Nvfp4Record) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    y = np.empty((int(off[-1]), geo.hidden), dtype=np.float32)
+    table = _ptrs(recs)
+    lib().oracle_moe_down_nvfp4(_p(table), _p(np.ascontiguousarray(off, dtype=np.int32)), len(recs), _p(h), _p(y),
+                                ctypes.byref(geo))
+    return y
+
+
+def moe_decode_nvfp4(logits: np.ndarray, x: np.ndarray, all_recs, k: int, geo: Nvfp4Record):
+    """(ids, weights, out f32) of one decode MoE step over NVFP4 records."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, E = logits.shape
+    ids = np.empty((T, k), dtype=np.int32)
+    w = np.empty((T, k), dtype=np.float32)
+    out = np.empty((T, geo.hidden), dtype=np.float32)
+    table = _ptrs(all_recs)  # held for the call: the C side reads it
+    rc = lib().oracle_moe_decode_nvfp4(_p(logits), _p(x), _p(table), T, E, k, ctypes.byref(geo), _p(ids), _p(w),
+                                       _p(out))
     assert rc == 0
     return ids, w, out
 

@@ -139,6 +139,22 @@ void oracle_moe_combine_slots(const float* y, const int32_t* slot_assign, const 
 int oracle_moe_decode_fp8(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
                           const OomFp8Record* geo, int32_t* ids, float* weights, float* out);
 
+/* NVFP4 (nvfp4-modelopt-g16) routed experts. E2M1 value of a 4-bit code
+ * (crates/oominf-cpu/src/kernel.rs:8-11). */
+float oracle_e2m1_to_f32(uint8_t code);
+/* y[t, r] = sum_c e2m1(code(r, c)) * (e4m3(scale(r, c / 16)) * s2) * x[t, c], column order
+ * (kernel.rs:76-98); packed [rows, cols / 2], scales [rows, cols / 16]; y [T, rows]. */
+void oracle_nvfp4_rows(const uint8_t* packed, const uint8_t* scales, float s2, int64_t rows, int64_t cols,
+                       const float* x, int T, float* y);
+/* gate/up + SwiGLU and down over NVFP4 records (moe.cu:52-151 semantics). */
+void oracle_moe_gate_up_nvfp4(const uint8_t* const* recs, const int32_t* off, const int32_t* assign_tok, int n_e,
+                              const float* x, float* h, const OomNvfp4Record* geo);
+void oracle_moe_down_nvfp4(const uint8_t* const* recs, const int32_t* off, int n_e, const float* h, float* y,
+                           const OomNvfp4Record* geo);
+/* The whole routed decode step over NVFP4 records (router, plan, gate/up, down, combine). */
+int oracle_moe_decode_nvfp4(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
+                            const OomNvfp4Record* geo, int32_t* ids, float* weights, float* out);
+
 /* ---- prefill grouped GEMM (FP8 x FP8) ---------------------------------- */
 
 /* y[a, r] = xs(a) * sum_kb ws(r, kb) * sum_{c in kb} e4m3(xq[row(a), c]) * e4m3(W[r, c])

@@ -233,6 +233,102 @@ int oracle_moe_decode_fp8(const float* logits, const float* x, const uint8_t* co
     return 0;
 }
 
+/* ---- NVFP4 routed experts (nvfp4-modelopt-g16) ------------------------------------- */
+
+/* E2M1 values by 4-bit code: low three bits the magnitude, bit 3 the sign
+ * (crates/oominf-cpu/src/kernel.rs:8-11). */
+static const float E2M1[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                               -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+float oracle_e2m1_to_f32(uint8_t code) { return E2M1[code & 15]; }
+
+/* One row of an NVFP4 matrix against x (crates/oominf-cpu/src/kernel.rs:76-98,
+ * nvfp4_rows_scalar): w = e2m1(code) * (e4m3(scale) * scale_2), code c the low nibble of
+ * byte c / 2 for even c and the high nibble for odd c; acc += w * x in column order. */
+static float nvfp4_dot(const uint8_t* packed, const uint8_t* scales, float s2, int64_t cols, const float* x) {
+    float acc = 0.0f;
+    for (int64_t c = 0; c < cols; c++) {
+        uint8_t byte = packed[c / 2];
+        uint8_t code = (c % 2 == 0) ? (uint8_t)(byte & 0x0f) : (uint8_t)(byte >> 4);
+        float w = E2M1[code] * (oracle_e4m3_to_f32(scales[c / 16]) * s2);
+        acc += w * x[c];
+    }
+    return acc;
+}
+
+void oracle_nvfp4_rows(const uint8_t* packed, const uint8_t* scales, float s2, int64_t rows, int64_t cols,
+                       const float* x, int T, float* y) {
+    for (int64_t r = 0; r < rows; r++)
+        for (int t = 0; t < T; t++)
+            y[(size_t)t * rows + r] = nvfp4_dot(packed + r * cols / 2, scales + r * cols / 16, s2, cols,
+                                                x + (size_t)t * cols);
+}
+
+static float rec_f32(const uint8_t* rec, int64_t index) {
+    float v;
+    memcpy(&v, rec + index * 4, 4);
+    return v;
+}
+
+/* h[a, j] = silu(x_t . gate_j) * (x_t . up_j) over NVFP4 records (the HostExperts
+ * gate/up of crates/oominf-cpu/src/lib.rs:355-369 on kernel.rs:52-98; the device's
+ * moe_gate_up, crates/oominf-cuda/kernels/moe.cu:52-106). */
+void oracle_moe_gate_up_nvfp4(const uint8_t* const* recs, const int32_t* off, const int32_t* assign_tok, int n_e,
+                              const float* x, float* h, const OomNvfp4Record* geo) {
+    int64_t H = geo->hidden, I = geo->inter;
+    for (int i = 0; i < n_e; i++) {
+        const uint8_t* rec = recs[i];
+        float s2g = rec_f32(rec, geo->scale2[0]), s2u = rec_f32(rec, geo->scale2[1]);
+        for (int a = off[i]; a < off[i + 1]; a++) {
+            const float* xt = x + (size_t)assign_tok[a] * H;
+            for (int64_t j = 0; j < I; j++) {
+                float g = nvfp4_dot(rec + geo->gate_weight + j * H / 2, rec + geo->gate_scale + j * H / 16, s2g, H, xt);
+                float u = nvfp4_dot(rec + geo->up_weight + j * H / 2, rec + geo->up_scale + j * H / 16, s2u, H, xt);
+                h[(size_t)a * I + j] = siluf(g) * u;
+            }
+        }
+    }
+}
+
+/* y[a, r] = h[a] . down_r over NVFP4 records (moe.cu:108-151; kernel.rs:76-98). */
+void oracle_moe_down_nvfp4(const uint8_t* const* recs, const int32_t* off, int n_e, const float* h, float* y,
+                           const OomNvfp4Record* geo) {
+    int64_t H = geo->hidden, I = geo->inter;
+    for (int i = 0; i < n_e; i++) {
+        const uint8_t* rec = recs[i];
+        float s2 = rec_f32(rec, geo->scale2[2]);
+        for (int a = off[i]; a < off[i + 1]; a++)
+            for (int64_t r = 0; r < H; r++)
+                y[(size_t)a * H + r] = nvfp4_dot(rec + geo->down_weight + r * I / 2, rec + geo->down_scale + r * I / 16,
+                                                 s2, I, h + (size_t)a * I);
+    }
+}
+
+int oracle_moe_decode_nvfp4(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
+                            const OomNvfp4Record* geo, int32_t* ids, float* weights, float* out) {
+    int A = T * k;
+    int64_t H = geo->hidden, I = geo->inter;
+    oracle_router_topk(logits, T, E, k, ids, weights);
+    int32_t* experts = (int32_t*)malloc(sizeof(int32_t) * (size_t)(A + 1));
+    int32_t* off = (int32_t*)malloc(sizeof(int32_t) * (size_t)(A + 2));
+    int32_t* tok = (int32_t*)malloc(sizeof(int32_t) * (size_t)A);
+    int32_t* slot = (int32_t*)malloc(sizeof(int32_t) * (size_t)A);
+    int n_e = oracle_moe_plan(ids, T, k, E, experts, off, tok, slot);
+    if (n_e < 0) {
+        free(experts); free(off); free(tok); free(slot);
+        return -1;
+    }
+    const uint8_t** recs = (const uint8_t**)malloc(sizeof(void*) * (size_t)(n_e ? n_e : 1));
+    for (int i = 0; i < n_e; i++) recs[i] = all_recs[experts[i]];
+    float* h = (float*)malloc(sizeof(float) * (size_t)A * (size_t)I);
+    float* y = (float*)malloc(sizeof(float) * (size_t)A * (size_t)H);
+    oracle_moe_gate_up_nvfp4(recs, off, tok, n_e, x, h, geo);
+    oracle_moe_down_nvfp4(recs, off, n_e, h, y, geo);
+    oracle_moe_combine_slots(y, slot, weights, out, T, (int)H, k);
+    free(h); free(y); free(recs); free(experts); free(off); free(tok); free(slot);
+    return 0;
+}
+
 /* ---- prefill grouped GEMM (FP8 x FP8) ---------------------------------------- */
 
 void oracle_grouped_gemm_fp8(const uint8_t* const* recs, const int32_t* off, const int32_t* rows, int n_e,

@@ -81,6 +81,29 @@ def main():
         "source": "crates/oominf-cpu/src/lib.rs:446-494",
         "hidden": hidden, "inter": inter, "x": xs, "tokens": [1, 0], "y_per_token": ys, "rtol": 1e-4,
     }
+    # crates/oominf-metal/src/tests.rs:239-270 (nvfp4_gemm_matches_cpu_reference_with_signs_and_scales):
+    # 2 tokens x 3 rows x 32 columns, x[i] = (i - 31) / 17, packed byte i = (13 i) % 256,
+    # scale bytes [0x38, 0x30, 0x40, 0x38, 0x28, 0x40] whose values the test states as
+    # [1, 0.5, 2, 1, 0.25, 2], scale_2 = 0.75, E2M1 values by code as listed there;
+    # y = sum_c x * code * scale * 0.75 (tolerance 1e-4).
+    e2m1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+    vals = [(i - 31.0) / 17.0 for i in range(64)]
+    packed4 = [(i * 13) % 256 for i in range(48)]
+    sbytes = [0x38, 0x30, 0x40, 0x38, 0x28, 0x40]
+    svals = [1.0, 0.5, 2.0, 1.0, 0.25, 2.0]
+    y4 = []
+    for token in range(2):
+        for row in range(3):
+            acc = 0.0
+            for c in range(32):
+                nib = (packed4[row * 16 + c // 2] >> ((c % 2) * 4)) & 15
+                acc += float(np.float32(vals[token * 32 + c])) * e2m1[nib] * svals[row * 2 + c // 16] * 0.75
+            y4.append(acc)
+    out["nvfp4_rows_known_answer"] = {
+        "source": "crates/oominf-metal/src/tests.rs:239-270",
+        "tokens": 2, "rows": 3, "cols": 32, "x": vals, "packed": packed4, "scales": sbytes,
+        "scale_values": svals, "scale2": 0.75, "e2m1": e2m1, "y": y4, "tol": 1e-4,
+    }
     with open(os.path.join(HERE, "known_answers.json"), "w") as f:
         json.dump(out, f, indent=1)
     print("wrote", os.path.join(HERE, "known_answers.json"))

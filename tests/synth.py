@@ -98,6 +98,78 @@ def f64_moe(logits_ids_w, x: np.ndarray, recs, geo: oracle.Fp8Record) -> np.ndar
     return out
 
 
+# E2M1 values by code as the reference's tests list them (crates/oominf-cuda/tests/moe_tiled.rs:28-32,
+# crates/oominf-metal/src/tests.rs:252-254): the f64 decode below uses this table, not the oracle.
+E2M1_F64 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0])
+
+
+def nvfp4_parts(geo: oracle.Nvfp4Record):
+    """(weight offset, scale offset, scale_2 float index, rows, cols) of gate, up, down."""
+    H, I = geo.hidden, geo.inter
+    return [(geo.gate_weight, geo.gate_scale, geo.scale2[0], I, H), (geo.up_weight, geo.up_scale, geo.scale2[1], I, H),
+            (geo.down_weight, geo.down_scale, geo.scale2[2], H, I)]
+
+
+def nvfp4_record(geo: oracle.Nvfp4Record, seed: int, e: int, stride: int | None = None) -> np.ndarray:
+    """One NVFP4 record: random code bytes; scale bytes in [0x28, 0x50), positive and finite
+    (about 2^-2 .. 2^2, as crates/oominf-cuda/tests/moe_tiled.rs:58-78 draws them);
+    weight_scale_2 in [0.01, 0.03) and input_scale 1 in the scalars part."""
+    stride = stride or oracle.nvfp4_stride(geo)
+    rng = np.random.default_rng([seed, e, 4])
+    rec = np.zeros(stride, dtype=np.uint8)
+    scal = np.zeros(64, dtype=np.float32)
+    scal[[1, 3, 5]] = 1.0
+    for wo, so, s2i, n, k in nvfp4_parts(geo):
+        scal[s2i] = 0.01 + 0.02 * rng.random()
+        rec[wo:wo + n * k // 2] = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+        rec[so:so + n * k // 16] = rng.integers(0x28, 0x50, n * k // 16, dtype=np.uint8)
+    rec[:256] = scal.view(np.uint8)
+    return rec
+
+
+def nvfp4_records(geo: oracle.Nvfp4Record, seed: int, E: int, only=None) -> list[np.ndarray]:
+    """Records of E experts; experts outside `only` (when given) are left zero."""
+    stride = oracle.nvfp4_stride(geo)
+    return [nvfp4_record(geo, seed, e, stride) if only is None or e in only else np.zeros(stride, np.uint8)
+            for e in range(E)]
+
+
+def nvfp4_weights(rec: np.ndarray, geo: oracle.Nvfp4Record):
+    """(gate [I, H], up [I, H], down [H, I]) float64 weights of an NVFP4 record:
+    e2m1(code) * e4m3(scale) * scale_2 exactly (the reference's f64 test decode,
+    moe_tiled.rs:85-95), e4m3 through torch's float8_e4m3fn."""
+    import torch
+
+    out = []
+    for wo, so, s2i, n, k in nvfp4_parts(geo):
+        b = rec[wo:wo + n * k // 2].reshape(n, k // 2)
+        codes = np.empty((n, k), dtype=np.uint8)
+        codes[:, 0::2] = b & 15
+        codes[:, 1::2] = b >> 4
+        sc = torch.from_numpy(rec[so:so + n * k // 16].copy()).view(torch.float8_e4m3fn).double().numpy()
+        s2 = float(rec[:256].view(np.float32)[s2i])
+        out.append(E2M1_F64[codes] * np.repeat(sc.reshape(n, k // 16), 16, axis=1) * s2)
+    return out
+
+
+def f64_moe_nvfp4(ids_w, x: np.ndarray, recs, geo: oracle.Nvfp4Record) -> np.ndarray:
+    """f64 evaluation of the routed MoE FFN over NVFP4 records with the given ids and weights."""
+    ids, w = ids_w
+    T, k = ids.shape
+    out = np.zeros((T, geo.hidden))
+    cache = {}
+    for t in range(T):
+        xt = x[t].astype(np.float64)
+        for s in range(k):
+            e = int(ids[t, s])
+            if e not in cache:
+                cache[e] = nvfp4_weights(recs[e], geo)
+            g, u, d = cache[e]
+            gv, uv = g @ xt, u @ xt
+            out[t] += float(w[t, s]) * (d @ (gv / (1.0 + np.exp(-gv)) * uv))
+    return out
+
+
 def paged_attention_case(seed, H, Hkv, D, kv_len, page=16, spare_pages=3):
     """q bf16 [H, D]; K and V bf16 [n_pages, page, Hkv, D] with a few pages more than the
     sequence uses; the page table maps logical page i to a seeded random physical page."""

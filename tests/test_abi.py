@@ -64,6 +64,18 @@ def test_argument_errors_without_a_device():
     assert rc == -1 and b"multiple of 16" in lib.oom_last_error()
     rc = lib.oom_attn_decode_paged(null, 1, null, null, null, 1, 16, 10, 64, 8, 128, 0.1, null, 1, null, 0, null)
     assert rc == -1 and b"null buffer" in lib.oom_last_error()
+    g4 = hip.nvfp4_geometry(2560, 640)
+    bad4 = hip.nvfp4_geometry(2560, 648)
+    bad4.inter = 644
+    rc = lib.oom_moe_gate_up_nvfp4(null, null, null, 1, null, 1, null, ctypes.byref(bad4), null)
+    assert rc == -1 and b"multiples of 16" in lib.oom_last_error()
+    wide = hip.nvfp4_geometry(8192, 640)
+    rc = lib.oom_moe_down_nvfp4(null, null, 1, null, null, ctypes.byref(wide), null)
+    assert rc == -1 and b"at most 4096" in lib.oom_last_error()
+    rc = lib.oom_moe_decode_nvfp4(null, null, 1, null, 1, 512, 10, ctypes.byref(g4), null, null, null, 1, null, 0, null)
+    assert rc == -1 and b"null buffer" in lib.oom_last_error()
+    rc = lib.oom_moe_decode_nvfp4(null, null, 1, null, 1, 512, 40, ctypes.byref(g4), null, null, null, 1, null, 0, null)
+    assert rc == -1 and b"top-k > 32" in lib.oom_last_error()
 
 
 def test_workspace_sizes():
@@ -72,6 +84,16 @@ def test_workspace_sizes():
     need = hip.moe_decode_fp8_workspace_size(16, 128, 8, geo)
     assert need >= 16 * 8 * (4096 + 1536) * 4
     assert hip.moe_plan_size(16, 128, 8) == 2 + 2 * 128 + 2 * 128
+
+
+def test_nvfp4_geometry_agrees_with_oracle():
+    for h, i in [(2560, 640), (4096, 1536), (1040, 432)]:
+        a, b = hip.nvfp4_geometry(h, i), oracle.nvfp4_geometry(h, i)
+        assert [getattr(a, f) for f, _ in a._fields_[:-1]] == [getattr(b, f) for f, _ in b._fields_[:-1]]
+        assert list(a.scale2) == list(b.scale2)
+        assert hip.nvfp4_stride(a) == oracle.nvfp4_stride(b)
+    g = hip.nvfp4_geometry(2560, 640)
+    assert hip.moe_decode_nvfp4_workspace_size(1, 512, 10, g) >= 10 * (2560 + 640) * 4
 
 
 def test_geometry_agrees_with_oracle():
