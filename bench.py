@@ -9,7 +9,7 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 256 MB Infinity Cache.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config decode1|decode16|layer1|layer16|attn|prefill|copy]
+                    [--config decode1|decode16|layer1|layer16|nvfp4|attn|prefill|copy]
 
 Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
 kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
@@ -460,6 +460,110 @@ def bench_layer(args, T, config):
     return res
 
 
+def make_nvfp4_set(E, geo, stride, seed, torch):
+    """[E, stride] uint8 NVFP4 records: random code bytes, scale bytes in [0x28, 0x50)
+    (positive e4m3 values of about 2^-2 .. 2^2), weight_scale_2 in [0.01, 0.03)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    buf = torch.zeros((E, stride), dtype=torch.uint8, device="cuda")
+    H, I = geo.hidden, geo.inter
+    for wo, so, n, k in [(geo.gate_weight, geo.gate_scale, I, H), (geo.up_weight, geo.up_scale, I, H),
+                         (geo.down_weight, geo.down_scale, H, I)]:
+        buf[:, wo:wo + n * k // 2] = torch.randint(0, 256, (E, n * k // 2), generator=g, device="cuda",
+                                                   dtype=torch.uint8)
+        buf[:, so:so + n * k // 16] = torch.randint(0x28, 0x50, (E, n * k // 16), generator=g, device="cuda",
+                                                    dtype=torch.uint8)
+    scal = torch.zeros((E, 64), dtype=torch.float32, device="cuda")
+    for i in range(3):
+        scal[:, geo.scale2[i]] = 0.01 + 0.02 * torch.rand((E,), generator=g, device="cuda")
+    buf[:, :256] = scal.view(torch.uint8)
+    return buf
+
+
+def bench_nvfp4(args):
+    """One routed MoE decode step over NVFP4 (nvfp4-modelopt-g16) records at the released
+    model's routed geometry: 512 experts, top-10, hidden 2560, inter 640, batch 1, fresh
+    N(0, 1) logits each step, bf16 x (oom_moe_decode_nvfp4)."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    T, E, k, H, I = 1, 512, 10, 2560, 640
+    geo = hip.nvfp4_geometry(H, I)
+    stride = hip.nvfp4_stride(geo)
+    log(f"bench: nvfp4 decode T={T} E={E} k={k} H={H} I={I}; building 2 expert sets of {E * stride / 1e9:.2f} GB")
+    sets = [make_nvfp4_set(E, geo, stride, 2468 + s, torch) for s in range(2)]
+    addrs = [torch.tensor([b.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
+             for b in sets]
+    n = args.warmup + args.steps
+    g = torch.Generator(device="cuda")
+    g.manual_seed(97)
+    logits = torch.randn((n, T, E), generator=g, device="cuda").contiguous()
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ids = torch.empty((n, T, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n, T, k), dtype=torch.float32, device="cuda")
+    ws = torch.zeros(hip.moe_decode_nvfp4_workspace_size(T, E, k, geo), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        hip.moe_decode_nvfp4(logits[i], x, addrs[i % 2], k, geo, ids[i], wts[i], out, ws, stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(args.warmup, n):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    idn = ids[args.warmup:].cpu().numpy()
+    distinct = float(np.mean([len(np.unique(s_)) for s_ in idn]))
+    per_expert = 3 * H * I // 2 + 3 * H * I // 16 + 12  # codes, scale bytes, the three scale_2 floats
+    bytes_step = distinct * per_expert + 2 * T * H * 2
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    res = {
+        "metric": "MoE NVFP4 decode step us/token + achieved HBM GB/s (% of MI355X peak), 1 GPU",
+        "value": ms * 1e3 / T, "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "nvfp4 (e2m1 + e4m3 group-16 scales) weights, bf16 activations, fp32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": "MoE FFN decode step over nvfp4-modelopt-g16 records, batch 1: 512 experts top-10, "
+                               "hidden 2560, inter 640, random codes and scales, fresh N(0,1) logits; 2 expert sets "
+                               "alternate past the MALL",
+                   "batch": T, "experts": E, "top_k": k, "hidden": H, "inter": I,
+                   "distinct_experts_per_step": distinct},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": measured_traffic("nvfp4"),
+                     "kernel": "oom_moe_decode_nvfp4 step (router, plan, gate/up, down, combine launches)",
+                     "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
+    }
+    if not args.no_cpu:
+        import oracle
+
+        host = sets[0].cpu().numpy()
+        ogeo = oracle.nvfp4_geometry(H, I)
+        recs = [host[e] for e in range(E)]
+        rng = np.random.default_rng(8)
+        xs = x.float().cpu().numpy()
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            oracle.moe_decode_nvfp4(rng.standard_normal((T, E)).astype(np.float32), xs, recs, k, ogeo)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds and reps >= 3:
+                break
+        res["cpu_baseline"] = {"value": el / reps / T * 1e6, "unit": "us/token", "cores": 1, "kind": "port",
+                               "sample": f"{reps} steps of the same decode (fresh logits), the oracle's scalar "
+                                         f"restatement of the reference's nvfp4_rows_scalar path, one thread, on "
+                                         f"{cpu_model()}"}
+    return res
+
+
 PEAK_FP8_TFLOPS = 5000.0
 
 
@@ -559,8 +663,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "attn", "prefill",
-                                                            "copy"])
+    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "attn",
+                                                            "prefill", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -582,6 +686,8 @@ def main():
         res = bench_prefill(args)
     elif args.config == "decode1":
         res = bench_decode(args, 1, None, args.config)
+    elif args.config == "nvfp4":
+        res = bench_nvfp4(args)
     elif args.config in ("layer1", "layer16"):
         res = bench_layer(args, 1 if args.config == "layer1" else 16, args.config)
     else:

@@ -13,7 +13,8 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict
     int t = blockIdx.x, lane = threadIdx.x;
     int id = 0;
     float w = 0.0f;
-    if (E <= 256) route_token_regs(logits + (size_t)t * E, E, k, lane, id, w);
+    if (E <= 256) route_token_regs<4>(logits + (size_t)t * E, E, k, lane, id, w);
+    else if (E <= 512) route_token_regs<8>(logits + (size_t)t * E, E, k, lane, id, w);
     else route_token_wave(logits + (size_t)t * E, E, k, probs, lane, id, w);
     if (lane < k) {
         ids[(size_t)t * k + lane] = id;

@@ -98,36 +98,43 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v, int lane) {
     return (uint64_t)hi << 32 | lo;
 }
 
-// route_token_wave for E <= 256, without LDS round trips: lane l holds experts
-// l + 64 q (q < 4) in registers; sums keep the reference's order (sum32_xor_order).
+// route_token_wave for E <= 64 EQ (EQ = 4: 256, EQ = 8: 512), without LDS round trips:
+// lane l holds experts l + 64 q (q < EQ) in registers; sums keep the reference's order
+// (virtual thread l + 64 q of its 256-thread block adds experts l + 64 q and l + 64 q + 256
+// in id order, then sum32_xor_order).
 // The k picks rank experts by one 64-bit key, the probability's bits above the
 // complemented id: p >= 0, so a larger key is a larger p, and among equal p the lower
 // id, which is the reference's argmax with ties to the lower id. Each round is one wave
 // maximum of the lanes' best keys; the winner's lane drops that key (0 is below every
 // expert's key) and takes its next best.
+template <int EQ = 4>
 __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, int E, int k, int lane, int& id_out,
                                                  float& w_out) {
-    float lv[4];
+    static_assert(EQ == 4 || EQ == 8, "4 or 8 logits per lane");
+    float lv[EQ];
     float m = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
+    for (int q = 0; q < EQ; q++) {
         lv[q] = lane + 64 * q < E ? l[lane + 64 * q] : -INFINITY;
         m = fmaxf(m, lv[q]);
     }
     m = wave_max(m);
-    // E <= 256: virtual thread vt = lane + 64 q holds at most expert vt
-    float ex[4], w8[8];
+    // virtual thread vt = lane + 64 q (q < 4) holds experts vt and, with EQ = 8, vt + 256
+    float ex[EQ], w8[8];
+#pragma unroll
+    for (int q = 0; q < EQ; q++) ex[q] = lane + 64 * q < E ? expf(lv[q] - m) : 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        ex[q] = lane + 64 * q < E ? expf(lv[q] - m) : 0.0f;
-        const float s = sum32_xor_order(0.0f + ex[q]);
+        float vt = 0.0f + ex[q];
+        if constexpr (EQ == 8) vt = vt + ex[q + 4];
+        const float s = sum32_xor_order(vt);
         w8[2 * q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
         w8[2 * q + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
     }
     const float sum = ((w8[0] + w8[4]) + (w8[2] + w8[6])) + ((w8[1] + w8[5]) + (w8[3] + w8[7]));
-    uint64_t key[4], best_mine = 0;
+    uint64_t key[EQ], best_mine = 0;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
+    for (int q = 0; q < EQ; q++) {
         const int e = lane + 64 * q;
         key[q] = e < E ? ((uint64_t)__float_as_uint(ex[q] / sum) << 32) | (uint32_t)~(uint32_t)e : 0ull;
         best_mine = key[q] > best_mine ? key[q] : best_mine;
@@ -140,7 +147,7 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, in
         if ((e & 63) == lane) {
             best_mine = 0;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
+            for (int q = 0; q < EQ; q++) {
                 if (key[q] == best) key[q] = 0;
                 best_mine = key[q] > best_mine ? key[q] : best_mine;
             }

@@ -79,7 +79,8 @@ def test_e4m3_decode_every_code_on_device(hip):
 # ---- router -------------------------------------------------------------------------
 
 @pytest.mark.parametrize("T,E,k,zipf", [(1, 128, 8, None), (16, 128, 8, 1.1), (64, 128, 8, 1.1),
-                                        (2048, 128, 8, 1.1), (3, 300, 5, None), (2, 8192, 32, None)])
+                                        (2048, 128, 8, 1.1), (3, 300, 5, None), (2, 8192, 32, None),
+                                        (1, 512, 10, None), (7, 400, 8, 1.1), (2, 512, 32, None)])
 def test_router_bit_exact(hip, T, E, k, zipf):
     import torch
 
