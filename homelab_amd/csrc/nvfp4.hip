@@ -147,10 +147,11 @@ __device__ __forceinline__ void piece_dot(const float* f, const float4* xs4, int
     }
 }
 
-// One gate/up pass over TB staged tokens (nb real): the wave's rows j0 + 2p + half.
-template <int TB>
+// One gate/up pass over TB staged tokens (nb real): the wave's rows j0 + 2p + half;
+// put(t, j, v) stores h of staged token t at intermediate row j.
+template <int TB, typename Put>
 __device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amdgpu_buffer_rsrc_t r, float s2g,
-                                         float s2u, int j0, int lane, int nb, int a0, float* h) {
+                                         float s2u, int j0, int lane, int nb, Put put) {
     const int H = g.H, I = g.I, CH = (H + 1023) >> 10, hg = H >> 4;
     const int half = lane >> 5, l = lane & 31;
     float acc[2 * TB * N4_GP];  // [gate|up][t][p]
@@ -213,7 +214,7 @@ __device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amd
     const int v = l / GROUP;
     if (l % GROUP == 0 && v < NV / 2) {
         const int t = v / N4_GP, j = j0 + 2 * (v % N4_GP) + half;
-        if (t < nb && j < I) h[(size_t)(a0 + t) * I + j] = siluf(tot) * up;
+        if (t < nb && j < I) put(t, j, siluf(tot) * up);
     }
 }
 
@@ -237,15 +238,17 @@ __global__ void __launch_bounds__(256) moe_gate_up_nvfp4_kernel(const uint64_t* 
         __syncthreads();
         stage4<XDT>(xs4, x, g.H, CH, nb, [&](int t) { return assign_tok[a0 + t]; });
         __syncthreads();
-        if (nb == 1) gu4_pass<1>(xs4, g, r, s2g, s2u, j0, lane, nb, a0, h);
-        else gu4_pass<2>(xs4, g, r, s2g, s2u, j0, lane, nb, a0, h);
+        const auto put = [&](int t, int j, float v) { h[(size_t)(a0 + t) * g.I + j] = v; };
+        if (nb == 1) gu4_pass<1>(xs4, g, r, s2g, s2u, j0, lane, nb, put);
+        else gu4_pass<2>(xs4, g, r, s2g, s2u, j0, lane, nb, put);
     }
 }
 
-// One down pass over TB staged h rows (nb real): the wave's output rows r0 + 2p + half.
-template <int TB>
+// One down pass over TB staged h rows (nb real): the wave's output rows r0 + 2p + half;
+// put(t, row, v) stores y of staged row t at output row `row`.
+template <int TB, typename Put>
 __device__ __forceinline__ void dn4_pass(const float4* xs4, const Rec4& g, __amdgpu_buffer_rsrc_t r, float s2,
-                                         int r0, int lane, int nb, int a0, float* y) {
+                                         int r0, int lane, int nb, Put put) {
     const int H = g.H, I = g.I, CH = (I + 1023) >> 10, ig = I >> 4;
     const int half = lane >> 5, l = lane & 31;
     float acc[TB * N4_DP];
@@ -293,7 +296,7 @@ __device__ __forceinline__ void dn4_pass(const float4* xs4, const Rec4& g, __amd
     const int v = l / GROUP;
     if (l % GROUP == 0) {
         const int t = v / N4_DP, row = r0 + 2 * (v % N4_DP) + half;
-        if (t < nb && row < H) y[(size_t)(a0 + t) * H + row] = tot;
+        if (t < nb && row < H) put(t, row, tot);
     }
 }
 
@@ -315,8 +318,9 @@ __global__ void __launch_bounds__(256) moe_down_nvfp4_kernel(const uint64_t* __r
         __syncthreads();
         stage4<OOM_F32>(xs4, h, g.I, CH, nb, [&](int t) { return a0 + t; });
         __syncthreads();
-        if (nb == 1) dn4_pass<1>(xs4, g, r, s2, r0, lane, nb, a0, y);
-        else dn4_pass<2>(xs4, g, r, s2, r0, lane, nb, a0, y);
+        const auto put = [&](int t, int row, float v) { y[(size_t)(a0 + t) * g.H + row] = v; };
+        if (nb == 1) dn4_pass<1>(xs4, g, r, s2, r0, lane, nb, put);
+        else dn4_pass<2>(xs4, g, r, s2, r0, lane, nb, put);
     }
 }
 
@@ -337,6 +341,170 @@ static int check_geo4(const OomNvfp4Record* geo, const char* who) {
 }
 
 static size_t stage_lds(int64_t width) { return (size_t)N4_TB * cdiv(width, 1024) * 1024 * sizeof(float); }
+
+// ---- one token in one launch ---------------------------------------------------------------
+// The step of oom_moe_decode_nvfp4 for T = 1 as one persistent kernel, the same arithmetic
+// as the five-launch step (router, plan, gate/up, down, slot-order combine):
+//   - every block routes the token on wave 0 (route_token_regs: the router kernel's picks
+//     and weights) while its other waves stage x into LDS; with one token each picked
+//     expert has one assignment, so h row s belongs to slot s and no plan is built;
+//   - phase 1: wave items (slot, 2 N4_GP intermediate rows) in global wave order, h stored
+//     device-coherent (waves of other XCDs read it after the barrier);
+//   - one grid barrier (every block resident: the grid never exceeds the occupancy limit);
+//   - phase 2: block b takes output tiles of 2 N4_DP rows b, b + G, ...; it stages the k
+//     h rows once (device-coherent loads), its waves take the tile's rows of slots
+//     wave, wave + 4, ... into LDS, and the tile's outputs sum w[s] y_s in slot order
+//     (moe_combine_kernel's fmaf order), so no y buffer or combine launch is needed.
+constexpr int N4F_KMAX = 16;                 // expert slots of the one-launch step
+constexpr size_t N4F_LDS_MAX = 64 * 1024;    // staged x or h rows
+constexpr uint32_t N4F_SPIN_LIMIT = 1u << 22;
+
+struct Fused4Args {
+    const float* logits;
+    const void* x;
+    const uint64_t* all_recs;
+    int E, k;
+    Rec4 g;
+    int32_t* ids;
+    float* weights;
+    void* out;
+    float* h;  // [k, I]
+    uint32_t* bar;
+    uint32_t* status;
+};
+
+// Rows 0 .. rows - 1 of h (f32, width K) into LDS in stage4's lane order through
+// device-coherent 16-byte loads, four in flight per thread; zeros past K.
+__device__ __forceinline__ void stage_rows_dev(float4* xs4, const float* h, int K, int CH, int rows) {
+    const int span = CH * 1024, nvec = rows * span / 4;
+    const __amdgpu_buffer_rsrc_t hr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(h), (short)0, rows * K * 4, BUF_FLAGS);
+    for (int base = 0; base < nvec; base += 256 * 4) {
+        uint4 v[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const int i = base + (int)threadIdx.x + 256 * n;
+            const int t = i * 4 / span, kk = i * 4 - t * span;
+            const auto q = __builtin_amdgcn_raw_buffer_load_b128(hr, i < nvec && kk < K ? (t * K + kk) * 4 : OOB, 0,
+                                                                 BUF_SC1);
+            v[n] = make_uint4(q[0], q[1], q[2], q[3]);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const int i = base + (int)threadIdx.x + 256 * n;
+            if (i >= nvec) break;
+            const int t = i * 4 / span, kk = i * 4 - t * span;
+            const int c = kk >> 10, l = (kk & 1023) >> 5, j = kk & 31;
+            xs4[((t * CH + c) * 8 + (j >> 2)) * 32 + l] = make_float4(__uint_as_float(v[n].x), __uint_as_float(v[n].y),
+                                                                      __uint_as_float(v[n].z), __uint_as_float(v[n].w));
+        }
+    }
+}
+
+template <int XDT, int EQ, int ODT>
+__global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
+    extern __shared__ float4 xs4[];
+    __shared__ uint64_t recs_l[N4F_KMAX];
+    __shared__ float w_l[N4F_KMAX];
+    __shared__ float ylds[N4F_KMAX][2 * N4_DP];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const Rec4& g = a.g;
+    const int k = a.k, H = g.H, I = g.I;
+    if (wave == 0) {
+        int id = 0;
+        float w = 0.0f;
+        route_token_regs<EQ>(a.logits, a.E, k, lane, id, w);
+        if (lane < k) {
+            recs_l[lane] = a.all_recs[id];
+            w_l[lane] = w;
+            if (blockIdx.x == 0) {
+                a.ids[lane] = id;
+                a.weights[lane] = w;
+            }
+        }
+    }
+    const int CHH = (H + 1023) >> 10, CHI = (I + 1023) >> 10;
+    stage4<XDT>(xs4, a.x, H, CHH, 1, [](int) { return 0; });
+    __syncthreads();
+    // ---- phase 1: h[s, j0 .. j0 + 2 N4_GP) per wave item ----
+    const int ipe = (I + 2 * N4_GP - 1) / (2 * N4_GP), NG = k * ipe;
+    const int NW = gridDim.x * N4_WAVES;
+    for (int it = blockIdx.x * N4_WAVES + wave; it < NG; it += NW) {
+        const int s = it / ipe, j0 = (it - s * ipe) * 2 * N4_GP;
+        const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs_l[s], g.bytes);
+        const float s2g = ldf(r, g.s2g), s2u = ldf(r, g.s2u);
+        float* hs = a.h + (size_t)s * I;
+        gu4_pass<1>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
+    }
+    wait_mem();  // this wave's h stores are complete before its block arrives
+    grid_barrier_words(a.bar, a.status, N4F_SPIN_LIMIT);
+    // ---- phase 2: the k h rows once, then per output tile the slot rows and the combine ----
+    stage_rows_dev(xs4, a.h, I, CHI, k);
+    __syncthreads();
+    const int tiles = (H + 2 * N4_DP - 1) / (2 * N4_DP);
+    for (int tb = blockIdx.x; tb < tiles; tb += gridDim.x) {
+        const int r0 = tb * 2 * N4_DP;
+        for (int s = wave; s < k; s += N4_WAVES) {
+            const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs_l[s], g.bytes);
+            const float s2 = ldf(r, g.s2d);
+            dn4_pass<1>(xs4 + (size_t)s * CHI * 256, g, r, s2, r0, lane, 1,
+                        [&](int, int row, float v) { ylds[s][row - r0] = v; });
+        }
+        __syncthreads();
+        const int row = r0 + (int)threadIdx.x;
+        if (threadIdx.x < 2 * N4_DP && row < H) {
+            float acc = 0.0f;
+            for (int s = 0; s < k; s++) acc = fmaf(w_l[s], ylds[s][threadIdx.x], acc);
+            store_out<ODT>(a.out, row, acc);
+        }
+        __syncthreads();
+    }
+}
+
+// LDS of the one-launch kernel: x staged for one token, then the k h rows.
+static size_t fused4_lds(const OomNvfp4Record& g, int k) {
+    return std::max(stage_lds(g.hidden), (size_t)k * cdiv(g.inter, 1024) * 1024 * sizeof(float));
+}
+
+static bool fused4_ok(int T, int E, int k, const OomNvfp4Record& g) {
+    return T == 1 && E <= 512 && k <= N4F_KMAX && fused4_lds(g, k) <= N4F_LDS_MAX &&
+           (int64_t)k * g.inter * 4 < OOB;
+}
+
+template <int XDT, int EQ, int ODT>
+static int launch_fused4_t(const Fused4Args& a, size_t lds, hipStream_t st) {
+    static thread_local int cached_dev = -1, cached_blocks = 0;
+    static thread_local size_t cached_lds = 0;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev != cached_dev || lds != cached_lds) {
+        int cus = 0, per = 0;
+        cached_blocks = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_nvfp4_1_kernel<XDT, EQ, ODT>, 256, lds) ==
+                hipSuccess)
+            cached_blocks = cus * per;
+        cached_dev = dev;
+        cached_lds = lds;
+    }
+    if (cached_blocks <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_nvfp4: occupancy query failed");
+    // enough blocks for one wave item each or one output tile each, never more than fit
+    const int64_t items = cdiv((int64_t)a.k * cdiv(a.g.I, 2 * N4_GP), N4_WAVES);
+    const int64_t tiles = cdiv(a.g.H, 2 * N4_DP);
+    const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, std::max(items, tiles)));
+    hipLaunchKernelGGL((moe_decode_nvfp4_1_kernel<XDT, EQ, ODT>), dim3(blocks), dim3(256), lds, st, a);
+    return launched("oom_moe_decode_nvfp4");
+}
+
+template <int XDT, int EQ>
+static int launch_fused4_o(const Fused4Args& a, int odt, size_t lds, hipStream_t st) {
+    return odt == OOM_BF16 ? launch_fused4_t<XDT, EQ, OOM_BF16>(a, lds, st) : launch_fused4_t<XDT, EQ, OOM_F32>(a, lds, st);
+}
+
+template <int XDT>
+static int launch_fused4_e(const Fused4Args& a, int odt, size_t lds, hipStream_t st) {
+    return a.E <= 256 ? launch_fused4_o<XDT, 4>(a, odt, lds, st) : launch_fused4_o<XDT, 8>(a, odt, lds, st);
+}
 
 static int launch_gate_up4(const uint64_t* recs, const int32_t* off, const int32_t* tok, int grid_e, const void* x,
                            int xdt, float* h, const OomNvfp4Record& geo, const int32_t* n_e_dev, hipStream_t st) {
@@ -360,7 +528,8 @@ static int launch_down4(const uint64_t* recs, const int32_t* off, int grid_e, co
     return launched("oom_moe_down_nvfp4");
 }
 
-// Workspace of oom_moe_decode_nvfp4: plan | recs | h | y.
+// Workspace of oom_moe_decode_nvfp4: the decode workspace header (barrier words and
+// status of the one-launch kernel) | plan | recs | h | y.
 struct Decode4Ws {
     size_t plan, recs, h, y, total;
 };
@@ -370,8 +539,8 @@ static size_t a256(size_t v) { return (v + 255) & ~size_t(255); }
 static Decode4Ws decode4_ws(int T, int E, int k, const OomNvfp4Record& g) {
     Decode4Ws w;
     const size_t A = (size_t)T * k;
-    w.plan = 0;
-    w.recs = a256(PlanView::size(E, (int)A) * sizeof(int32_t));
+    w.plan = WS_HEADER;
+    w.recs = w.plan + a256(PlanView::size(E, (int)A) * sizeof(int32_t));
     w.h = w.recs + a256(std::min<size_t>(E, A) * sizeof(uint64_t));
     w.y = w.h + a256(A * (size_t)g.inter * sizeof(float));
     w.total = w.y + a256(A * (size_t)g.hidden * sizeof(float));
@@ -431,6 +600,13 @@ extern "C" int oom_moe_decode_nvfp4(const float* logits, const void* x, int x_dt
     float* h = reinterpret_cast<float*>(base + w.h);
     float* y = reinterpret_cast<float*>(base + w.y);
     hipStream_t st = as_stream(stream);
+    if (fused4_ok(T, E, k, *geo)) {
+        Fused4Args a{logits, x, all_recs, E, k, rec4_of(*geo), ids, weights, out, h,
+                     reinterpret_cast<uint32_t*>(base + WS_BAR), reinterpret_cast<uint32_t*>(base + WS_STATUS)};
+        const size_t lds = fused4_lds(*geo, k);
+        return x_dtype == OOM_BF16 ? launch_fused4_e<OOM_BF16>(a, out_dtype, lds, st)
+                                   : launch_fused4_e<OOM_F32>(a, out_dtype, lds, st);
+    }
     const int A = T * k;
     const PlanView pv{plan, E, A};
     if (int rc = oom_router_topk(logits, ids, weights, T, E, k, stream)) return rc;

@@ -160,3 +160,67 @@ def test_decode_nvfp4_matches_oracle(hip, T, E, k, zipf, H, I, xf32):
     f64 = synth.f64_moe_nvfp4((want_ids, want_w), x, recs, geo)
     err = np.abs(out32.cpu().numpy() - f64).max()
     assert err <= 2e-5 * np.abs(f64).max(), f"f32 out: max err {err:.3e} vs scale {np.abs(f64).max():.3e}"
+
+
+@pytest.mark.parametrize("E,k,H,I,xf32", [
+    (512, 10, 2560, 640, False),   # the released model's routed experts (8 logits a lane in the router)
+    (64, 8, 4096, 1536, False),    # the FP8 benchmark's widths: 64 KiB of staged h rows
+    (100, 16, 1040, 432, True),    # 16 slots, widths ending inside a piece, f32 activations
+    (16, 1, 256, 128, False),      # one slot; fewer output tiles than blocks
+])
+def test_decode_nvfp4_one_launch_matches_stages(hip, E, k, H, I, xf32):
+    """One token takes the one-launch kernel; its f32 output equals, bit for bit, the staged
+    launches (router, gate/up, down, slot-order combine) over the same routing, on three
+    calls in a row on one workspace (the grid barrier's generations advance)."""
+    import torch
+
+    print(f"case: nvfp4 one-launch E={E} k={k} H={H} I={I} x={'f32' if xf32 else 'bf16'}", flush=True)
+    seed = 900 + E + H
+    geo = oracle.nvfp4_geometry(H, I)
+    hgeo = hip.nvfp4_geometry(H, I)
+    logits = synth.decode_logits(seed, 1, E, None)
+    ids0, _ = oracle.router_topk(logits, k)
+    recs = synth.nvfp4_records(geo, seed, E, only=set(int(e) for e in np.unique(ids0)))
+    xb = synth.activations_bf16(seed, 1, H)
+    x = oracle.bf16_to_f32(xb)
+    xd = _dev(x) if xf32 else _bf16(xb)
+    buf, addrs = _upload(recs)
+    ld = _dev(logits)
+    # staged: the router kernel, the oracle's grouping, then gate/up, down and combine launches
+    ids_s = torch.empty((1, k), dtype=torch.int32, device="cuda")
+    w_s = torch.empty((1, k), dtype=torch.float32, device="cuda")
+    hip.router_topk(ld, ids_s, w_s, k)
+    torch.cuda.synchronize()
+    experts, off, tok, slot = oracle.moe_plan(ids_s.cpu().numpy(), E)
+    n_e = len(experts)
+    recs_s = addrs[torch.from_numpy(np.asarray(experts, dtype=np.int64)).cuda()]
+    h = torch.empty((k, I), dtype=torch.float32, device="cuda")
+    y = torch.empty((k, H), dtype=torch.float32, device="cuda")
+    hip.moe_gate_up_nvfp4(recs_s, _dev(np.asarray(off, dtype=np.int32)), _dev(np.asarray(tok, dtype=np.int32)), n_e,
+                          xd, h, hgeo)
+    hip.moe_down_nvfp4(recs_s, _dev(np.asarray(off, dtype=np.int32)), n_e, h, y, hgeo)
+    want = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    hip.moe_combine_slots(y, _dev(np.asarray(slot, dtype=np.int32).reshape(1, k)), w_s, want)
+    torch.cuda.synchronize()
+    want = want.cpu().numpy()
+    ws = torch.zeros(hip.moe_decode_nvfp4_workspace_size(1, E, k, hgeo), dtype=torch.uint8, device="cuda")
+    ids = torch.empty((1, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((1, k), dtype=torch.float32, device="cuda")
+    for rep in range(3):
+        out = torch.full((1, H), float("nan"), dtype=torch.float32, device="cuda")
+        hip.moe_decode_nvfp4(ld, xd, addrs, k, hgeo, ids, w, out, ws)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ids.cpu().numpy(), ids_s.cpu().numpy(), err_msg=f"rep {rep}")
+        np.testing.assert_array_equal(w.cpu().numpy(), w_s.cpu().numpy(), err_msg=f"rep {rep}")
+        got = out.cpu().numpy()
+        diff = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+        assert diff.size == 0, f"rep {rep}: {diff.size} of {H} differ, first at {diff[:4]}"
+    # and the oracle's tolerance on a bf16 output
+    want_ids, want_w, want_or = oracle.moe_decode_nvfp4(logits, x, recs, k, geo)
+    outb = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
+    hip.moe_decode_nvfp4(ld, xd, addrs, k, hgeo, ids, w, outb, ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy(), want_ids)
+    got = outb.float().cpu().numpy()
+    bad = ~np.isclose(got, want_or, rtol=RTOL, atol=ATOL)
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside; worst {np.abs(got - want_or)[bad].max():.3e}"
