@@ -149,7 +149,8 @@ __device__ __forceinline__ void piece_dot(const float* f, const float4* xs4, int
 
 // One gate/up pass over TB staged tokens (nb real): the wave's rows j0 + 2p + half;
 // put(t, j, v) stores h of staged token t at intermediate row j.
-template <int TB, typename Put>
+// CS chunks of 1024 columns load per round (all of a row's with CS = 4).
+template <int TB, int CS = 2, typename Put>
 __device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amdgpu_buffer_rsrc_t r, float s2g,
                                          float s2u, int j0, int lane, int nb, Put put) {
     const int H = g.H, I = g.I, CH = (H + 1023) >> 10, hg = H >> 4;
@@ -157,14 +158,14 @@ __device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amd
     float acc[2 * TB * N4_GP];  // [gate|up][t][p]
 #pragma unroll
     for (int i = 0; i < 2 * TB * N4_GP; i++) acc[i] = 0.0f;
-    for (int c0 = 0; c0 < CH; c0 += 2) {
-        uint4 wg[N4_GP][2], wu[N4_GP][2];
-        uint32_t bg[N4_GP][2][2], bu[N4_GP][2][2];
+    for (int c0 = 0; c0 < CH; c0 += CS) {
+        uint4 wg[N4_GP][CS], wu[N4_GP][CS];
+        uint32_t bg[N4_GP][CS][2], bu[N4_GP][CS][2];
 #pragma unroll
         for (int p = 0; p < N4_GP; p++) {
             const int j = j0 + 2 * p + half;
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
+            for (int c = 0; c < CS; c++) {
                 const int col = (c0 + c) * 1024 + 32 * l;
                 const bool ok = j < I && c0 + c < CH && col < H;
                 wg[p][c] = ld16(r, ok ? g.gw + j * (H >> 1) + (col >> 1) : OOB);
@@ -178,7 +179,7 @@ __device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amd
             }
         }
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
+        for (int c = 0; c < CS; c++) {
             if (c0 + c >= CH) break;
             const int col = (c0 + c) * 1024 + 32 * l;
 #pragma unroll
@@ -351,9 +352,11 @@ static size_t stage_lds(int64_t width) { return (size_t)N4_TB * cdiv(width, 1024
 //   - phase 1: wave items (slot, 2 N4_GP intermediate rows) in global wave order, h stored
 //     device-coherent (waves of other XCDs read it after the barrier);
 //   - one grid barrier (every block resident: the grid never exceeds the occupancy limit);
+//   - phase 1 loads all of an item's row chunks in one round (gu4_pass<1, 4>);
 //   - phase 2: block b takes output tiles of 2 N4_DP rows b, b + G, ...; it stages the k
 //     h rows once (device-coherent loads), its waves take the tile's rows of slots
-//     wave, wave + 4, ... into LDS, and the tile's outputs sum w[s] y_s in slot order
+//     wave, wave + 4, ... into LDS (inter <= 2048: one load round a slot, the next
+//     slot's loads in flight), and the tile's outputs sum w[s] y_s in slot order
 //     (moe_combine_kernel's fmaf order), so no y buffer or combine launch is needed.
 constexpr int N4F_KMAX = 16;                 // expert slots of the one-launch step
 constexpr size_t N4F_LDS_MAX = 64 * 1024;    // staged x or h rows
@@ -401,6 +404,68 @@ __device__ __forceinline__ void stage_rows_dev(float4* xs4, const float* h, int 
     }
 }
 
+
+// dn4_pass<1> in two halves for inter <= 2048 (one load round), so a wave's next slot
+// loads while the current one is reduced: the loaded weights, scale bytes and scale_2 ...
+struct Dn4W {
+    uint4 wd[N4_DP][2];
+    uint32_t bd[N4_DP][2][2];
+    float s2;
+};
+
+__device__ __forceinline__ void dn4_load(Dn4W& w, const Rec4& g, __amdgpu_buffer_rsrc_t r, int r0, int lane) {
+    const int H = g.H, I = g.I, CH = (I + 1023) >> 10, ig = I >> 4;
+    const int half = lane >> 5, l = lane & 31;
+#pragma unroll
+    for (int p = 0; p < N4_DP; p++) {
+        const int row = r0 + 2 * p + half;
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int col = c * 1024 + 32 * l;
+            const bool ok = row < H && c < CH && col < I;
+            w.wd[p][c] = ld16(r, ok ? g.dw + row * (I >> 1) + (col >> 1) : OOB);
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+                w.bd[p][c][q] = ldb(r, ok && (col >> 4) + q < ig ? g.ds + row * ig + (col >> 4) + q : OOB);
+        }
+    }
+    w.s2 = ldf(r, g.s2d);
+}
+
+// ... and dn4_pass<1>'s arithmetic on them against staged row 0 of xs4.
+template <typename Put>
+__device__ __forceinline__ void dn4_compute(const Dn4W& w, const float4* xs4, const Rec4& g, int r0, int lane,
+                                            Put put) {
+    const int H = g.H, I = g.I, CH = (I + 1023) >> 10, ig = I >> 4;
+    const int half = lane >> 5, l = lane & 31;
+    float acc[N4_DP];
+#pragma unroll
+    for (int p = 0; p < N4_DP; p++) acc[p] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        if (c >= CH) break;
+        const int col = c * 1024 + 32 * l;
+#pragma unroll
+        for (int p = 0; p < N4_DP; p++) {
+            float sd[2];
+#pragma unroll
+            for (int q = 0; q < 2; q++) sd[q] = (col >> 4) + q < ig ? e4m3_byte(w.bd[p][c][q]) * w.s2 : 0.0f;
+            float f[32];
+            e2m1x32(w.wd[p][c], f);
+            float p0, p1;
+            piece_dot(f, xs4, 0, CH, c, l, p0, p1);
+            acc[p] = fmaf(p1, sd[1], fmaf(p0, sd[0], acc[p]));
+        }
+    }
+    constexpr int GROUP = 32 / N4_DP;
+    const float tot = wave_sum_multi<N4_DP, 16>(acc, lane);
+    const int v = l / GROUP;
+    if (l % GROUP == 0) {
+        const int row = r0 + 2 * v + half;
+        if (row < H) put(row, tot);
+    }
+}
+
 template <int XDT, int EQ, int ODT>
 __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     extern __shared__ float4 xs4[];
@@ -434,7 +499,7 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
         const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs_l[s], g.bytes);
         const float s2g = ldf(r, g.s2g), s2u = ldf(r, g.s2u);
         float* hs = a.h + (size_t)s * I;
-        gu4_pass<1>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
+        gu4_pass<1, 4>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
     }
     wait_mem();  // this wave's h stores are complete before its block arrives
     grid_barrier_words(a.bar, a.status, N4F_SPIN_LIMIT);
@@ -444,11 +509,19 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     const int tiles = (H + 2 * N4_DP - 1) / (2 * N4_DP);
     for (int tb = blockIdx.x; tb < tiles; tb += gridDim.x) {
         const int r0 = tb * 2 * N4_DP;
-        for (int s = wave; s < k; s += N4_WAVES) {
-            const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs_l[s], g.bytes);
-            const float s2 = ldf(r, g.s2d);
-            dn4_pass<1>(xs4 + (size_t)s * CHI * 256, g, r, s2, r0, lane, 1,
-                        [&](int, int row, float v) { ylds[s][row - r0] = v; });
+        // slots wave, wave + 4, ...: the next slot's loads are in flight while the current
+        // one is reduced (a slot past k loads through an empty resource: zeros, no access)
+        const auto rsrc_of = [&](int s) { return uniform_rsrc(recs_l[s < k ? s : 0], s < k ? g.bytes : 0); };
+        Dn4W wa, wb;
+        dn4_load(wa, g, rsrc_of(wave), r0, lane);
+        for (int s = wave; s < k;) {
+            dn4_load(wb, g, rsrc_of(s + N4_WAVES), r0, lane);
+            dn4_compute(wa, xs4 + (size_t)s * CHI * 256, g, r0, lane, [&](int row, float v) { ylds[s][row - r0] = v; });
+            s += N4_WAVES;
+            if (s >= k) break;
+            dn4_load(wa, g, rsrc_of(s + N4_WAVES), r0, lane);
+            dn4_compute(wb, xs4 + (size_t)s * CHI * 256, g, r0, lane, [&](int row, float v) { ylds[s][row - r0] = v; });
+            s += N4_WAVES;
         }
         __syncthreads();
         const int row = r0 + (int)threadIdx.x;
@@ -467,7 +540,7 @@ static size_t fused4_lds(const OomNvfp4Record& g, int k) {
 }
 
 static bool fused4_ok(int T, int E, int k, const OomNvfp4Record& g) {
-    return T == 1 && E <= 512 && k <= N4F_KMAX && fused4_lds(g, k) <= N4F_LDS_MAX &&
+    return T == 1 && E <= 512 && k <= N4F_KMAX && g.inter <= 2048 && fused4_lds(g, k) <= N4F_LDS_MAX &&
            (int64_t)k * g.inter * 4 < OOB;
 }
 

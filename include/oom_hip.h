@@ -200,7 +200,10 @@ int oom_moe_down_nvfp4(const uint64_t* recs, const int32_t* off, int n_experts, 
 /* One decode MoE FFN step over NVFP4 records with no host synchronisation: router
  * top-k, device routing plan, gate/up + SwiGLU, down and slot-order weighted combine, as
  * oom_moe_decode_fp8 (same arguments, NVFP4 geometry). The routed part of Moe::forward
- * (crates/oominf-models-qwen/src/moe.rs:290-366) on the released record format. */
+ * (crates/oominf-models-qwen/src/moe.rs:290-366) on the released record format. One
+ * token (T = 1, E <= 512, k <= 16, inter <= 2048) runs as one launch with one grid
+ * barrier over the workspace header, with the staged launches' arithmetic; the workspace
+ * must be zero-filled once before its first use (oom_workspace_init). */
 size_t oom_moe_decode_nvfp4_workspace_size(int T, int E, int k, const OomNvfp4Record* geo);
 int oom_moe_decode_nvfp4(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T, int E,
                          int k, const OomNvfp4Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
