@@ -9,7 +9,7 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 256 MB Infinity Cache.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config decode1|decode16|layer1|layer16|nvfp4|attn|prefill|copy]
+                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|prefill|copy]
 
 Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
 kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
@@ -538,7 +538,7 @@ def bench_nvfp4(args):
                    "distinct_experts_per_step": distinct},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
                      "traffic": measured_traffic("nvfp4"),
-                     "kernel": "oom_moe_decode_nvfp4 step (router, plan, gate/up, down, combine launches)",
+                     "kernel": "moe_decode_nvfp4_1_kernel (oom_moe_decode_nvfp4, one launch for one token)",
                      "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
     }
     if not args.no_cpu:
@@ -658,12 +658,108 @@ def bench_prefill(args):
     return res
 
 
+
+PEAK_PCIE_GBS = 64.0  # PCIe 5.0 x16, one direction
+
+
+def bench_offload(args):
+    """The batch-1 FP8 decode step with every expert in the host tier: per step the routed
+    experts' records (8 x 18.9 MB) copy from pinned host memory into device slots on a copy
+    queue, double-buffered so step i+1's copies run beside step i's compute, ordered with
+    events (oom_copy_records_to_device, oom_event_record, oom_stream_wait_event). The
+    routing of every step is computed on the device before the timed region."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    T, E, k, H, I = 1, 128, 8, 4096, 1536
+    geo = hip.record_geometry(H, I)
+    stride = hip.record_stride(geo)
+    steps = min(args.steps, 50)
+    warmup = min(args.warmup, 5)
+    n = warmup + steps
+    log(f"bench: offload decode T={T} E={E} k={k} H={H} I={I}; {E * stride / 1e9:.2f} GB of records in pinned host memory")
+    dev_set = make_expert_set(E, geo, stride, 1234, torch)
+    host = hip.PinnedHost(E * stride)
+    host.array()[:] = dev_set.reshape(-1).cpu().numpy()
+    del dev_set
+    torch.cuda.empty_cache()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(99)
+    logits = torch.randn((n, T, E), generator=g, device="cuda").contiguous()
+    ids = torch.empty((n, T, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n, T, k), dtype=torch.float32, device="cuda")
+    for i in range(n):
+        hip.router_topk(logits[i], ids[i], wts[i], k)
+    routed = ids.cpu().numpy()
+    slots = [torch.empty((k, stride), dtype=torch.uint8, device="cuda") for _ in range(2)]
+    dst = [[b.data_ptr() + j * stride for j in range(k)] for b in slots]
+    tables = []
+    for i in range(n):
+        t = np.full(E, dst[i % 2][0], dtype=np.int64)
+        for j, e in enumerate(routed[i, 0]):
+            t[e] = dst[i % 2][j]
+        tables.append(torch.from_numpy(t).cuda())
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(hip.moe_decode_fp8_workspace_size(T, E, k, geo), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    q = hip.CopyQueue()
+    copied = [hip.Event() for _ in range(n)]
+    computed = [hip.Event() for _ in range(n)]
+
+    def stage(i):
+        if i >= 2:
+            computed[i - 2].wait_on(q)  # the slots' previous reader is done
+        q.copy_records(dst[i % 2], [host.ptr + int(e) * stride for e in routed[i, 0]], stride)
+        copied[i].record(q)
+
+    def run(lo, hi):
+        stage(lo)
+        for i in range(lo, hi):
+            if i + 1 < hi:
+                stage(i + 1)
+            copied[i].wait_on(stream)
+            hip.moe_decode_fp8(logits[i], x, tables[i], k, geo, ids[i], wts[i], out, ws, stream)
+            computed[i].record(stream)
+
+    run(0, warmup)
+    torch.cuda.synchronize()
+    q.sync()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    run(warmup, n)
+    end.record(stream)
+    torch.cuda.synchronize()
+    q.sync()
+    ms = start.elapsed_time(end) / steps
+    h2d = k * stride / (ms * 1e-3) / 1e9
+    for ev in copied + computed:
+        ev.close()
+    q.close()
+    host.close()
+    return {
+        "metric": "MoE FP8 decode step with host-tier experts: us/token + host-to-device GB/s, 1 GPU",
+        "value": ms * 1e3 / T, "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3 weights, bf16 activations, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "MoE FFN decode step, batch 1: 128 experts top-8, hidden 4096, inter 1536, all "
+                               "records in pinned host memory; the 8 routed records copy to device slots each step "
+                               "on a copy queue, double-buffered beside compute",
+                   "batch": T, "experts": E, "top_k": k, "hidden": H, "inter": I},
+        "roofline": {"bound": "pcie", "achieved": h2d, "peak": PEAK_PCIE_GBS, "unit": "GB/s",
+                     "frac": h2d / PEAK_PCIE_GBS, "traffic": None,
+                     "kernel": "host-to-device copies of the routed records (oom_copy_records_to_device)",
+                     "algorithmic_bytes_per_step": float(k * stride)},
+    }
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "attn",
+    ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "offload", "attn",
                                                             "prefill", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -686,6 +782,8 @@ def main():
         res = bench_prefill(args)
     elif args.config == "decode1":
         res = bench_decode(args, 1, None, args.config)
+    elif args.config == "offload":
+        res = bench_offload(args)
     elif args.config == "nvfp4":
         res = bench_nvfp4(args)
     elif args.config in ("layer1", "layer16"):

@@ -33,6 +33,7 @@ class Fp8Record(ctypes.Structure):
 
 # entry point -> (restype, argtypes); every symbol include/oom_hip.h declares
 P, I32, I64, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+U64 = ctypes.c_uint64
 SIGNATURES = {
     "oom_last_error": (ctypes.c_char_p, []),
     "oom_workspace_init": (I32, [P, SZ, P]),
@@ -61,6 +62,21 @@ SIGNATURES = {
     "oom_moe_prefill_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
     "oom_attn_decode_workspace_size": (SZ, [I32, I32, I32, I32]),
     "oom_attn_decode_paged": (I32, [P, I32, P, P, P, I32, I32, I32, I32, I32, I32, F, P, I32, P, SZ, P]),
+    "oom_copy_queue_create": (I32, [P]),
+    "oom_copy_queue_destroy": (I32, [P]),
+    "oom_host_alloc": (I32, [P, SZ]),
+    "oom_host_free": (I32, [P]),
+    "oom_copy_to_device": (I32, [P, U64, P, SZ]),
+    "oom_copy_on_device": (I32, [P, U64, U64, SZ]),
+    "oom_copy_records_to_device": (I32, [P, P, P, SZ, I32]),
+    "oom_download_async": (I32, [P, P, P, SZ]),
+    "oom_event_create": (I32, [P]),
+    "oom_event_destroy": (I32, [P]),
+    "oom_event_record": (I32, [P, P]),
+    "oom_stream_wait_event": (I32, [P, P]),
+    "oom_event_done": (I32, [P]),
+    "oom_event_wait": (I32, [P]),
+    "oom_stream_sync": (I32, [P]),
 }
 
 
@@ -314,3 +330,98 @@ def moe_prefill_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, o
     check(lib().oom_moe_prefill_fp8(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k, ctypes.byref(geo),
                                     _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
                                     ws.numel() * ws.element_size(), _stream(stream)))
+
+
+# ---- copies beside compute: the Transfer trait (crates/oominf-core/src/backend.rs:945-1018) ----
+
+def _handle(x) -> ctypes.c_void_p:
+    """A copy queue, a torch stream or None (torch's current stream) as a stream handle."""
+    if isinstance(x, CopyQueue):
+        return x.handle
+    return _stream(x)
+
+
+class CopyQueue:
+    """Transfer::copy_queue: a HIP stream of its own (default priority) for copies."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(lib().oom_copy_queue_create(ctypes.byref(h)))
+        self.handle = h
+
+    def copy_to_device(self, dst: int, src: int, nbytes: int) -> None:
+        check(lib().oom_copy_to_device(self.handle, dst, ctypes.c_void_p(src), nbytes))
+
+    def copy_on_device(self, dst: int, src: int, nbytes: int) -> None:
+        check(lib().oom_copy_on_device(self.handle, dst, src, nbytes))
+
+    def copy_records(self, dst: list[int], src: list[int], nbytes: int) -> None:
+        """Records src[i] (pinned host) -> dst[i] (device), nbytes each, in order."""
+        n = len(dst)
+        d = (ctypes.c_uint64 * n)(*dst)
+        s = (ctypes.c_void_p * n)(*src)
+        check(lib().oom_copy_records_to_device(self.handle, d, s, nbytes, n))
+
+    def sync(self) -> None:
+        check(lib().oom_stream_sync(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().oom_copy_queue_destroy(self.handle))
+            self.handle = None
+
+
+class Event:
+    """A Transfer event: record on the compute stream or a copy queue, wait on either."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(lib().oom_event_create(ctypes.byref(h)))
+        self.handle = h
+
+    def record(self, stream=None) -> None:
+        check(lib().oom_event_record(self.handle, _handle(stream)))
+
+    def wait_on(self, stream=None) -> None:
+        """Work queued later on `stream` waits for this event (compute_wait / copies_wait)."""
+        check(lib().oom_stream_wait_event(_handle(stream), self.handle))
+
+    def done(self) -> bool:
+        rc = lib().oom_event_done(self.handle)
+        if rc < 0:
+            check(rc)
+        return rc == 1
+
+    def wait(self) -> None:
+        check(lib().oom_event_wait(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().oom_event_destroy(self.handle))
+            self.handle = None
+
+
+class PinnedHost:
+    """Pinned host memory from oom_host_alloc; `array()` is a numpy view of it."""
+
+    def __init__(self, nbytes: int):
+        h = ctypes.c_void_p()
+        check(lib().oom_host_alloc(ctypes.byref(h), nbytes))
+        self.ptr = int(h.value)
+        self.nbytes = nbytes
+
+    def array(self, dtype="uint8"):
+        import numpy as np
+
+        buf = (ctypes.c_uint8 * self.nbytes).from_address(self.ptr)
+        return np.frombuffer(buf, dtype=np.uint8).view(dtype)
+
+    def close(self) -> None:
+        if self.ptr:
+            check(lib().oom_host_free(ctypes.c_void_p(self.ptr)))
+            self.ptr = 0
+
+
+def download_async(dst_host: int, src, nbytes: int, stream=None) -> None:
+    """Transfer::download_async: after the work queued on `stream`, device src -> pinned host."""
+    check(lib().oom_download_async(_handle(stream), ctypes.c_void_p(dst_host), _ptr(src), nbytes))

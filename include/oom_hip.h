@@ -260,6 +260,44 @@ int oom_attn_decode_paged(const void* q, int q_dtype, const uint16_t* k_pages, c
                           const int32_t* page_table, int n_pages, int page_size, int kv_len, int heads, int kv_heads,
                           int d, float scale, void* out, int out_dtype, void* ws, size_t ws_bytes, void* stream);
 
+
+/* ---- copies beside compute (expert offload) ----
+ * The Transfer trait (crates/oominf-core/src/backend.rs:945-1018; CUDA form
+ * crates/oominf-cuda/src/memory.rs:300-380): a copy queue runs beside the compute stream,
+ * events order the two, so TieredExperts can stage host-tier expert records into device
+ * slots while the previous layer computes. Queues and events are opaque handles. */
+
+/* Transfer::copy_queue: a stream of its own at default priority, non-blocking. */
+int oom_copy_queue_create(void** queue);
+int oom_copy_queue_destroy(void* queue);
+/* Pinned host memory, the source of asynchronous copies. Replaces Transfer::pin_host /
+ * unpin_host (backend.rs:956-963): registering existing memory is not offered, so a host
+ * expert tier is allocated here instead. */
+int oom_host_alloc(void** ptr, size_t bytes);
+int oom_host_free(void* ptr);
+/* Transfer::copy_to_device (backend.rs:964-976): len bytes from pinned host src to device
+ * address dst, queued on `queue`. */
+int oom_copy_to_device(void* queue, uint64_t dst, const void* src, size_t len);
+/* Transfer::copy_on_device (backend.rs:998-1006). */
+int oom_copy_on_device(void* queue, uint64_t dst, uint64_t src, size_t len);
+/* n records of `bytes` each, src[i] (pinned host) -> dst[i] (device), in order on `queue`:
+ * the per-layer staging loop of TieredExperts over copy_to_device (crates/oominf-core/src/experts.rs). */
+int oom_copy_records_to_device(void* queue, const uint64_t* dst, const void* const* src, size_t bytes, int n);
+/* Transfer::download_async (backend.rs:977-985): after the work queued on `stream` so far,
+ * len bytes from device src to pinned host dst. */
+int oom_download_async(void* stream, void* dst, const void* src, size_t len);
+/* Transfer events (backend.rs:1007-1017): record_compute / record_copies are
+ * oom_event_record on the compute stream or the queue; compute_wait / copies_wait are
+ * oom_stream_wait_event; event_done returns 1 (done), 0 (pending) or an error;
+ * event_wait and copies_sync block the host. */
+int oom_event_create(void** event);
+int oom_event_destroy(void* event);
+int oom_event_record(void* event, void* stream);
+int oom_stream_wait_event(void* stream, void* event);
+int oom_event_done(void* event);
+int oom_event_wait(void* event);
+int oom_stream_sync(void* stream);
+
 #ifdef __cplusplus
 }
 #endif
