@@ -9,7 +9,7 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 256 MB Infinity Cache.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|prefill|copy]
+                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|prefill|gemv|copy]
 
 Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
 kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
@@ -107,11 +107,16 @@ def zipf_bias(E, s, seed):
 
 
 def usable_cores() -> int:
+    """Every core this process may run on: the affinity mask, within the job's CPU share
+    when the environment states one (OMP_NUM_THREADS, as the batch system sets it)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(16, n))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, n)
 
 
 def cpu_model() -> str:
@@ -231,6 +236,102 @@ def bench_decode(args, T, zipf, config):
         res["cpu_baseline"] = {"value": us, "unit": "us/token", "cores": cores, "kind": "port",
                                "sample": f"{nsteps} steps of the same batch-{T} decode MoE layer (fresh logits), "
                                          f"oracle restatement of crates/oominf-cpu HostExperts on {cpu_model()}"}
+    return res
+
+
+def cpu_baseline_gemv(x, q, scale, budget_s):
+    """The oracle's restatement of the reference FP8 GEMV (crates/oominf-cuda/kernels/ops.cu:339-440
+    arithmetic) on this host's cores, the rows split evenly over one thread each, for
+    about `budget_s` seconds. Returns (us_per_call, threads, calls)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    import oracle
+
+    N = q.shape[0]
+    threads = usable_cores()
+    bounds = np.linspace(0, N, threads + 1).astype(int)
+    parts = [(np.ascontiguousarray(q[a:b]), np.ascontiguousarray(scale[a:b])) for a, b in zip(bounds[:-1], bounds[1:])]
+
+    def one(i):
+        qq, ss = parts[i]
+        return oracle.gemv_fp8(x, qq, ss, oracle.SCALE_ROW)
+
+    t0 = time.perf_counter()
+    calls = 0
+    with ThreadPoolExecutor(threads) as pool:
+        while True:
+            list(pool.map(one, range(threads)))
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s and calls >= 3:
+                break
+    return el / calls * 1e6, threads, calls
+
+
+def bench_gemv(args):
+    """One FP8 weight-only GEMV, batch 1: y = W x with W 4096 x 4096 e4m3 quantised from
+    N(0, 0.02) with per-output-row absmax fp32 scales, x 1 x 4096 bf16 N(0, 1), fp32
+    accumulate, bf16 y (oom_gemv_fp8, OOM_SCALE_ROW). 48 weight copies (805 MB) rotate
+    between calls so W streams from HBM, not from the 256 MB MALL."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    N = K = 4096
+    copies = 48
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    qs = torch.empty((copies, N, K), dtype=torch.uint8, device="cuda")
+    ss = torch.empty((copies, N), dtype=torch.float32, device="cuda")
+    for c in range(copies):
+        w = torch.randn((N, K), generator=g, device="cuda") * 0.02
+        amax = w.abs().amax(dim=1)
+        sc = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+        qs[c] = (w / sc[:, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+        ss[c] = sc
+    x = torch.randn((1, K), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(hip.gemv_fp8_workspace_size(1, N, K), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        c = i % copies
+        hip.gemv_fp8(x, qs[c], ss[c], hip.SCALE_ROW, y, ws, stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(args.steps):
+        step(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    bytes_call = N * K + N * 4 + K * 2 + N * 2
+    gbs = bytes_call / (ms * 1e-3) / 1e9
+    res = {
+        "metric": "FP8 weight-only GEMV us/call + achieved HBM GB/s (% of MI355X peak), 1 GPU",
+        "value": ms * 1e3, "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3 weights, bf16 x and y, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "FP8 GEMV, batch 1: W 4096x4096 e4m3 from N(0,0.02) with per-row absmax fp32 scales, "
+                               "x 1x4096 bf16 N(0,1), bf16 y; 48 weight copies rotate past the MALL",
+                   "batch": 1, "rows": N, "cols": K, "scale_layout": "row"},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": measured_traffic("gemv"), "kernel": "gemv kernel (oom_gemv_fp8, per-row scales)",
+                     "algorithmic_bytes_per_step": float(bytes_call), "copy_gbs": copy_bandwidth(torch)},
+    }
+    if not args.no_cpu:
+        xn = x.float().cpu().numpy()
+        us, threads, n = cpu_baseline_gemv(xn, qs[0].cpu().numpy(), ss[0].cpu().numpy(), args.cpu_seconds)
+        res["cpu_baseline"] = {"value": us, "unit": "us/call", "cores": threads, "kind": "port",
+                               "sample": f"{n} calls of the same 4096x4096 GEMV, oracle restatement of the "
+                                         f"reference's FP8 GEMV arithmetic, rows split over {threads} threads, on "
+                                         f"{cpu_model()}"}
     return res
 
 
@@ -760,7 +861,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "offload", "attn",
-                                                            "prefill", "copy"])
+                                                            "prefill", "gemv", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -778,6 +879,8 @@ def main():
                "copies": args.steps + 1}
     elif args.config == "attn":
         res = bench_attn(args)
+    elif args.config == "gemv":
+        res = bench_gemv(args)
     elif args.config == "prefill":
         res = bench_prefill(args)
     elif args.config == "decode1":

@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboom_hip.so")
 
 OK = 0
+ERR_ARG, ERR_WORKSPACE, ERR_LAUNCH, ERR_KERNEL = -1, -2, -3, -4
 F32, BF16 = 0, 1
 SCALE_ROW, SCALE_1X128, SCALE_128X128 = 0, 1, 2
 
@@ -37,6 +38,8 @@ U64 = ctypes.c_uint64
 SIGNATURES = {
     "oom_last_error": (ctypes.c_char_p, []),
     "oom_workspace_init": (I32, [P, SZ, P]),
+    "oom_status": (I32, [P]),
+    "oom_set_wait_limit": (I32, [ctypes.c_uint32]),
     "oom_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
     "oom_gemv_fp8_workspace_size": (SZ, [I32, I64, I64]),
     "oom_gemv_fp8": (I32, [P, I32, P, P, I32, P, I32, I32, I64, I64, P, SZ, P]),
@@ -98,6 +101,17 @@ def lib() -> ctypes.CDLL:
 def check(rc: int) -> None:
     if rc != OK:
         raise OomError(f"status {rc}: {lib().oom_last_error().decode()}")
+
+
+def status(stream=None) -> int:
+    """oom_status: waits for `stream`, returns OK or ERR_KERNEL (a bounded wait inside an
+    earlier kernel gave up; its outputs are invalid) and clears the device's status word."""
+    return lib().oom_status(_stream(stream))
+
+
+def set_wait_limit(spins: int) -> None:
+    """oom_set_wait_limit: polls of each bounded wait of later launches (0: the default)."""
+    check(lib().oom_set_wait_limit(spins))
 
 
 def _ptr(t) -> ctypes.c_void_p | None:

@@ -1,4 +1,7 @@
-// Error state of the C ABI and the workspace fill.
+// Error state of the C ABI, the device status word of the kernels' bounded waits, and
+// the workspace fill.
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -25,7 +28,62 @@ __global__ void __launch_bounds__(256) fill_zero(uint4* p, size_t words, uint8_t
     if (blockIdx.x == 0 && (int)threadIdx.x < tail_bytes) tail[threadIdx.x] = 0;
 }
 
+// The device's status word: a kernel whose bounded wait gives up stores 1 here (its
+// outputs are invalid); oom_status reads and clears it. One 256-byte line per device
+// (each device holds its own copy of a __device__ variable, at its own address).
+static __device__ __align__(256) uint32_t status_line[64];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_dev_mu;
+static uint32_t* g_status_ptr[MAX_DEVICES] = {};
+static std::atomic<uint32_t> g_wait_limit{DEFAULT_WAIT_LIMIT};
+
+// The address of the current device's status word, looked up once per device with that
+// device current (nullptr if the runtime refuses).
+uint32_t* status_word() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    uint32_t* p = __atomic_load_n(&g_status_ptr[dev], __ATOMIC_ACQUIRE);
+    if (p) return p;
+    std::lock_guard<std::mutex> lock(g_dev_mu);
+    if (!g_status_ptr[dev]) {
+        void* q = nullptr;
+        if (hipGetSymbolAddress(&q, HIP_SYMBOL(status_line)) != hipSuccess || !q) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        __atomic_store_n(&g_status_ptr[dev], reinterpret_cast<uint32_t*>(q), __ATOMIC_RELEASE);
+    }
+    return g_status_ptr[dev];
+}
+
+uint32_t wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+
 }  // namespace oom
+
+extern "C" int oom_set_wait_limit(uint32_t spins) {
+    oom::g_wait_limit.store(spins ? spins : oom::DEFAULT_WAIT_LIMIT, std::memory_order_relaxed);
+    return OOM_OK;
+}
+
+extern "C" int oom_status(void* stream) {
+    using namespace oom;
+    uint32_t* p = status_word();
+    if (!p) return fail(OOM_ERR_LAUNCH, "oom_status: the device status word has no address");
+    hipStream_t st = as_stream(stream);
+    uint32_t v = 0;
+    if (hipMemcpyAsync(&v, p, sizeof(v), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail(OOM_ERR_LAUNCH, std::string("oom_status: ") + hipGetErrorString(hipGetLastError()));
+    if (v == 0) return OOM_OK;
+    // clear the word with the fill kernel (no memset node), ordered after the read
+    hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, reinterpret_cast<uint4*>(p), (size_t)1,
+                       reinterpret_cast<uint8_t*>(p), 0);
+    if (int rc = launched("oom_status")) return rc;
+    return fail(OOM_ERR_KERNEL,
+                "a bounded wait inside a kernel gave up (grid not resident at once, or a wait limit set by "
+                "oom_set_wait_limit): the outputs of that call are invalid");
+}
 
 extern "C" const char* oom_last_error(void) { return oom::g_last_error.c_str(); }
 

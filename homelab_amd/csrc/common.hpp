@@ -17,6 +17,13 @@ int fail(int code, const std::string& msg);
 // Maps a HIP launch status to OOM_OK / OOM_ERR_LAUNCH with the runtime's message.
 int launched(const char* what);
 
+// Polls of a bounded wait before it gives up (oom_set_wait_limit changes it).
+constexpr uint32_t DEFAULT_WAIT_LIMIT = 1u << 22;
+// The current device's status word (set by a kernel whose bounded wait gave up), or
+// nullptr if the runtime gives it no address; the spin limit of bounded waits.
+uint32_t* status_word();
+uint32_t wait_limit();
+
 #define OOM_REQUIRE(cond, msg)                                 \
     do {                                                       \
         if (!(cond)) return ::oom::fail(OOM_ERR_ARG, (msg));   \

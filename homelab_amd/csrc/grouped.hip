@@ -1,8 +1,8 @@
 // Prefill MoE on gfx950: per-token e4m3 activation quantiser, FP8 x FP8 grouped GEMM on
 // the matrix cores (v_mfma_scale_f32_16x16x128_f8f6f4, unit block scales), the gate/up
-// pass with SwiGLU and the per-128-column e4m3 quantisation of h in its epilogue, and
-// the whole prefill step (router, plan, quantise, gate/up, down, combine) without a
-// host round trip.
+// pass with SwiGLU in its epilogue, the down pass over h kept at fp32 precision (two
+// bf16 terms on v_mfma_f32_16x16x32_bf16), and the whole prefill step (router, plan,
+// quantise, gate/up, down, combine) without a host round trip.
 //
 // Grouped GEMM: y[a, r] = xs(a) * sum_kb ws(r, kb) * sum_{c in kb} e4m3(xq[row(a), c]) *
 // e4m3(W[r, c]) for the assignments a of each expert (the semantics of
@@ -16,8 +16,14 @@
 //    assignment) and the weight rows in LDS (rows padded to 144 bytes), and the next
 //    step's global loads are in flight while the current step runs on the matrix cores.
 //  * Gate/up: both weight tiles share the activation tile; the epilogue forms
-//    h = silu(g) * u, finds each row's absmax over the tile's 128 columns (the
-//    quantisation group), and writes e4m3 h and its scale.
+//    h = silu(g) * u and writes it as two bf16 planes, hi = bf16(h) and lo = bf16(h - hi)
+//    (16 significant bits, relative error <= 2^-17): h is not quantised again, as the
+//    reference keeps it in fp32 for its exact tiled path (ExpertPrecision::Exact,
+//    crates/oominf-core/src/backend.rs:144-149; crates/oominf-cuda/kernels/moe.cu:166-335
+//    splits fp32 activations into exact bf16 terms the same way).
+//  * Down: A = the h planes, B = e4m3 weight rows converted exactly to bf16 in registers;
+//    both terms run on the bf16 matrix cores, fp32 accumulate, the weight's 128 x 128 block
+//    scale applied to each 128-column block sum.
 #include <algorithm>
 
 #include "router.hpp"
@@ -45,9 +51,9 @@ struct GArgs {
     int64_t N, K;
     int64_t w_off, s_off;   // first (or only) weight part and its scales
     int64_t w2_off, s2_off; // up part (gate/up pass)
-    float* y;               // [A, N] fp32 (plain pass)
-    uint8_t* hq;            // [A, N] e4m3 h (gate/up pass)
-    float* hs;              // [A, N / 128] h scales (gate/up pass)
+    float* y;               // [A, N] fp32 (plain and down passes)
+    uint16_t* hh;           // [A, N] bf16 hi term of h (gate/up pass) / of the activations (down pass)
+    uint16_t* hl;           // [A, N] bf16 lo term
 };
 
 // e4m3fn code of v, round to nearest even, saturating at +-448 (the quantiser's rule,
@@ -280,7 +286,6 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     // wave each)
     constexpr int STOT = SBYTES + 2 * GTHREADS * 4;
     __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT], sb2[NST == 3 ? STOT : 16];
-    __shared__ float rowmax[GBM][2];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;  // rows 32 wm .. + 32, columns 64 wn .. + 64
@@ -398,47 +403,205 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
                 }
             }
     } else {
-        // h = silu(xs g) * (xs u); row absmax over the tile's 128 columns
-        float h[2][4][4];
+        // h = silu(xs g) * (xs u) as two bf16 terms: hi = bf16(h), lo = bf16(h - hi)
 #pragma unroll
         for (int ms = 0; ms < 2; ms++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int a = min(arow_out[ms][e], a1 - 1);
-                const float xsr = g.xs[g.rows ? g.rows[a] : a];
-                float mx = 0.0f;
-#pragma unroll
-                for (int ns = 0; ns < 4; ns++) {
-                    const float gv = acc[0][ms][ns][e] * xsr, uv = acc[1][ms][ns][e] * xsr;
-                    h[ms][ns][e] = siluf(gv) * uv;
-                    mx = fmaxf(mx, fabsf(h[ms][ns][e]));
-                }
-                // over the 16 lanes holding this row's columns (lane % 16)
-                mx = fmaxf(mx, dpp_f32<DPP_XOR1>(mx));
-                mx = fmaxf(mx, dpp_f32<DPP_XOR2>(mx));
-                mx = fmaxf(mx, lane_xor<4>(mx, lane));
-                mx = fmaxf(mx, lane_xor<8>(mx, lane));
-                if ((lane & 15) == 0) rowmax[32 * wm + 16 * ms + 4 * (lane >> 4) + e][wn] = mx;
-            }
-        __syncthreads();
-        const int ngrp = (int)(g.N / 128);
-#pragma unroll
-        for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int rr = 32 * wm + 16 * ms + 4 * (lane >> 4) + e;
                 const int a = arow_out[ms][e];
-                const float amax = fmaxf(rowmax[rr][0], rowmax[rr][1]);
-                const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
                 if (a >= a1) continue;
-                if (wn == 0 && (lane & 15) == 0) g.hs[(int64_t)a * ngrp + n0 / 128] = s;
+                const float xsr = g.xs[g.rows ? g.rows[a] : a];
 #pragma unroll
                 for (int ns = 0; ns < 4; ns++) {
+                    const float h = siluf(acc[0][ms][ns][e] * xsr) * (acc[1][ms][ns][e] * xsr);
+                    const uint16_t hi = f32_to_bf16(h);
                     const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
-                    g.hq[(int64_t)a * g.N + n] = (uint8_t)(e4m3_pair(h[ms][ns][e] / s, 0.0f) & 0xff);
+                    g.hh[(int64_t)a * g.N + n] = hi;
+                    g.hl[(int64_t)a * g.N + n] = f32_to_bf16(h - bf16_to_f32(hi));
                 }
             }
     }
+}
+
+// ---- down pass over h as two bf16 terms ----------------------------------------------
+//
+// y[a, r] = sum_kb ws(r, kb) * sum_{c in kb} (hi[a, c] + lo[a, c]) * e4m3(W[r, c]) for the
+// assignments a of each expert (W = the down weights [N = hidden, K = inter]); e4m3 -> bf16
+// is exact and bf16 products are exact in fp32, so each 128-column block sum is an fp32 sum
+// of exact products, scaled by the weight's block scale as it joins the accumulator.
+//
+// K steps of 64 through three LDS stages (direct-to-LDS loads, as the FP8 passes): a stage
+// holds the hi and lo tiles (128 assignments x 64 bf16 = 128 bytes a row, 8 chunks, the
+// FP8 tiles' chunk swizzle) and the weight tile (128 rows x 64 bytes, 4 chunks, chunk c of
+// row r at 4 r + (c ^ ((r >> 2) & 3)), so the 16 rows of an operand read, and any 8 of
+// them, land in distinct 16-byte bank groups). Lane l of a wave takes K values
+// 16 (l / 16) .. + 16 of the step for its row (A: assignment l % 16 of a 16-row subtile,
+// B: weight row l % 16), as two 8-value halves, one per MFMA: the same K order on both
+// sides, so the contraction is the plain sum.
+constexpr int GBK2 = 64;                       // K step of the down pass
+constexpr int D_HT = GBM * GBK2 * 2;           // bytes of one h term tile
+constexpr int D_WT = GBN * GBK2;               // bytes of the weight tile
+constexpr int D_SBYTES = 2 * D_HT + D_WT;      // one stage's operands
+constexpr int D_STOT = D_SBYTES + GTHREADS * 4;  // + the weight scale (64 words a wave)
+constexpr int D_LPS = 2 * 2 + 1 + 1;           // loads a wave issues per stage
+
+typedef __bf16 gbf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ int wchunk_pos(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
+
+struct DSrc {
+    __amdgpu_buffer_rsrc_t hr, wr, sr;
+    int ho[2], wo;  // step-0 byte offsets (the two terms share ho: hl is at hh + plane bytes)
+    int hl_off;     // bytes from hh to hl
+    int so;         // step-0 byte offset of this lane's weight scale (G_OOB: none)
+};
+
+__device__ __forceinline__ void d_issue(const DSrc& s, int kb, int nkb, uint8_t* sb, float* scw, int wave) {
+    const bool ok = kb < nkb;
+    const int k0 = kb * GBK2 * 2;  // bytes into an h row
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            dma16(s.hr, sb + t * D_HT + (2 * wave + j) * 1024, ok ? s.ho[j] + t * s.hl_off + k0 : G_OOB);
+    dma16(s.wr, sb + 2 * D_HT + wave * 1024, ok ? s.wo + kb * GBK2 : G_OOB);
+    dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
+}
+
+// One K step: blk += the step's products (both terms); every second step (and the last)
+// the 128-column block sum joins acc, scaled by the weight's block scale.
+__device__ __forceinline__ void d_step(const uint8_t* sb, const float* scw, int wm, int wn, int wave, int lane,
+                                       bool fold, gf32x4 (&blk)[2][4], float (&acc)[2][4][4]) {
+    const int g = lane >> 4;
+    gbf16x8 a[2][2][2];  // [ms][term][half]
+#pragma unroll
+    for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int row = 32 * wm + 16 * ms + (lane & 15);
+            const uint8_t* base = sb + t * D_HT;
+            const uint4 lo = *reinterpret_cast<const uint4*>(base + 16 * chunk_pos(row, 2 * g));
+            const uint4 hi = *reinterpret_cast<const uint4*>(base + 16 * chunk_pos(row, 2 * g + 1));
+            a[ms][t][0] = __builtin_bit_cast(gbf16x8, lo);
+            a[ms][t][1] = __builtin_bit_cast(gbf16x8, hi);
+        }
+#pragma unroll
+    for (int ns = 0; ns < 4; ns++) {
+        const int row = 64 * wn + 16 * ns + (lane & 15);
+        const uint4 w = *reinterpret_cast<const uint4*>(sb + 2 * D_HT + 16 * wchunk_pos(row, g));
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        gbf16x8 b[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(ww[2 * hf + q], 1.0f, false);
+                const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(ww[2 * hf + q], 1.0f, true);
+                b[hf][4 * q] = p0[0];
+                b[hf][4 * q + 1] = p0[1];
+                b[hf][4 * q + 2] = p1[0];
+                b[hf][4 * q + 3] = p1[1];
+            }
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+                    blk[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ms][t][hf], b[hf], blk[ms][ns], 0, 0, 0);
+    }
+    if (fold) {
+        const float ws = scw[64 * wave];
+#pragma unroll
+        for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+            for (int ns = 0; ns < 4; ns++) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[ms][ns][e] = fmaf(blk[ms][ns][e], ws, acc[ms][ns][e]);
+                blk[ms][ns] = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+    }
+}
+
+// Down pass: tiles from the device tile table in XCD runs, as grouped_gemm_kernel.
+__global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
+    __shared__ __align__(16) uint8_t sb0[D_STOT], sb1[D_STOT], sb2[D_STOT];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int NT = (int)gridDim.x, MT = *g.ntiles, W = NT * MT;
+    const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), C = (W + 7) / 8;
+    if ((L >> 3) >= C) return;
+    const int w = (L & 7) * C + (L >> 3);
+    if (w >= W) return;
+    const int nt = w / MT, mt = w - nt * MT;
+    const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBN;
+    const int a0 = g.off[i], a1 = g.off[i + 1];
+    if (a0 + m0 >= a1) return;
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
+    const int nkb = (int)(g.K / GBK2);
+    DSrc src;
+    // the two h planes as one resource (hl follows hh by hl_off bytes)
+    src.hl_off = (int)((const uint8_t*)g.hl - (const uint8_t*)g.hh);
+    src.hr = __builtin_amdgcn_make_buffer_rsrc(g.hh, (short)0, 0x7fff0000, G_BUF_FLAGS);
+    src.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, (int)(g.w_off + g.N * g.K),
+                                               G_BUF_FLAGS);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int r, c;
+        pos_chunk((2 * wave + j) * 64 + lane, r, c);
+        int a = a0 + m0 + r;
+        if (a >= a1) a = a0;
+        src.ho[j] = (int)(a * g.K * 2) + 16 * c;
+    }
+    {
+        const int p = wave * 64 + lane, r = p >> 2, c = (p & 3) ^ ((r >> 2) & 3);
+        src.wo = (int)(g.w_off + (int64_t)(n0 + r) * g.K) + 16 * c;
+    }
+    src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
+    src.so = lane == 0 ? (int)(g.s_off + (int64_t)(n0 / 128) * (g.K / 128) * 4) : G_OOB;
+    float acc[2][4][4];
+    gf32x4 blk[2][4];
+#pragma unroll
+    for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+        for (int ns = 0; ns < 4; ns++) {
+            blk[ms][ns] = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[ms][ns][e] = 0.0f;
+        }
+#define D_SW(B) reinterpret_cast<float*>((B) + D_SBYTES)
+#define D_STEP(SB, NSB)                                                                                  \
+    {                                                                                                    \
+        wait_vm<D_LPS>();                                                                                \
+        g_barrier();                                                                                     \
+        d_issue(src, kb + 2, nkb, NSB, D_SW(NSB), wave);                                                 \
+        d_step(SB, D_SW(SB), wm, wn, wave, lane, (kb & 1) || kb + 1 == nkb, blk, acc);                  \
+        if (++kb == nkb) break;                                                                          \
+    }
+    int kb = 0;
+    d_issue(src, 0, nkb, sb0, D_SW(sb0), wave);
+    d_issue(src, 1, nkb, sb1, D_SW(sb1), wave);
+    for (;;) {
+        D_STEP(sb0, sb2)
+        D_STEP(sb1, sb0)
+        D_STEP(sb2, sb1)
+    }
+#undef D_SW
+#undef D_STEP
+    wait_vm<0>();  // the zero-filled stages past the end have landed before the block ends
+#pragma unroll
+    for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int a = a0 + m0 + 32 * wm + 16 * ms + 4 * (lane >> 4) + e;
+            if (a >= a1) continue;
+#pragma unroll
+            for (int ns = 0; ns < 4; ns++) {
+                const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
+                g.y[(int64_t)a * g.N + n] = acc[ms][ns][e];
+            }
+        }
 }
 
 // ---- host side -----------------------------------------------------------------------
@@ -447,6 +610,11 @@ int launch_grouped(const GArgs& a, int mode, dim3 grid, hipStream_t st) {
     if (mode == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
     else hipLaunchKernelGGL(grouped_gemm_kernel<0>, grid, dim3(GTHREADS), 0, st, a);
     return launched("grouped_gemm_fp8");
+}
+
+int launch_grouped_down(const GArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL(grouped_down_bf16_kernel, grid, dim3(GTHREADS), 0, st, a);
+    return launched("grouped_down_bf16");
 }
 
 int launch_quant_rows(const void* x, int xdt, int64_t rows, int64_t cols, uint8_t* q, float* s, hipStream_t st) {
@@ -472,9 +640,10 @@ int launch_combine(const float* y, const int32_t* slot, const float* w, void* ou
                    hipStream_t st);
 int check_geo(const OomFp8Record* g, const char* who);
 
-// Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | hq | hs | y.
+// Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | hh | hl | y (hh and hl:
+// the bf16 hi and lo terms of h [A, inter]).
 struct PrefillWs {
-    size_t plan, recs, xq, xs, tiles, hq, hs, y, total;
+    size_t plan, recs, xq, xs, tiles, hh, hl, y, total;
     int max_tiles;
 };
 
@@ -489,9 +658,9 @@ static PrefillWs prefill_ws(int T, int E, int k, const OomFp8Record& g) {
     w.xq = w.recs + p_al256((size_t)std::min<size_t>(E, A) * sizeof(uint64_t));
     w.xs = w.xq + p_al256((size_t)T * H);
     w.tiles = w.xs + p_al256((size_t)T * sizeof(float));
-    w.hq = w.tiles + p_al256((2 * (size_t)w.max_tiles + 1) * sizeof(int32_t));
-    w.hs = w.hq + p_al256(A * I);
-    w.y = w.hs + p_al256(A * (I / 128) * sizeof(float));
+    w.hh = w.tiles + p_al256((2 * (size_t)w.max_tiles + 1) * sizeof(int32_t));
+    w.hl = w.hh + p_al256(A * I * sizeof(uint16_t));
+    w.y = w.hl + p_al256(A * I * sizeof(uint16_t));
     w.total = w.y + p_al256(A * H * sizeof(float));
     return w;
 }
@@ -553,6 +722,9 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     OOM_REQUIRE(std::max({geo->gate_weight, geo->up_weight, geo->down_weight}) + geo->hidden * geo->inter < 0x7fff0000ll,
                 "oom_moe_prefill_fp8: weight parts beyond 2 GiB of their record");
     OOM_REQUIRE(T >= 1 && (int64_t)T * k <= (1 << 24), "oom_moe_prefill_fp8: T must be >= 1 and T * k <= 2^24");
+    // buffer-resource offsets are 32-bit: the e4m3 rows and both h planes stay below 2 GiB
+    OOM_REQUIRE((int64_t)T * geo->hidden < 0x7fff0000ll && (int64_t)T * k * geo->inter * 4 < 0x7fff0000ll,
+                "oom_moe_prefill_fp8: activations or h beyond 2 GiB (split the prefill into chunks of tokens)");
     OOM_REQUIRE(k >= 1 && k <= 32 && E >= k && E <= 8192, "oom_moe_prefill_fp8: router top-k > 32 or experts > 8192");
     OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_moe_prefill_fp8: x_dtype");
     OOM_REQUIRE(out_dtype == OOM_F32 || out_dtype == OOM_BF16, "oom_moe_prefill_fp8: out_dtype");
@@ -568,8 +740,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     float* xs = reinterpret_cast<float*>(base + w.xs);
     int32_t* tiles = reinterpret_cast<int32_t*>(base + w.tiles);
     int32_t* ntiles = tiles + 2 * w.max_tiles;
-    uint8_t* hq = base + w.hq;
-    float* hs = reinterpret_cast<float*>(base + w.hs);
+    uint16_t* hh = reinterpret_cast<uint16_t*>(base + w.hh);
+    uint16_t* hl = reinterpret_cast<uint16_t*>(base + w.hl);
     float* y = reinterpret_cast<float*>(base + w.y);
     hipStream_t st = as_stream(stream);
     const int A = T * k;
@@ -593,26 +765,23 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     a.s_off = geo->gate_scale;
     a.w2_off = geo->up_weight;
     a.s2_off = geo->up_scale;
-    a.hq = hq;
-    a.hs = hs;
+    a.hh = hh;
+    a.hl = hl;
     // 8 spare rows of blocks: the XCD-run order needs the grid to cover 8 ceil(W / 8) slots
     if (int rc = launch_grouped(a, 1, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles + 8, 1), st)) return rc;
     GArgs d{};
     d.recs = recs;
     d.off = pv.off();
-    d.rows = nullptr;
     d.tiles = tiles;
     d.ntiles = ntiles;
-    d.xq = hq;
-    d.xs = hs;
-    d.x_group = 128;
     d.N = geo->hidden;
     d.K = geo->inter;
     d.w_off = geo->down_weight;
     d.s_off = geo->down_scale;
-    d.w2_off = geo->down_weight;
-    d.s2_off = geo->down_scale;
+    d.hh = hh;
+    d.hl = hl;
     d.y = y;
-    if (int rc = launch_grouped(d, 0, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles + 8, 1), st)) return rc;
+    if (int rc = launch_grouped_down(d, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles + 8, 1), st))
+        return rc;
     return launch_combine(y, pv.slot_assign(), weights, out, out_dtype, T, (int)geo->hidden, k, st);
 }

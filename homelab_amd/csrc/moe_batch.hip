@@ -43,7 +43,6 @@ constexpr int B_DEPTH = 8;         // K steps in flight per wave (3 loads each)
 constexpr int B_XS = B_HMAX + 8;   // LDS row stride (bf16) of the activations
 constexpr int B_HS = B_IMAX + 8;   // LDS row stride (bf16) of h
 constexpr int B_TILE = 16;         // output rows of a phase-2 item
-constexpr uint32_t B_SPIN = 1u << 22;
 
 typedef __bf16 bbf16x8 __attribute__((ext_vector_type(8)));
 typedef float bf32x4 __attribute__((ext_vector_type(4)));
@@ -62,6 +61,8 @@ struct BArgs {
     float* h;  // [A, I]
     float* y;  // [A, H]
     uint32_t* hdr;
+    uint32_t* status;  // the device's status word: 1 if a wait gave up (results invalid)
+    uint32_t spin;     // polls before a wait gives up
 };
 
 // The activation / h rows come first: their 16-byte LDS reads and writes need 16-byte
@@ -264,12 +265,12 @@ __device__ __forceinline__ void batch_picks(const uint64_t (&key)[EQ], uint64_t 
 
 template <int EQ, int ODT>
 __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
+    const uint32_t bbase1 = grid_barrier_base(a.hdr + WS_BAR / 4), bbase2 = grid_barrier_base(a.hdr + WS_BAR2 / 4);
     __shared__ BLds L;
     constexpr int NT = 64 * B_W, TPW = B_T / B_W;  // threads; tokens routed per wave
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int T = a.T, E = a.E, k = a.k, A = T * k, H = a.H, I = a.I;
-    uint32_t* const status = a.hdr + WS_STATUS / 4;
     // ---- set-up: this wave's tokens' logits (t = wave + B_W j) in flight first ----
     float lv[TPW][EQ];
 #pragma unroll
@@ -446,7 +447,7 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     };
     start_run();
     wait_mem();  // this wave's h stores are complete before its block arrives
-    grid_barrier_words(a.hdr + WS_BAR / 4, status, B_SPIN);
+    grid_barrier_words(a.hdr + WS_BAR / 4, bbase1, a.status, a.spin);
     while (r0 < last) {
         // stage the slot's h: thread tid takes columns 4 (tid + NT c) .. + 4 of every
         // assignment (zeros past nb and I), 16 loads in flight per pass
@@ -503,7 +504,7 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     // ---- combine: out[t][r .. r + 4] = sum over the token's slots, in slot order, of w y;
     // one lane per 4 rows of a token, the slots' y loads all in flight ----
     wait_mem();
-    grid_barrier_words(a.hdr + WS_BAR / 4, status, B_SPIN);
+    grid_barrier_words(a.hdr + WS_BAR2 / 4, bbase2, a.status, a.spin);  // the second meeting's own area
     const int nq4 = H >> 2;
     for (int g = gw * 64 + lane; g < T * nq4; g += NW * 64) {
         const int t = g / nq4, r = (g - t * nq4) * 4;
@@ -521,6 +522,8 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) store_out<ODT>(a.out, (size_t)t * H + r + e, acc[e]);
     }
+    grid_barrier_exit(a.hdr + WS_BAR / 4);
+    grid_barrier_exit(a.hdr + WS_BAR2 / 4);
 }
 
 // ---- host side -----------------------------------------------------------------------
@@ -598,6 +601,9 @@ int launch_batch(const float* logits, const void* x, const uint64_t* all_recs, i
     a.h = reinterpret_cast<float*>(base + w.h);
     a.y = reinterpret_cast<float*>(base + w.y);
     a.hdr = reinterpret_cast<uint32_t*>(base);
+    a.status = status_word();
+    a.spin = wait_limit();
+    if (!a.status) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: the device status word has no address");
     if (a.E <= 128) return odt == OOM_BF16 ? launch_batch_t<2, OOM_BF16>(a, st) : launch_batch_t<2, OOM_F32>(a, st);
     return odt == OOM_BF16 ? launch_batch_t<4, OOM_BF16>(a, st) : launch_batch_t<4, OOM_F32>(a, st);
 }

@@ -47,7 +47,6 @@ constexpr int F_AMAX = 512;  // assignments (T * k) per step
 constexpr int F_EMAX = 256;  // experts (register router; larger E takes the multi-launch path)
 constexpr int F_HMAX = 4096; // hidden: 4 chunks of 1024 per lane row
 constexpr int F_IMAX = 2048; // inter: 2 chunks
-constexpr uint32_t F_SPIN_LIMIT = 1u << 22;
 
 struct FusedArgs {
     const float* logits;
@@ -62,7 +61,8 @@ struct FusedArgs {
     float* y;
     uint32_t* tickets;   // [ceil(H / FD_R)] down items finished per row tile, TICKET_STRIDE apart
     uint32_t* bar;       // barrier: group counters, top counter, group flags (256 B apart)
-    uint32_t* status;    // 1 if a wait gave up (results invalid)
+    uint32_t* status;    // the device's status word: 1 if a wait gave up (results invalid)
+    uint32_t spin;       // polls before a wait gives up
     int h_bytes;         // bytes of h (bounds of its buffer resource)
     int rec_bytes;       // bytes of a record up to the end of its last part
     // the shared expert (one token, SH): its record address at shared_rec[0] (same geometry
@@ -553,8 +553,11 @@ __device__ __forceinline__ float gate_dot(const FusedArgs& a, const XRow<XDT>& x
     return wave_sum(acc);
 }
 
-// Grid-wide barrier over the workspace header's barrier words (stream.hpp). Used once per kernel.
-__device__ __forceinline__ void grid_barrier(const FusedArgs& a) { grid_barrier_words(a.bar, a.status, F_SPIN_LIMIT); }
+// Grid-wide barrier over the workspace header's barrier area (stream.hpp), `base` read at
+// the kernel's start. Used once per kernel.
+__device__ __forceinline__ void grid_barrier(const FusedArgs& a, uint32_t base) {
+    grid_barrier_words(a.bar, base, a.status, a.spin);
+}
 
 // The plan of up to 64 slots on one wave, lane s = slot s: ranks by readlane
 // broadcast, no LDS round trips. Reads pl.ids, writes slot_assign, assign_tok, experts,
@@ -596,6 +599,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
     static_assert(!SH || TG == 1, "the shared expert rides the one-token kernel");
     constexpr int WB = TG == 1 ? FW1 : FW;  // waves per block
     __shared__ PlanLds pl;
+    const uint32_t bbase = grid_barrier_base(a.bar);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int T = a.T, E = a.E, k = a.k, A = T * k;
@@ -718,7 +722,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             gate1_compute<XDT>(a, pl, it1, NG, w1, xr, lane);
         }
         wait_mem();  // this wave's h stores (and loads) are complete before its block arrives
-        grid_barrier(a);
+        grid_barrier(a, bbase);
         // ---- phase 2, one token: the slot's h once, then per tile the 16 rows of each
         // expert into LDS and the slot-order combine by wave 0 ----
         __shared__ float ylds[FW1][2 * FD1_NP];
@@ -769,7 +773,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
         // ---- the first down item's weights stream while the grid meets ----
         DownW d;
         if (gwave < ND) down_load(a, pl, gwave / tiles_d, gwave % tiles_d, lane, d);
-        grid_barrier(a);
+        grid_barrier(a, bbase);
         // ---- phase 2: down projection -> y, then the ticketed slot-order combine ----
         for (int it = gwave; it < ND; it += NW) {
             if (it != gwave) down_load(a, pl, it / tiles_d, it % tiles_d, lane, d);
@@ -779,6 +783,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
                 combine_tile<ODT>(a, pl, it % tiles_d, lane);
         }
     }
+    grid_barrier_exit(a.bar);
 }
 
 // ---- host side -----------------------------------------------------------------------
@@ -831,6 +836,7 @@ static int launch_fused_t(const FusedArgs& a, size_t lds, hipStream_t st) {
         cached_lds = lds;
     }
     if (cached_blocks <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
+    if (!a.status) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: the device status word has no address");
     // never more waves than items (at most min(E, A) experts' worth)
     const int wb = TG == 1 ? FW1 : FW;
     const int64_t items =
@@ -866,7 +872,8 @@ static FusedArgs fused_args(const float* logits, const void* x, const uint64_t* 
     a.y = reinterpret_cast<float*>(base + w.y);
     a.tickets = reinterpret_cast<uint32_t*>(base + WS_TICKETS);
     a.bar = reinterpret_cast<uint32_t*>(base + WS_BAR);
-    a.status = reinterpret_cast<uint32_t*>(base + WS_STATUS);
+    a.status = status_word();
+    a.spin = wait_limit();
     a.h_bytes = (int)((size_t)T * k * g.inter * sizeof(float));
     a.rec_bytes = (int)record_span(g);
     a.shared_rec = nullptr;

@@ -11,8 +11,10 @@
 //   - a wave streams two rows at a time, one per half (lanes 0..31 row 2p, 32..63 row
 //     2p + 1), so a 640-column down row keeps 20 of each 32 lanes busy, not 20 of 64;
 //   - the codes convert exactly to fp32 with v_cvt_scalef32_pk_f32_fp4 (scale 1), each
-//     group's 16 products sum in fp32 and are scaled once by e4m3(scale) * scale_2, so
-//     only the summation order differs from the reference's per-weight decode;
+//     group's 16 products e2m1 * x sum in fp32, and the group sum is multiplied once by
+//     e4m3(scale) * scale_2. The reference multiplies every weight first, (e2m1 * gs) * x,
+//     so the rounding differs as well as the order (both within the f64 bars the tests
+//     hold: 1e-5 of sum |x . w| per output);
 //   - the inputs of a pass (x rows of up to TB assignments, or h rows) sit in LDS as fp32
 //     in the same lane order (float4 i of lane l's 32 columns of chunk c of row t at
 //     ((t * CH + c) * 8 + i) * 32 + l), staged with 16-byte loads all in flight before
@@ -360,7 +362,6 @@ static size_t stage_lds(int64_t width) { return (size_t)N4_TB * cdiv(width, 1024
 //     (moe_combine_kernel's fmaf order), so no y buffer or combine launch is needed.
 constexpr int N4F_KMAX = 16;                 // expert slots of the one-launch step
 constexpr size_t N4F_LDS_MAX = 64 * 1024;    // staged x or h rows
-constexpr uint32_t N4F_SPIN_LIMIT = 1u << 22;
 
 struct Fused4Args {
     const float* logits;
@@ -373,7 +374,8 @@ struct Fused4Args {
     void* out;
     float* h;  // [k, I]
     uint32_t* bar;
-    uint32_t* status;
+    uint32_t* status;  // the device's status word: 1 if the grid barrier's wait gave up
+    uint32_t spin;     // polls before a wait gives up
 };
 
 // Rows 0 .. rows - 1 of h (f32, width K) into LDS in stage4's lane order through
@@ -468,6 +470,7 @@ __device__ __forceinline__ void dn4_compute(const Dn4W& w, const float4* xs4, co
 
 template <int XDT, int EQ, int ODT>
 __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
+    const uint32_t bbase = grid_barrier_base(a.bar);
     extern __shared__ float4 xs4[];
     __shared__ uint64_t recs_l[N4F_KMAX];
     __shared__ float w_l[N4F_KMAX];
@@ -502,7 +505,7 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
         gu4_pass<1, 4>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
     }
     wait_mem();  // this wave's h stores are complete before its block arrives
-    grid_barrier_words(a.bar, a.status, N4F_SPIN_LIMIT);
+    grid_barrier_words(a.bar, bbase, a.status, a.spin);
     // ---- phase 2: the k h rows once, then per output tile the slot rows and the combine ----
     stage_rows_dev(xs4, a.h, I, CHI, k);
     __syncthreads();
@@ -532,6 +535,7 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
         }
         __syncthreads();
     }
+    grid_barrier_exit(a.bar);
 }
 
 // LDS of the one-launch kernel: x staged for one token, then the k h rows.
@@ -674,8 +678,10 @@ extern "C" int oom_moe_decode_nvfp4(const float* logits, const void* x, int x_dt
     float* y = reinterpret_cast<float*>(base + w.y);
     hipStream_t st = as_stream(stream);
     if (fused4_ok(T, E, k, *geo)) {
+        uint32_t* status = status_word();
+        if (!status) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_nvfp4: the device status word has no address");
         Fused4Args a{logits, x, all_recs, E, k, rec4_of(*geo), ids, weights, out, h,
-                     reinterpret_cast<uint32_t*>(base + WS_BAR), reinterpret_cast<uint32_t*>(base + WS_STATUS)};
+                     reinterpret_cast<uint32_t*>(base + WS_BAR), status, wait_limit()};
         const size_t lds = fused4_lds(*geo, k);
         return x_dtype == OOM_BF16 ? launch_fused4_e<OOM_BF16>(a, out_dtype, lds, st)
                                    : launch_fused4_e<OOM_F32>(a, out_dtype, lds, st);

@@ -6,6 +6,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "grid_barrier.hpp"
 
 namespace oom {
 
@@ -16,18 +17,15 @@ constexpr int BUF_SC1 = 16;            // cache-policy bit of a device-coherent 
 // ---- decode workspace header ---------------------------------------------------------
 // Every decode workspace starts with this header at fixed offsets, whatever the step's
 // shape, so a workspace shared by steps of different shapes (batch 1 and batch 16 of one
-// model) never reads another layout's data as its state. Each word or counter has a
-// 256-byte line of its own: atomics and polls on one line serialise at the memory side.
-constexpr size_t WS_EPOCH = 0;          // u32: the one-token kernel's call epoch
-constexpr size_t WS_STATUS = 256;       // u32: 1 if a wait of a decode kernel gave up
-constexpr int D1_MAX_BLOCKS = 1024;     // blocks of the one-token kernel
-constexpr size_t WS_STARTED = 512;      // u32[D1_MAX_BLOCKS]: the epoch each block of the last call saw
-constexpr int BAR_GROUPS = 8;           // barrier groups of the multi-token kernel
-constexpr int BAR_STRIDE = 64;          // u32 words between its counters
-constexpr size_t WS_BAR = WS_STARTED + D1_MAX_BLOCKS * 4;        // (2 BAR_GROUPS + 1) lines
+// model) never reads another layout's data as its state. Each counter has a 256-byte line
+// of its own: atomics and polls on one line serialise at the memory side. Barrier areas
+// and tickets are left at zero by every call that completes, so only a new workspace
+// needs clearing (oom_workspace_init).
+constexpr size_t WS_BAR = 0;                                      // barrier area of a kernel's first grid meeting
+constexpr size_t WS_BAR2 = WS_BAR + BAR_WORDS * 4;                // ... and of its second
 constexpr int TICKET_STRIDE = 64;
 constexpr int MAX_TILES = 4096 / 8;     // row tiles of 8 rows for hidden <= 4096
-constexpr size_t WS_TICKETS = WS_BAR + (2 * BAR_GROUPS + 1) * BAR_STRIDE * 4;  // MAX_TILES lines
+constexpr size_t WS_TICKETS = WS_BAR2 + BAR_WORDS * 4;            // MAX_TILES lines
 constexpr size_t WS_HEADER = (WS_TICKETS + (size_t)MAX_TILES * TICKET_STRIDE * 4 + 4095) & ~size_t(4095);
 
 // ---- loads ----------------------------------------------------------------------------
@@ -114,49 +112,55 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ---- grid barrier -------------------------------------------------------------------------
-// One arrival per block, in two levels so no counter sees more than 64 arrivals: block b
-// arrives at group b % G (G = 8, one group per XCD under round-robin dispatch); the last
-// of a group arrives at the top counter; the last of those publishes the next generation
-// in every group's generation word, which that group's blocks poll. Counters are reset by
-// their last arrival and generations only grow, so nothing needs clearing between calls.
-// `bar` is the workspace header's barrier area; a wait that gives up sets *status = 1.
-// Every block of the grid must be resident.
-__device__ __forceinline__ void grid_barrier_words(uint32_t* bar, uint32_t* status, uint32_t spin_limit) {
+// The protocol is grid_barrier.hpp's over relaxed agent-scope atomics, which are performed
+// at the device's point of coherence (not in one XCD's L2): lane q < BAR_GROUPS of the
+// block's first wave handles group counter q.
+
+// The bases of barrier area `bar`: lane q < BAR_GROUPS of the first wave reads group q's
+// exit counter (every other thread returns 0). Called at kernel start by every thread;
+// the value is used by the block's first wave at the barrier.
+__device__ __forceinline__ uint32_t grid_barrier_base(uint32_t* bar) {
+    return threadIdx.x < (unsigned)BAR_GROUPS
+               ? __hip_atomic_load(bar + BAR_EXIT + threadIdx.x * BAR_STRIDE, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT)
+               : 0u;
+}
+
+// The block's exit from barrier area `bar`: its last action on the area, after its wait
+// (every block of the grid, exactly once per call, on every path).
+__device__ __forceinline__ void grid_barrier_exit(uint32_t* bar) {
+    if (threadIdx.x == 0)
+        (void)__hip_atomic_fetch_add(bar + BAR_EXIT + (blockIdx.x % bar_groups(gridDim.x)) * BAR_STRIDE, 1u,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The grid meets at barrier area `bar` (one area per meeting of a kernel), `base` from
+// grid_barrier_base at the kernel's start; every block calls grid_barrier_exit(bar) after
+// it. Every wave's earlier stores must be complete
+// (wait_mem) before it reaches the barrier. A wait that gives up after `spin_limit` polls
+// sets the device's status word (*status = 1, read by oom_status) and lets the block go
+// on: the kernel still ends, its outputs are invalid. The launchers size the grid by the
+// occupancy limit so it is resident at once; when it is not, the bounded wait turns that
+// into a reported error, not a hang.
+__device__ __forceinline__ void grid_barrier_words(uint32_t* bar, uint32_t base, uint32_t* status,
+                                                   uint32_t spin_limit) {
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t G = min(gridDim.x, (uint32_t)BAR_GROUPS), g = blockIdx.x % G;
-        const uint32_t n_g = (gridDim.x - g + G - 1) / G;
-        uint32_t* cnt = bar + g * BAR_STRIDE;
-        uint32_t* genw = bar + (BAR_GROUPS + 1 + g) * BAR_STRIDE;
-        uint32_t* top = bar + BAR_GROUPS * BAR_STRIDE;
-        // the generation is read before this block arrives, and waited for: memory
-        // operations to different addresses may be performed out of order, and a read
-        // after the last arrival would see the next generation and wait for one more
-        const uint32_t gen = __hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_mem();
-        const uint32_t target = gen + 1u;
-        bool released = false;
-        if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_g - 1) {
-            __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            wait_mem();
-            if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1) {
-                __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                wait_mem();
-                for (uint32_t q = 0; q < G; q++)
-                    __hip_atomic_store(bar + (BAR_GROUPS + 1 + q) * BAR_STRIDE, target, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                wait_mem();
-                released = true;
-            }
-        }
-        if (!released) {
-            uint32_t spins = 0;
-            while ((int32_t)(__hip_atomic_load(genw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-                __builtin_amdgcn_s_sleep(4);
-                if (++spins > spin_limit) {
-                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        wait_mem();  // the bases have been read before this block arrives
+        if (lane == 0)
+            (void)__hip_atomic_fetch_add(bar + (blockIdx.x % bar_groups(gridDim.x)) * BAR_STRIDE, 1u,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t need = lane < BAR_GROUPS ? base + bar_group_size((uint32_t)lane, gridDim.x) : 0u;
+        uint32_t* mine = bar + (lane < BAR_GROUPS ? lane : 0) * BAR_STRIDE;
+        for (uint32_t spins = 0;;) {
+            const bool met = lane >= BAR_GROUPS ||
+                             (int32_t)(__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - need) >= 0;
+            if (__ballot(!met) == 0) break;
+            __builtin_amdgcn_s_sleep(2);
+            if (++spins > spin_limit) {
+                if (lane == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
             }
         }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);

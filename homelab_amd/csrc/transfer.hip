@@ -118,6 +118,11 @@ extern "C" int oom_event_wait(void* event) {
     return hip_ok(hipEventSynchronize(static_cast<hipEvent_t>(event)), "oom_event_wait");
 }
 
+extern "C" int oom_status(void* stream);
+
+// A sync point: waits for `stream`, then reports a bounded wait that gave up inside an
+// earlier kernel (OOM_ERR_KERNEL) the way oom_status does.
 extern "C" int oom_stream_sync(void* stream) {
-    return hip_ok(hipStreamSynchronize(oom::as_stream(stream)), "oom_stream_sync");
+    if (int rc = hip_ok(hipStreamSynchronize(oom::as_stream(stream)), "oom_stream_sync")) return rc;
+    return oom_status(stream);
 }

@@ -32,6 +32,7 @@ extern "C" {
 #define OOM_ERR_ARG (-1)       /* shape unsupported, null pointer, misaligned buffer */
 #define OOM_ERR_WORKSPACE (-2) /* workspace smaller than *_workspace_size() */
 #define OOM_ERR_LAUNCH (-3)    /* the HIP runtime refused a launch */
+#define OOM_ERR_KERNEL (-4)    /* a bounded wait inside an earlier kernel gave up (oom_status) */
 
 /* Element types of activations and outputs. */
 #define OOM_F32 0
@@ -65,6 +66,23 @@ typedef struct OomFp8Record {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* oom_last_error(void);
+
+/* Kernel-side failures. The persistent decode kernels meet across the grid through
+ * bounded waits; a wait that gives up (the grid was not resident at once, or a limit
+ * set by oom_set_wait_limit) lets the kernel end normally with invalid outputs and
+ * sets the current device's status word. Like the reference's asynchronous CUDA
+ * errors, which surface at its next synchronising call as an Err (its error contract:
+ * crates/oominf-cuda/src/lib.rs:157-160), that failure is reported at a sync point:
+ * oom_status waits for `stream`, then returns OOM_ERR_KERNEL if any kernel of this
+ * library on the current device gave up a wait since the last oom_status (and clears
+ * the word), else OOM_OK. oom_stream_sync reports it the same way. */
+int oom_status(void* stream);
+
+/* Polls of each bounded wait before it gives up, for later launches of this process
+ * (0 restores the default, 2^22 polls of about 0.1 us). A tiny limit makes waits give
+ * up at once: kernels still end normally, and oom_status then reports OOM_ERR_KERNEL;
+ * tests use it to exercise the failure path without a GPU fault. */
+int oom_set_wait_limit(uint32_t spins);
 
 /* Zero-fills `bytes` of workspace at `ws` on `stream` with a fill kernel (no
  * hipMemset node, so it is safe inside graph capture). */

@@ -169,8 +169,9 @@ void oracle_grouped_gemm_fp8(const uint8_t* const* recs, const int32_t* off, con
                              int64_t w_off, int64_t s_off);
 
 /* Whole prefill MoE FFN over the routed assignments of T tokens: x fp32 [T, H]
- * quantised per token, gate and up grouped GEMMs, h = silu(g) * u quantised per
- * (assignment, 128 columns), down grouped GEMM, slot-order combine.
+ * quantised per token, gate and up grouped GEMMs, h = silu(g) * u kept in fp32 (the
+ * reference's exact tiled path, ExpertPrecision::Exact), the down projection as
+ * oracle_moe_down_fp8, slot-order combine.
  * crates/oominf-models-qwen/src/moe.rs:746-758 (tiled run_group) + :700.
  * Returns n_e or -1. */
 int oracle_moe_prefill_fp8(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,

@@ -383,14 +383,14 @@ int oracle_moe_prefill_fp8(const float* logits, const float* x, const uint8_t* c
     oracle_grouped_gemm_fp8(recs, off, tok, n_e, xq, xs, 0, g, I, H, geo->gate_weight, geo->gate_scale);
     oracle_grouped_gemm_fp8(recs, off, tok, n_e, xq, xs, 0, u, I, H, geo->up_weight, geo->up_scale);
     for (size_t i = 0; i < (size_t)A * (size_t)I; i++) g[i] = siluf(g[i]) * u[i];
-    int64_t nib = cdiv(I, 128);
-    uint8_t* hq = (uint8_t*)malloc((size_t)A * (size_t)I);
-    float* hs = (float*)malloc(sizeof(float) * (size_t)A * (size_t)nib);
-    oracle_quantize_act(g, A, I, 128, hq, hs);
+    /* h stays fp32 into the down projection, as the reference's exact tiled path keeps its
+     * activations (ExpertPrecision::Exact, crates/oominf-core/src/backend.rs:144-149;
+     * crates/oominf-cuda/kernels/moe.cu:166-335 with three bf16 terms): the decode path's
+     * down, per-128-column block sums times the block scale. */
     float* y = (float*)malloc(sizeof(float) * (size_t)A * (size_t)H);
-    oracle_grouped_gemm_fp8(recs, off, NULL, n_e, hq, hs, 128, y, H, I, geo->down_weight, geo->down_scale);
+    oracle_moe_down_fp8(recs, off, n_e, g, y, geo);
     oracle_moe_combine_slots(y, slot, weights, out, T, (int)H, k);
-    free(y); free(hq); free(hs); free(g); free(u); free(xq); free(xs);
+    free(y); free(g); free(u); free(xq); free(xs);
     free(recs); free(experts); free(off); free(tok); free(slot);
     return n_e;
 }

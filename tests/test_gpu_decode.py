@@ -218,10 +218,15 @@ def test_experts_stage_by_stage(hip, H, I, E, T, k):
     assert_bf16_close(to_f32(out), out_want, "combine")
 
 
-@pytest.mark.parametrize("T,E,k,zipf", [(1, 128, 8, None), (16, 128, 8, 1.1), (64, 128, 8, 1.1), (5, 16, 4, None)])
+@pytest.mark.parametrize("T,E,k,zipf", [(1, 128, 8, None), (16, 128, 8, 1.1), (64, 128, 8, 1.1), (5, 16, 4, None),
+                                        (64, 512, 10, 1.1),   # the released model's E, ballot ranks, one round
+                                        (128, 512, 10, 1.1),  # ... past 1024 slots: two rounds
+                                        (3, 8192, 32, None),  # the largest E and k: the counting fallback
+                                        (40, 8192, 32, 1.1)])  # ... over two rounds of 1024 slots
 def test_device_plan_matches_host_plan(hip, T, E, k, zipf):
     import torch
 
+    print(f"case: device plan T={T} E={E} k={k} zipf={zipf}", flush=True)
     logits = synth.decode_logits(5 + T, T, E, zipf)
     ids, _ = oracle.router_topk(logits, k)
     experts, off, tok, slot = oracle.moe_plan(ids, E)
@@ -255,6 +260,9 @@ def decode_case(T, E, k, zipf, seed, H=4096, I=1536):
 @pytest.mark.parametrize("T,E,k,zipf,H,I", [(1, 128, 8, None, 4096, 1536), (16, 128, 8, 1.1, 4096, 1536),
                                             (4, 128, 8, None, 4096, 1536), (64, 128, 8, 1.1, 1024, 512),
                                             (3, 16, 4, None, 256, 128), (80, 64, 8, None, 1024, 512),
+                                            # E > 256 takes the multi-launch path (router, device plan at
+                                            # E = 512, gate/up, down, combine)
+                                            (4, 512, 8, None, 1024, 512), (1, 512, 10, None, 2048, 512),
                                             pytest.param(2, 300, 6, None, 512, 256, marks=pytest.mark.skip(
                                                 reason="left the GPU faulted once with the one-launch kernel's "
                                                        "E > 256 router (cause not found on the CPU); that path is "

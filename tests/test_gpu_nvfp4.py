@@ -120,6 +120,7 @@ def test_gate_up_and_down_stage_by_stage(hip, H, I, T, xf32):
 
 @pytest.mark.parametrize("T,E,k,zipf,H,I,xf32", [
     (1, 512, 10, None, 2560, 640, False),   # the released model's routed experts, one token
+    (4, 512, 10, None, 2560, 640, False),   # ... four tokens: router, device plan at E = 512, staged launches
     (4, 64, 8, None, 4096, 1536, False),    # the FP8 benchmark's widths in NVFP4
     (16, 128, 8, 1.1, 1040, 432, False),    # widths ending inside a 32-column piece, popular experts
     (9, 32, 6, None, 512, 256, False),      # experts with more tokens than a pass holds
@@ -224,3 +225,4 @@ def test_decode_nvfp4_one_launch_matches_stages(hip, E, k, H, I, xf32):
     got = outb.float().cpu().numpy()
     bad = ~np.isclose(got, want_or, rtol=RTOL, atol=ATOL)
     assert not bad.any(), f"{bad.sum()} of {bad.size} outside; worst {np.abs(got - want_or)[bad].max():.3e}"
+    assert hip.status() == hip.OK, "a wait of the one-launch kernel gave up"

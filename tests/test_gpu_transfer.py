@@ -1,7 +1,10 @@
 """Copies beside compute (the Transfer trait, crates/oominf-core/src/backend.rs:945-1018):
 host-tier expert records staged into device slots on a copy queue, ordered against the
-decode step with events, give the same output as resident records, bit for bit; a download
-queued after compute lands in pinned host memory when its event completes."""
+decode step with events. Checked: every slot holds its host record byte for byte; the
+step over the slots gives the same output as resident records, bit for bit, and the
+oracle's output (moe_decode on the host records) within 2e-5 of scale; downloads queued
+after compute (the output, and the router ids as download_start_i32 / download_wait_i32
+take them, backend.rs:984-993) land in pinned host memory when their event completes."""
 import numpy as np
 import pytest
 
@@ -47,6 +50,7 @@ def test_staged_records_match_resident(hip, E, k, H, I):
     hip.moe_decode_fp8(ld, xd, addrs, k, hgeo, gids, gw, want, ws)
     torch.cuda.synchronize()
     want = want.cpu().numpy()
+    want_ids, _, want_or = oracle.moe_decode(logits, oracle.bf16_to_f32(xb), recs, k, geo)
     # host tier: all records in pinned host memory; k device slots
     host = hip.PinnedHost(E * stride)
     host.array()[:] = np.stack(recs).reshape(-1)
@@ -64,6 +68,10 @@ def test_staged_records_match_resident(hip, E, k, H, I):
             q.copy_records(dst, [host.ptr + e * stride for e in order], stride)
             copied.record(q)
             copied.wait_on(None)
+            # the slots hold the host records, byte for byte
+            copied.wait()
+            for i, e in enumerate(order):
+                assert np.array_equal(slots[i].cpu().numpy(), recs[e]), f"rep {rep}: slot {i} != record {e}"
             table = np.full(E, dst[0], dtype=np.int64)
             for i, e in enumerate(order):
                 table[e] = dst[i]
@@ -79,9 +87,22 @@ def test_staged_records_match_resident(hip, E, k, H, I):
             got = dl.array("float32").copy()
             dl.close()
             done.close()
+            # the ids as download_start_i32 / download_wait_i32 take them: a download after
+            # the compute issued so far into pinned memory, then a wait on its event
+            dli = hip.PinnedHost(k * 4)
+            done_i = hip.Event()
+            hip.download_async(dli.ptr, gids, k * 4)
+            done_i.record()
+            done_i.wait()
+            got_ids = dli.array("int32").copy()
+            dli.close()
+            done_i.close()
+            np.testing.assert_array_equal(got_ids, want_ids.reshape(-1), err_msg=f"rep {rep}: downloaded ids")
             np.testing.assert_array_equal(gids.cpu().numpy(), ids, err_msg=f"rep {rep}")
             diff = np.flatnonzero(got.view(np.uint32) != want.reshape(-1).view(np.uint32))
             assert diff.size == 0, f"rep {rep}: {diff.size} of {H} differ"
+            err = np.abs(got - want_or.reshape(-1)).max()
+            assert err <= 2e-5 * np.abs(want_or).max(), f"rep {rep}: staged output vs oracle: {err:.3e}"
         # a device-to-device copy on the queue
         moved = torch.zeros(stride, dtype=torch.uint8, device="cuda")
         q.copy_on_device(moved.data_ptr(), slots.data_ptr(), stride)

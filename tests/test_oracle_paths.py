@@ -225,6 +225,25 @@ def test_prefill_matches_decode_semantics_within_quantisation():
     assert rel < 0.06
 
 
+def test_prefill_is_decode_over_dequantised_activations():
+    # with h kept in fp32, the prefill oracle is the decode oracle (pinned against f64 and
+    # the closed-form record) applied to the per-token e4m3 activations xs * e4m3(xq): the
+    # only difference is where xs multiplies (after each gate/up sum instead of into every
+    # activation), a few fp32 roundings; a dropped term, a wrong scale or a quantised h
+    # would move it by orders of magnitude more
+    geo, recs = small_moe()
+    T, E, k = 12, 16, 4
+    logits = synth.decode_logits(19, T, E)
+    x = oracle.bf16_to_f32(synth.activations_bf16(19, T, geo.hidden))
+    xq, xs = oracle.quantize_act(x)
+    xd = (oracle.e4m3_decode(xq).astype(np.float64) * xs[:, None]).astype(np.float32)
+    ids_p, w_p, out_p = oracle.moe_prefill(logits, x, recs, k, geo)
+    ids_d, w_d, out_d = oracle.moe_decode(logits, xd, recs, k, geo)
+    np.testing.assert_array_equal(ids_p, ids_d)
+    err = np.abs(out_p - out_d).max()
+    assert err <= 2e-6 * np.abs(out_d).max(), err
+
+
 # ---- paged decode attention -----------------------------------------------------------
 
 def paged_case(seed, H, Hkv, D, kv_len, page=16):
