@@ -55,6 +55,8 @@ SIGNATURES = {
     "oom_moe_plan": (I32, [P, I32, I32, I32, P, P, P, P]),
     "oom_moe_decode_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
     "oom_moe_decode_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
+    "oom_moe_decode_fp8_noalloc_max_bytes": (SZ, []),
+    "oom_moe_decode_fp8_noalloc": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P]),
     "oom_moe_gate_up_nvfp4": (I32, [P, P, P, I32, P, I32, P, P, P]),
     "oom_moe_down_nvfp4": (I32, [P, P, I32, P, P, P, P]),
     "oom_moe_decode_nvfp4_workspace_size": (SZ, [I32, I32, I32, P]),

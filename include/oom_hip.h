@@ -179,6 +179,20 @@ int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const ui
                        int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
                        void* ws, size_t ws_bytes, void* stream);
 
+/* oom_moe_decode_fp8 without a caller workspace: the same step, same kernels, same bits,
+ * with its scratch in a device array of the library (oom_moe_decode_fp8_noalloc_max_bytes()
+ * bytes, 4 MiB: every step with T <= 16, k <= 8, hidden <= 4096 and inter <= 2048 fits;
+ * a larger step returns OOM_ERR_WORKSPACE). It allocates nothing, not even on its first
+ * call, so callers that cannot allocate can use it: code under graph capture, tight
+ * serving loops, harnesses that forbid allocation. Every call on one device shares that
+ * device's array and leaves it ready for the next call; calls that overlap in time on
+ * one device (two streams, two threads) race, so order them on one stream. No counterpart
+ * in the reference, whose backend keeps its scratch in a per-device workspace. */
+size_t oom_moe_decode_fp8_noalloc_max_bytes(void);
+int oom_moe_decode_fp8_noalloc(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T,
+                               int E, int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out,
+                               int out_dtype, void* stream);
+
 /* The shared expert's gated add: out[t, c] = routed[t, c] + sigmoid(gate_logit[t]) *
  * shared[t, c], sigmoid(v) = 1 / (1 + e^-v); routed and shared f32 [T, H], gate_logit f32
  * [T]; out [T, H] in out_dtype. Replaces Elementwise::moe_combine
