@@ -358,8 +358,8 @@ __device__ __forceinline__ void gate1_load(const FusedArgs& a, const PlanLds& pl
         const int col = c * 1024 + lane * 16;
         const bool ok = col < H;
         const int row = j * H + col, sc = ((j >> 7) * nkb + (col >> 7)) * 4;
-        w.g[c] = ld16(r, ok ? (int)a.gw + row : OOB);
-        w.u[c] = ld16(r, ok ? (int)a.uw + row : OOB);
+        w.g[c] = ld16nt(r, ok ? (int)a.gw + row : OOB);
+        w.u[c] = ld16nt(r, ok ? (int)a.uw + row : OOB);
         w.sg[c] = ldf(r, ok ? (int)a.gs + sc : OOB);
         w.su[c] = ldf(r, ok ? (int)a.us + sc : OOB);
     }
@@ -420,7 +420,7 @@ __device__ __forceinline__ void down1_load(const FusedArgs& a, const PlanLds& pl
 #pragma unroll
         for (int p = 0; p < FD1_NP; p++) {
             const int row = r0 + 2 * p + half;
-            d.w[p][c] = ld16(r, row < H && col < I ? (int)a.dw + row * I + col : OOB);
+            d.w[p][c] = ld16nt(r, row < H && col < I ? (int)a.dw + row * I + col : OOB);
         }
         d.s[c] = ldf(r, col < I ? (int)a.ds + ((r0 >> 7) * nkb + (col >> 7)) * 4 : OOB);
     }
