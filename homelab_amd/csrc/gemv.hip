@@ -23,7 +23,7 @@
 //     T can have at this N (rows / 4), then the partials: a workspace left by a call
 //     of another T or K still has zero tickets where this call looks (partials are
 //     written before they are read), so calls with one N share a workspace.
-#include "common.hpp"
+#include "stream.hpp"
 
 namespace oom {
 
@@ -44,46 +44,56 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
     const int kl = min(K, k0 + klen) - k0;
     const int row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
     const int nkb = (K + 127) >> 7;
-    // the weights first: their loads are in flight while x is staged
+    // x's loads first (16 bytes: 8 bf16 or 4 f32 of one lane's 16 columns, when x is
+    // 16-byte aligned; K % 16 == 0 keeps a load inside one row and on one side of kl), then
+    // the weights': loads complete in issue order, so x can be staged in LDS while the
+    // weights are still in flight
+    // (buffer loads, no branch: an unaligned x or a lane past the data reads zeros through an
+    // out-of-range offset, which keeps the compiler's count of loads in flight exact)
+    const bool xal = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    constexpr int EPL = XDT == OOM_BF16 ? 8 : 4;
+    constexpr int NV = T * KCH * 1024 / EPL;
+    constexpr int NLD = (NV + 255) / 256;
+    constexpr int XES = XDT == OOM_BF16 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, tn * K * XES, BUF_FLAGS);
+    uint4 v[NLD];
+#pragma unroll
+    for (int n = 0; n < NLD; n++) {
+        const int i = threadIdx.x + 256 * n;
+        const int t = i * EPL / klen, kk = i * EPL - t * klen;
+        const bool ok = xal && i < NV && t < tn && kk < kl;
+        v[n] = ld16(xr, ok ? (t * K + k0 + kk) * XES : OOB);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // x's loads stay ahead of the weights
+    // each row's split through a resource of its own (the row is uniform over the wave);
+    // nontemporal: the weights are read once a call
     constexpr int NW = WB ? 2 : 1;  // 16-byte loads per lane per (row, chunk)
     uint4 w[R][KCH][NW];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        int row = min(row0 + r, N - 1);
+        const int row = min(row0 + r, N - 1);
+        const __amdgpu_buffer_rsrc_t wr =
+            uniform_rsrc(reinterpret_cast<uint64_t>(q + ((size_t)row * K + k0) * NW), kl * NW);
 #pragma unroll
         for (int c = 0; c < KCH; c++) {
-            int col = c * 1024 + lane * 16;
+            const int col = c * 1024 + lane * 16;
 #pragma unroll
-            for (int h = 0; h < NW; h++)
-                w[r][c][h] = col < kl ? *reinterpret_cast<const uint4*>(q + ((size_t)row * K + k0 + col) * NW + 16 * h)
-                                      : make_uint4(0, 0, 0, 0);
+            for (int h = 0; h < NW; h++) w[r][c][h] = ld16nt(wr, col < kl ? col * NW + 16 * h : OOB);
         }
     }
 
     // stage x[t, k0 .. k0 + kl) in lane order (zeros past kl and for padded tokens): element
     // kk = c * 1024 + 16 l + j of token t sits at float index
     // (((t * KCH + c) * 4 + j / 4) * 64 + l) * 4 + j % 4
+    // (written on every path, zeros for an unaligned x, so the loads stay ahead of the
+    // weights' instead of moving into a branch)
     float* xs = reinterpret_cast<float*>(xs4);
-    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
-        // 16-byte loads (8 bf16 or 4 f32 of one lane's 16 columns), all issued before the
-        // first LDS store; K % 16 == 0 keeps a load inside one row and on one side of kl
-        constexpr int EPL = XDT == OOM_BF16 ? 8 : 4;
-        constexpr int NV = T * KCH * 1024 / EPL;
-        constexpr int NLD = (NV + 255) / 256;
-        uint4 v[NLD];
+    {
 #pragma unroll
         for (int n = 0; n < NLD; n++) {
             const int i = threadIdx.x + 256 * n;
-            const int t = i * EPL / klen, kk = i * EPL - t * klen;
-            const bool ok = i < NV && t < tn && kk < kl;
-            const size_t e = (size_t)t * K + k0 + kk;
-            v[n] = ok ? *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + e * (XDT == OOM_BF16 ? 2 : 4))
-                      : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int n = 0; n < NLD; n++) {
-            const int i = threadIdx.x + 256 * n;
-            if (i >= NV) break;
+            if (NV % 256 != 0 && i >= NV) break;
             const int t = i * EPL / klen, kk = i * EPL - t * klen;
             const int c = kk >> 10, l = (kk & 1023) >> 4, j = kk & 15;
             float4* dst = &xs4[((t * KCH + c) * 4 + (j >> 2)) * 64 + l];
@@ -97,7 +107,9 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
                                      __uint_as_float(v[n].w));
             }
         }
-    } else {
+    }
+    if (!xal) {
+        __syncthreads();
         for (int i = threadIdx.x; i < T * klen; i += blockDim.x) {
             int t = i / klen, kk = i - t * klen;
             int c = kk >> 10, l = (kk & 1023) >> 4, j = kk & 15;
@@ -163,25 +175,31 @@ __global__ void __launch_bounds__(256) gemv_fp8_kernel(const void* __restrict__ 
     if (writer && row < N && t < tn) {
         if constexpr (!WB && SL == OOM_SCALE_ROW) tot *= scale[row];
         if (splits == 1) store_out<YDT>(y, (size_t)t * N + row, tot);
-        else partial[((size_t)split * T + t) * N + row] = tot;
+        else st_dev(&partial[((size_t)split * T + t) * N + row], tot);
     }
     if (splits == 1) return;
+    // Partials move between blocks (of any XCD) as device-coherent stores and loads, and
+    // the ticket is a relaxed device-scope add taken after this block's stores are
+    // acknowledged: no agent-scope fence, whose L2 write-back and invalidate per block
+    // cost ten times the whole GEMV.
     __shared__ bool last;
-    __threadfence();
+    wait_mem();
     __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(&tickets[blockIdx.x], 1u) == (unsigned)splits - 1;
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(&tickets[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == (unsigned)splits - 1;
+        if (last) __hip_atomic_store(&tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     const int tile = GEMV_WAVES * R, first = blockIdx.x * tile;
     for (int i = threadIdx.x; i < tn * tile; i += blockDim.x) {
         int tt = i / tile, n = first + i % tile;
         if (n >= N) continue;
         float sum = 0.0f;
-        for (int s = 0; s < splits; s++) sum += __builtin_nontemporal_load(&partial[((size_t)s * T + tt) * N + n]);
+        for (int s = 0; s < splits; s++) sum += ld_dev(&partial[((size_t)s * T + tt) * N + n]);
         store_out<YDT>(y, (size_t)tt * N + n, sum);
     }
-    if (threadIdx.x == 0) tickets[blockIdx.x] = 0;
 }
 
 // Launch geometry of one call (shared by the workspace query and the launch).
@@ -207,6 +225,16 @@ static GemvPlan gemv_plan(int T, int64_t N, int64_t K, bool wb = false) {
     // x of one split in LDS: tp * kch * 4 KiB <= 64 KiB
     int kch_max = std::max(1, 16 / p.tp);
     kch_max = std::min(kch_max, wb ? 2 : 4);  // bf16 rows take twice the registers per chunk
+    if (!wb && p.tp <= 4 && kchunks <= kch_max && cdiv(N, (int64_t)GEMV_WAVES * 2) >= 512) {
+        // two rows a wave fill the chip (>= 512 blocks) with the whole of K in one block:
+        // no split, so no second round trip through the partials
+        p.R = 2;
+        p.kch = kchunks <= 1 ? 1 : kchunks <= 2 ? 2 : 4;
+        p.splits = 1;
+        p.tiles = (int)cdiv(N, (int64_t)GEMV_WAVES * p.R);
+        p.lds = (size_t)p.tp * p.kch * 1024 * sizeof(float);
+        return p;
+    }
     p.tiles = (int)cdiv(N, (int64_t)GEMV_WAVES * p.R);
     // enough blocks to cover the CUs (>= 512 blocks), but a split never shorter than 1 KiB
     int want = (int)std::max<int64_t>(1, cdiv(512, p.tiles));
@@ -280,6 +308,7 @@ extern "C" int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const 
     OOM_REQUIRE(T >= 1 && T <= 16, "oom_gemv_fp8: T must be 1..16");
     OOM_REQUIRE(N >= 1 && K >= 16 && K % 16 == 0, "oom_gemv_fp8: K must be a positive multiple of 16");
     OOM_REQUIRE(N <= INT32_MAX && K <= INT32_MAX && N * K <= ((int64_t)1 << 40), "oom_gemv_fp8: shape too large");
+    OOM_REQUIRE((int64_t)T * K * 4 < 0x7fff0000ll, "oom_gemv_fp8: x beyond 2 GiB");
     OOM_REQUIRE(x && q && scale && y, "oom_gemv_fp8: null buffer");
     OOM_REQUIRE(aligned(q, 16), "oom_gemv_fp8: weights must be 16-byte aligned");
     OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_gemv_fp8: x_dtype");
@@ -299,9 +328,14 @@ extern "C" int oom_gemv_fp8(const void* x, int x_dtype, const uint8_t* q, const 
     hipStream_t st = as_stream(stream);
     int n = (int)N, k = (int)K;
     switch (p.tp) {
-        case 1: launch_gemv_k<1, 4>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
-        case 2: launch_gemv_k<2, 4>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
-        case 4: launch_gemv_k<4, 4>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
+#define GEMV_FP8_T(TP)                                                                                        \
+    if (p.R == 2) launch_gemv_k<TP, 2>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); \
+    else launch_gemv_k<TP, 4>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st);         \
+    break;
+        case 1: GEMV_FP8_T(1)
+        case 2: GEMV_FP8_T(2)
+        case 4: GEMV_FP8_T(4)
+#undef GEMV_FP8_T
         case 8: launch_gemv_k<8, 2>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
         default: launch_gemv_k<16, 2>(p, scale_layout, x_dtype, y_dtype, x, q, scale, y, part, tk, T, n, k, st); break;
     }
@@ -319,6 +353,7 @@ extern "C" int oom_gemv_bf16(const void* x, int x_dtype, const uint16_t* w, void
     OOM_REQUIRE(T >= 1 && T <= 16, "oom_gemv_bf16: T must be 1..16");
     OOM_REQUIRE(N >= 1 && K >= 16 && K % 16 == 0, "oom_gemv_bf16: K must be a positive multiple of 16");
     OOM_REQUIRE(N <= INT32_MAX && K <= INT32_MAX && N * K <= ((int64_t)1 << 39), "oom_gemv_bf16: shape too large");
+    OOM_REQUIRE((int64_t)T * K * 4 < 0x7fff0000ll, "oom_gemv_bf16: x beyond 2 GiB");
     OOM_REQUIRE(x && w && y, "oom_gemv_bf16: null buffer");
     OOM_REQUIRE(aligned(w, 16), "oom_gemv_bf16: weights must be 16-byte aligned");
     OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_gemv_bf16: x_dtype");

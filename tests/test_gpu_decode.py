@@ -112,8 +112,9 @@ def test_router_ties_and_errors(hip):
 # ---- dense FP8 GEMV ----------------------------------------------------------------
 
 @pytest.mark.parametrize("layout", [0, 1, 2])
-@pytest.mark.parametrize("T,N,K", [(1, 4096, 4096), (1, 300, 10240), (2, 640, 2560), (3, 2560, 640), (4, 512, 2560),
-                                   (8, 1000, 1536), (13, 320, 4096), (16, 640, 2560)])
+@pytest.mark.parametrize("T,N,K", [(1, 4096, 4096), (3, 4100, 1040), (1, 300, 10240), (2, 640, 2560),
+                                   (3, 2560, 640), (4, 512, 2560), (8, 1000, 1536), (13, 320, 4096),
+                                   (16, 640, 2560)])
 def test_gemv_fp8_parity(hip, layout, T, N, K):
     import torch
 
