@@ -3,20 +3,22 @@
 // tokens ([page_size, Hkv, D] each, token j in physical page page_table[j / page_size]).
 //
 //  * Block (b, g) takes keys [512 b, 512 b + 512) of KV head g; each of its 4 waves 128
-//    keys, in tiles of 16 (one MFMA tile, inside one page). K and V of a tile stream once
-//    for all G query heads; the next tile's loads are in flight while the current one
-//    is reduced.
+//    keys, as pairs of 16-key tiles (a tile is one MFMA tile, inside one page). K and V
+//    of a tile stream once for all G query heads; the next pair's loads are in flight
+//    while the current one is reduced.
 //  * Scores S^T = K . Q^T on bf16 MFMA (v_mfma_f32_16x16x32_bf16; products exact, fp32
 //    accumulate): keys are the M side, so K loads need head_dim contiguous per lane
 //    (the layout in memory) and each lane ends with 4 keys of one head, which keeps the
 //    online-softmax reductions to two lane swaps. fp32 q enters as an exact 3-term bf16
 //    split (hi + mid + lo).
-//  * P . V in fp32 on the VALU: V rows load coalesced (16 lanes x 8 head_dim columns
-//    per row) and P reaches every lane through LDS.
-//  * A block merges its waves' (max, sum, acc) in LDS into one partial; the partials of
-//    a KV head merge in a tree of fan-in 8 (the last block of each group, found by a
-//    ticket that its user resets, merges the group's partials rescaled by their maxima),
-//    and the block that merges the top level writes out = acc / sum.
+//  * P . V on the same bf16 matrix cores, 32 keys (a pair) per MFMA: P enters as an exact
+//    3-term bf16 split, so products are exact and accumulate in fp32; V rows load
+//    coalesced (16 lanes x 8 head_dim columns a key) and reach the B-operand layout
+//    through a per-wave transposed LDS area. (A VALU P . V made the kernel issue-bound:
+//    about 650 vector instructions per 16-key tile.)
+//  * A block merges its waves' (max, sum, acc) in LDS into one partial; a second kernel
+//    merges a KV head's partials weighted by their maxima against the global one and
+//    writes out = acc / sum (a KV head with one block writes its result directly).
 // The arithmetic follows the reference's fp32 online softmax
 // (crates/oominf-cuda/kernels/attention.cu:419-553): dot products, exp and accumulation
 // in fp32; only the summation order differs.
@@ -30,7 +32,7 @@ constexpr int AW = 4;           // waves per block
 constexpr int AKW = 128;        // keys per wave
 constexpr int AKB = AW * AKW;   // keys per block
 constexpr int AG = 8;           // query heads per KV head (at most)
-constexpr int A_TICKET_STRIDE = 64;
+constexpr int A_MAXB = 4096;    // blocks a KV head (2 Mi keys): the merge's weights sit in LDS
 constexpr int A_BUF_FLAGS = 0x00020000;
 constexpr int A_OOB = 0x7ffffff0;
 constexpr int A_BUF_SC1 = 16;
@@ -44,12 +46,9 @@ struct AttnArgs {
     const uint16_t* vp;
     const int32_t* pt;
     int n_pages, page_size, kv_len, Hkv, G, bph;
-    int pslots, tslots;  // merge-tree partial slots and tickets per KV head
     float scale;
     void* out;
-    float* part;        // [Hkv][pslots][2 AG + AG D]: max, sum, acc per block, then per merge group
-    uint32_t* tickets;  // [Hkv][tslots], A_TICKET_STRIDE apart
-    uint32_t* status;
+    float* part;        // [Hkv][bph][2 AG + AG D]: each block's max and sum per head, then its acc [AG][D]
 };
 
 __device__ __forceinline__ uint4 a_ld16(__amdgpu_buffer_rsrc_t r, int off) {
@@ -65,130 +64,110 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint16_t* base
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p), (short)0, ok ? page_bytes : 0, A_BUF_FLAGS);
 }
 
-// One 16-key tile (inside one page): K in the MFMA A layout (lane l holds key l % 16,
-// head_dim 32 s + 8 (l / 16) .. + 8) and V for the VALU (lane l holds head_dim
-// 8 (l % DL) .. + 8 of key KPI q + l / DL). Keys past kv_len, and tiles whose page
-// index is out of range, read zeros.
+// Loads of one 16-key tile (inside one page), keys past kv_len and tiles whose page
+// index is out of range reading zeros. K in the MFMA A layout of the scores: lane l holds
+// key l % 16, head_dim 32 s + 8 (l / 16) .. + 8. V: lane l holds head_dim 8 (l % 16) .. + 8
+// of key 4 q + l / 16 (q < 4).
 template <int D>
-struct KvTile {
-    uint4 k[D / 32];
-    uint4 v[16 * D / 512];
-};
-
-template <int D>
-__device__ __forceinline__ void kv_load(const AttnArgs& a, int g, int key0, int page, int lane, KvTile<D>& t) {
-    constexpr int DL = D / 8, KPI = 64 / DL, NT = 16 / KPI;
+__device__ __forceinline__ void k_load(const AttnArgs& a, int g, int key0, int page, int lane, uint4 (&k)[D / 32]) {
     const int ps = a.page_size, page_bytes = ps * a.Hkv * D * 2, row_bytes = a.Hkv * D * 2;
     if (key0 >= a.kv_len) page = -1;
     const __amdgpu_buffer_rsrc_t kr = page_rsrc(a.kp, page, a.n_pages, page_bytes);
+    const int slot0 = key0 % ps;
+    const int kbase = key0 + (lane & 15) < a.kv_len ? (slot0 + (lane & 15)) * row_bytes + g * D * 2 + 16 * (lane >> 4)
+                                                    : A_OOB;
+#pragma unroll
+    for (int s = 0; s < D / 32; s++) k[s] = a_ld16(kr, kbase == A_OOB ? A_OOB : kbase + 64 * s);
+}
+
+template <int D>
+__device__ __forceinline__ void v_load(const AttnArgs& a, int g, int key0, int page, int lane, uint4 (&v)[4]) {
+    static_assert(D == 128, "V loads: 16 lanes of 8 head_dim columns a key");
+    const int ps = a.page_size, page_bytes = ps * a.Hkv * D * 2, row_bytes = a.Hkv * D * 2;
+    if (key0 >= a.kv_len) page = -1;
     const __amdgpu_buffer_rsrc_t vr = page_rsrc(a.vp, page, a.n_pages, page_bytes);
     const int slot0 = key0 % ps;
-    const int kkey = key0 + (lane & 15);
-    const int kbase = kkey < a.kv_len ? (slot0 + (lane & 15)) * row_bytes + g * D * 2 + 16 * (lane >> 4) : A_OOB;
 #pragma unroll
-    for (int s = 0; s < D / 32; s++) t.k[s] = a_ld16(kr, kbase == A_OOB ? A_OOB : kbase + 64 * s);
-#pragma unroll
-    for (int q = 0; q < NT; q++) {
-        const int kk = KPI * q + lane / DL;
-        const int off = key0 + kk < a.kv_len ? (slot0 + kk) * row_bytes + g * D * 2 + (lane % DL) * 16 : A_OOB;
-        t.v[q] = a_ld16(vr, off);
+    for (int q = 0; q < 4; q++) {
+        const int kk = 4 * q + (lane >> 4);
+        v[q] = a_ld16(vr, key0 + kk < a.kv_len ? (slot0 + kk) * row_bytes + g * D * 2 + (lane & 15) * 16 : A_OOB);
     }
 }
 
-// One 16-key tile: scores, online softmax update of (m, l) for head lane % 16, and
-// acc += P . V. plds / clds are this wave's LDS rows.
+// P . V of a 32-key pair of tiles runs on the bf16 matrix cores: O[head, dim] +=
+// sum_kappa P[head, kappa] V[kappa, dim] (v_mfma_f32_16x16x32_bf16, heads on M, 16 dims
+// on N, the pair's 32 keys on K). Lane l supplies K values 8 (l / 16) .. + 8, and both
+// operands order a lane group's 8 keys the same way: position 2 e + t = key 4 (l / 16) + e
+// of tile t. That is where the scores leave P (lane l: keys 4 (l / 16) + e of head l % 16),
+// so the A operand is built in registers; V reaches that order through a per-wave LDS
+// area, written transposed: word e of the 16-byte entry (group q, dim d) holds the bf16
+// pair (tile 0, tile 1) of key 4 q + e, at word q VT_GROUP + 4 d + 4 (d / 8) + e. The pad
+// of 4 words every 8 dims spreads a write instruction's 64 words (16 dims 8 apart x 4
+// keys) over all 64 banks; a B-operand read (16 consecutive dims, 16 bytes each) takes
+// 8 lanes' contiguous 128 bytes at a time.
+constexpr int VT_GROUP = 128 * 4 + 16 * 4;  // words of one key group (4 keys of both tiles, 128 dims)
+constexpr int VT_WORDS = 4 * VT_GROUP;      // one wave's area
+
+__device__ __forceinline__ int vt_word(int q, int d, int e) { return q * VT_GROUP + 4 * d + 4 * (d >> 3) + e; }
+
+// The pair's V (tile t's loads in v[t]) into the wave's transposed area.
+__device__ __forceinline__ void v_to_lds(const uint4 (&v)[2][4], uint32_t* vt, int lane) {
+    const int e = lane >> 4, dl = lane & 15;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t w0[4] = {v[0][q].x, v[0][q].y, v[0][q].z, v[0][q].w};
+        const uint32_t w1[4] = {v[1][q].x, v[1][q].y, v[1][q].z, v[1][q].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int d = 8 * dl + 2 * i;  // word i: dims d (low half) and d + 1 (high half)
+            vt[vt_word(q, d, e)] = __builtin_amdgcn_perm(w1[i], w0[i], 0x05040100u);
+            vt[vt_word(q, d + 1, e)] = __builtin_amdgcn_perm(w1[i], w0[i], 0x07060302u);
+        }
+    }
+}
+
+// Scores of one 16-key tile for 16 (G real) heads, scaled and masked: lane l holds keys
+// key0 + 4 (l / 16) + e of head l % 16.
 template <int D, int NQ>
-__device__ __forceinline__ void attn_tile(const AttnArgs& a, const KvTile<D>& cur, int key0, int lane,
-                                          const abf16x8 (&qb)[NQ][D / 32], float& m, float& l, float (&acc)[AG][8],
-                                          float (*plds)[AG], float* clds) {
-    constexpr int NS = D / 32, DL = D / 8, KPI = 64 / DL, NT = 16 / KPI;
-    // ---- scores of 16 keys for 16 (G real) heads: lane l holds keys 4 (l / 16) + e of head l % 16 ----
-    float s[4];
-    {
-        af32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+__device__ __forceinline__ void tile_scores(const AttnArgs& a, const uint4 (&k)[D / 32],
+                                            const abf16x8 (&qb)[NQ][D / 32], int key0, int lane, float (&s)[4]) {
+    af32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int term = 0; term < NQ; term++)
+    for (int term = 0; term < NQ; term++)
 #pragma unroll
-            for (int ss = 0; ss < NS; ss++)
-                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(abf16x8, cur.k[ss]), qb[term][ss], c, 0,
-                                                            0, 0);
+        for (int ss = 0; ss < D / 32; ss++)
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(abf16x8, k[ss]), qb[term][ss], c, 0, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int key = key0 + 4 * (lane >> 4) + e;
-            s[e] = key < a.kv_len ? c[e] * a.scale : -INFINITY;
-        }
-    }
-    // ---- online softmax per head (lane % 16) over the tile's 16 keys ----
-    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-        tmax = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-        const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-        tmax = fmaxf(__uint_as_float(r2[0]), __uint_as_float(r2[1]));
-    }
-    const float mn = fmaxf(m, tmax);  // finite: the tile holds a visible key
-    const float corr = expf(m - mn);  // 0 while m is -inf
-    float p[4], tsum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        p[e] = expf(s[e] - mn);
-        tsum += p[e];
-    }
-    {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(tsum), __float_as_uint(tsum), false, false);
-        tsum = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-        const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(tsum), __float_as_uint(tsum), false, false);
-        tsum = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
-    }
-    l = l * corr + tsum;
-    m = mn;
-    // P and corr to this wave's LDS, then P . V
-    if ((lane & 15) < AG) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) plds[4 * (lane >> 4) + e][lane & 15] = p[e];
-        if (lane < AG) clds[lane] = corr;
-    }
-    wave_lds_order();
-    float cr[AG];
-#pragma unroll
-    for (int h = 0; h < AG; h++) cr[h] = clds[h];
-#pragma unroll
-    for (int h = 0; h < AG; h++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[h][e] *= cr[h];
-#pragma unroll
-    for (int q = 0; q < NT; q++) {
-        const int kk = KPI * q + lane / DL;
-        float pv[AG];
-#pragma unroll
-        for (int h = 0; h < AG; h++) pv[h] = plds[kk][h];
-        const uint32_t w[4] = {cur.v[q].x, cur.v[q].y, cur.v[q].z, cur.v[q].w};
-        float vf[8];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            vf[2 * e] = __uint_as_float(w[e] << 16);
-            vf[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-        }
-#pragma unroll
-        for (int h = 0; h < AG; h++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[h][e] = fmaf(pv[h], vf[e], acc[h][e]);
-    }
-    wave_lds_order();  // this tile's P reads are done before the next tile's writes
+    for (int e = 0; e < 4; e++) s[e] = key0 + 4 * (lane >> 4) + e < a.kv_len ? c[e] * a.scale : -INFINITY;
+}
+
+// max / sum over the four lane groups (the keys of one head)
+__device__ __forceinline__ float group_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r2[0]), __uint_as_float(r2[1]));
+}
+__device__ __forceinline__ float group_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
 }
 
 template <int D, int QDT, int ODT>
-__global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
-    constexpr int NS = D / 32, DL = D / 8, KPI = 64 / DL;
-    __shared__ float plds[AW][16][AG];
-    __shared__ float clds[AW][AG];
+__global__ void __launch_bounds__(AW * 64) attn_decode_kernel(AttnArgs a) {
+    constexpr int NS = D / 32, NP = AKW / 32, NB = D / 16;
+    static_assert(D == 128 && AW * VT_WORDS >= AW * AG * D, "the V areas hold the block merge afterwards");
+    // the waves' transposed V areas; after the key loop, the block merge's accumulators
+    __shared__ __align__(16) uint32_t vts[AW * VT_WORDS];
+    __shared__ __align__(16) float clds[AW][16];
     __shared__ float mlds[AW][AG], llds[AW][AG];
-    __shared__ float alds[AW][AG][D];
-    __shared__ uint32_t last;
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = blockIdx.y, b = blockIdx.x, G = a.G;
     const int kbase = b * AKB + wave * AKW;
+    uint32_t* const vt = vts + wave * VT_WORDS;
     // Q^T as the MFMA B operand: column = head l % 16 (zero past G), head_dim 32 s + 8 (l / 16) .. + 8
     constexpr int NQ = QDT == OOM_F32 ? 3 : 1;
     abf16x8 qb[NQ][NS];
@@ -225,58 +204,108 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
             }
         }
     }
-    // running softmax state of head lane % 16 (identical in the four lane groups) and
-    // this lane's accumulator acc[h][e] = head h, head_dim 8 (lane % DL) + e, over the
-    // keys this lane group sees
+    // running softmax state of head lane % 16 (identical in the four lane groups) and the
+    // output accumulator in the MFMA C layout: o[nb][e] = head 4 (l / 16) + e, dim 16 nb + l % 16
     float m = -INFINITY, l = 0.0f;
-    float acc[AG][8];
+    af32x4 o[NB];
 #pragma unroll
-    for (int h = 0; h < AG; h++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
-    constexpr int ntile = AKW / 16;
+    for (int nb = 0; nb < NB; nb++) o[nb] = af32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // the page of each of this wave's tiles, lane i holding tile i's (one load up front)
     const int pkey = kbase + 16 * lane;
-    const int pages = lane < ntile && pkey < a.kv_len ? a.pt[pkey / a.page_size] : -1;
-    // two tile buffers, fully unrolled (each buffer index is a constant): the next
-    // tile's loads are in flight while the current one is reduced
-    KvTile<D> tb[2];
-    kv_load<D>(a, g, kbase, __builtin_amdgcn_readlane(pages, 0), lane, tb[0]);
+    const int pages = lane < 2 * NP && pkey < a.kv_len ? a.pt[pkey / a.page_size] : -1;
+    // software pipeline over pairs: pair j + 1's V loads go out once pair j's V is in LDS,
+    // its K loads once pair j's scores are done, so about one pair is always in flight
+    uint4 kr[2][NS], vr[2][4];
 #pragma unroll
-    for (int i = 0; i < ntile; i++) {
-        const int k0 = kbase + 16 * i;
-        if (k0 >= a.kv_len) break;  // wave-uniform
-        kv_load<D>(a, g, i + 1 < ntile ? k0 + 16 : a.kv_len, __builtin_amdgcn_readlane(pages, (i + 1) & 63), lane,
-                   tb[(i + 1) % 2]);
-        attn_tile<D, NQ>(a, tb[i % 2], k0, lane, qb, m, l, acc, plds[wave], clds[wave]);
-    }
-    // ---- the lane groups' accumulators (same columns, different keys) add up ----
+    for (int t = 0; t < 2; t++) v_load<D>(a, g, kbase + 16 * t, __builtin_amdgcn_readlane(pages, t), lane, vr[t]);
 #pragma unroll
-    for (int h = 0; h < AG; h++)
+    for (int t = 0; t < 2; t++) k_load<D>(a, g, kbase + 16 * t, __builtin_amdgcn_readlane(pages, t), lane, kr[t]);
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float v = acc[h][e];
-            if constexpr (KPI >= 4) {
-                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-                v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    for (int j = 0; j < NP; j++) {
+        const int key0 = kbase + 32 * j;
+        if (key0 >= a.kv_len) break;  // wave-uniform
+        const int nk0 = j + 1 < NP ? key0 + 32 : a.kv_len;  // the next pair (none: every load reads zeros)
+        v_to_lds(vr, vt, lane);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            v_load<D>(a, g, nk0 + 16 * t, __builtin_amdgcn_readlane(pages, (2 * j + 2 + t) & 63), lane, vr[t]);
+        float s[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; t++) tile_scores<D, NQ>(a, kr[t], qb, key0 + 16 * t, lane, s[t]);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            k_load<D>(a, g, nk0 + 16 * t, __builtin_amdgcn_readlane(pages, (2 * j + 2 + t) & 63), lane, kr[t]);
+        // ---- online softmax of head lane % 16 over the pair's 32 keys ----
+        float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                           fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+        tmax = group_max(tmax);
+        const float mn = fmaxf(m, tmax);  // finite: the pair's first key is visible
+        const float corr = expf(m - mn);  // 0 while m is -inf
+        float p[2][4], tsum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                p[t][e] = expf(s[t][e] - mn);
+                tsum += p[t][e];
             }
-            const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-            acc[h][e] = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
+        l = l * corr + group_sum(tsum);
+        m = mn;
+        // ---- the accumulator rows (heads 4 (l / 16) + e) take their heads' corr ----
+        if (lane < 16) clds[wave][lane] = corr;
+        wave_lds_order();  // also orders this pair's V writes before the operand reads below
+        const float4 cr = *reinterpret_cast<const float4*>(&clds[wave][4 * (lane >> 4)]);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            o[nb][0] *= cr.x;
+            o[nb][1] *= cr.y;
+            o[nb][2] *= cr.z;
+            o[nb][3] *= cr.w;
         }
+        // ---- P as three bf16 terms (hi + mid + lo == p exactly), A operand order 2 e + t ----
+        abf16x8 pa[3];
+#pragma unroll
+        for (int term = 0; term < 3; term++) {
+            typedef __bf16 abf16x2 __attribute__((ext_vector_type(2)));
+            typedef float af32x2 __attribute__((ext_vector_type(2)));
+            uint32_t wv[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const af32x2 pf = {p[0][e], p[1][e]};
+                const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf, abf16x2));  // RNE
+                wv[e] = w;
+                p[0][e] -= __uint_as_float(w << 16);  // exact: the remainder of a round to nearest
+                p[1][e] -= __uint_as_float(w & 0xffff0000u);
+            }
+            pa[term] = __builtin_bit_cast(abf16x8, make_uint4(wv[0], wv[1], wv[2], wv[3]));
+        }
+        // ---- O += P . V, 16 dims at a time ----
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            const uint4 vb = *reinterpret_cast<const uint4*>(vt + vt_word(lane >> 4, 16 * nb + (lane & 15), 0));
+            const abf16x8 vop = __builtin_bit_cast(abf16x8, vb);
+#pragma unroll
+            for (int term = 0; term < 3; term++)
+                o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[term], vop, o[nb], 0, 0, 0);
+        }
+        wave_lds_order();  // this pair's reads of the V area are done before the next pair's writes
+    }
+    __syncthreads();  // every wave is done with its V area: it now holds the block merge
+    float (*alds)[AG][D] = reinterpret_cast<float (*)[AG][D]>(vts);
     // ---- block merge in LDS ----
-    if (lane < DL)
+    if (4 * (lane >> 4) < AG)
 #pragma unroll
-        for (int h = 0; h < AG; h++)
+        for (int nb = 0; nb < NB; nb++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) alds[wave][h][8 * lane + e] = acc[h][e];
+            for (int e = 0; e < 4; e++) alds[wave][4 * (lane >> 4) + e][16 * nb + (lane & 15)] = o[nb][e];
     if (lane < AG) {
         mlds[wave][lane] = m;
         llds[wave][lane] = l;
     }
     __syncthreads();
     // thread: head h = tid / (256 / AG), 4 columns
-    constexpr int TPH = 256 / AG, CPT = D / TPH;  // threads per head, columns per thread
-    static_assert(CPT >= 1 && CPT <= 8, "columns per thread");
+    constexpr int TPH = AW * 64 / AG, CPT = D / TPH;  // threads per head, columns per thread
+    static_assert(CPT == 4, "one 16-byte store per thread");
     const int h = tid / TPH, c0 = (tid % TPH) * CPT;
     float M = -INFINITY;
 #pragma unroll
@@ -291,117 +320,116 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < CPT; j++) A[j] = fmaf(alds[w][h][c0 + j], f, A[j]);
     }
-    static_assert(CPT == 4, "one 16-byte store per thread");
-    // ---- partials merge in a tree of fan-in AF: a block stores its (M, L, A) at its
-    // slot of the level and takes its group's ticket; the group's last block loads the
-    // group's partials (all loads in flight together), merges them in slot order and
-    // goes up a level with the group's index; the block that merges the last level
-    // writes out = A / L ----
-    constexpr int PSZ = 2 * AG + AG * D, AF = 8;
-    float* const hpart = a.part + (size_t)g * a.pslots * PSZ;
-    uint32_t* const htick = a.tickets + (size_t)g * a.tslots * A_TICKET_STRIDE;
-    int n = a.bph, idx = b, poff = 0, toff = 0;
-    while (n > 1) {
-        float* mine = hpart + (size_t)(poff + idx) * PSZ;
-        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(mine, (short)0, PSZ * 4, A_BUF_FLAGS);
-        if (tid % TPH == 0) {
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), wr, h * 4, 0, A_BUF_SC1);
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(L), wr, (AG + h) * 4, 0, A_BUF_SC1);
-        }
-        {
-            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-            const u32x4 v = {__float_as_uint(A[0]), __float_as_uint(A[1]), __float_as_uint(A[2]), __float_as_uint(A[3])};
-            __builtin_amdgcn_raw_buffer_store_b128(v, wr, (2 * AG + h * D + c0) * 4, 0, A_BUF_SC1);
-        }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);  // the stores are complete before the ticket
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __syncthreads();
-        const int grp = idx / AF, nin = min(AF, n - grp * AF);
-        if (tid == 0) {
-            uint32_t* t = htick + (size_t)(toff + grp) * A_TICKET_STRIDE;
-            const uint32_t old = __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = old == (uint32_t)nin - 1;
-            if (last) __hip_atomic_store(t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!last) return;
-        const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-            hpart + (size_t)(poff + grp * AF) * PSZ, (short)0, nin * PSZ * 4, A_BUF_FLAGS);
-        float bm[AF], bl[AF], bv[AF][CPT];
+    if (a.bph == 1) {  // the KV head's only block: its partial is the result
+        if (h < G) {
+            const size_t oi = (size_t)(g * G + h) * D + c0;
 #pragma unroll
-        for (int q = 0; q < AF; q++) {
-            const bool ok = q < nin;
-            const int base = q * PSZ * 4;
-            const float mraw =
-                __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, ok ? base + h * 4 : A_OOB, 0, A_BUF_SC1));
-            bm[q] = ok ? mraw : -INFINITY;
-            bl[q] = __uint_as_float(
-                __builtin_amdgcn_raw_buffer_load_b32(pr, ok ? base + (AG + h) * 4 : A_OOB, 0, A_BUF_SC1));
-            const auto v =
-                __builtin_amdgcn_raw_buffer_load_b128(pr, ok ? base + (2 * AG + h * D + c0) * 4 : A_OOB, 0, A_BUF_SC1);
-#pragma unroll
-            for (int j = 0; j < CPT; j++) bv[q][j] = __uint_as_float(v[j]);
+            for (int j = 0; j < CPT; j++) store_out<ODT>(a.out, oi + j, A[j] / L);
         }
-        M = -INFINITY;
-        L = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPT; j++) A[j] = 0.0f;
-#pragma unroll
-        for (int q = 0; q < AF; q++) {
-            if (bm[q] == -INFINITY) continue;
-            const float nm = fmaxf(M, bm[q]);
-            const float fo = expf(M - nm), fb = expf(bm[q] - nm);
-            L = L * fo + bl[q] * fb;
-#pragma unroll
-            for (int j = 0; j < CPT; j++) A[j] = A[j] * fo + bv[q][j] * fb;
-            M = nm;
-        }
-        poff += n;
-        toff += (n + AF - 1) / AF;
-        n = (n + AF - 1) / AF;
-        idx = grp;
+        return;
     }
-    if (h < G) {
-        const size_t o = (size_t)(g * G + h) * D + c0;
-#pragma unroll
-        for (int j = 0; j < CPT; j++) store_out<ODT>(a.out, o + j, A[j] / L);
+    // ---- the block's partial for attn_merge_kernel (plain stores: the kernel boundary
+    // publishes them) ----
+    float* mine = a.part + ((size_t)g * a.bph + b) * (2 * AG + AG * D);
+    if (tid % TPH == 0) {
+        mine[h] = M;
+        mine[AG + h] = L;
     }
+    *reinterpret_cast<float4*>(mine + 2 * AG + h * D + c0) = make_float4(A[0], A[1], A[2], A[3]);
+}
+
+// The merge of a KV head's block partials, one block of 64 per (KV head g, query head h):
+// the global max over the partials, each partial's weight exp(M_b - M) (in LDS), the sum,
+// and lane l's columns 2 l, 2 l + 1 of sum_b w_b acc_b in block order; out = acc / sum. A
+// second kernel, not a merge inside the first: a merge there puts three device-scope round
+// trips (stores acknowledged, a ticket, the partials' loads) on the last block's path,
+// which cost more than a kernel boundary.
+template <int D, int ODT>
+__global__ void __launch_bounds__(64) attn_merge_kernel(AttnArgs a) {
+    static_assert(D == 128, "two columns a lane");
+    constexpr int PSZ = 2 * AG + AG * D, CH = 64;  // partials a lane loads at once
+    __shared__ float wts[A_MAXB];
+    const int lane = threadIdx.x, g = blockIdx.x, h = blockIdx.y, n = a.bph, c0 = 2 * lane;
+    const float* hp = a.part + (size_t)g * n * PSZ;
+    float M = -INFINITY, L = 0.0f, A0 = 0.0f, A1 = 0.0f;
+    if (n <= CH) {
+        // up to 64 partials (32 Ki keys): every load of the merge in flight at once
+        const bool ok = lane < n;
+        const float mq = ok ? hp[(size_t)lane * PSZ + h] : -INFINITY;
+        const float lq = ok ? hp[(size_t)lane * PSZ + AG + h] : 0.0f;
+        float2 v[CH];
+#pragma unroll
+        for (int j = 0; j < CH; j++)
+            v[j] = j < n ? *reinterpret_cast<const float2*>(hp + (size_t)j * PSZ + 2 * AG + h * D + c0)
+                         : make_float2(0.0f, 0.0f);
+        M = wave_max(mq);  // finite: every block holds a visible key
+        const float w = mq == -INFINITY ? 0.0f : expf(mq - M);
+        L = wave_sum(lq * w);
+        wts[lane] = w;
+        wave_lds_order();
+#pragma unroll
+        for (int j = 0; j < CH; j++) {  // past n: zero columns and weights
+            A0 = fmaf(v[j].x, wts[j], A0);
+            A1 = fmaf(v[j].y, wts[j], A1);
+        }
+    } else {
+        for (int q = lane; q < n; q += 64) M = fmaxf(M, hp[(size_t)q * PSZ + h]);
+        M = wave_max(M);
+        for (int q0 = 0; q0 < n; q0 += 64) {
+            const int q = q0 + lane;
+            float w = 0.0f, lq = 0.0f;
+            if (q < n) {
+                const float mq = hp[(size_t)q * PSZ + h];
+                w = mq == -INFINITY ? 0.0f : expf(mq - M);
+                lq = hp[(size_t)q * PSZ + AG + h];
+                wts[q] = w;
+            }
+            L += wave_sum(lq * w);
+        }
+        wave_lds_order();
+        for (int q0 = 0; q0 < n; q0 += CH) {
+            float2 v[CH];
+#pragma unroll
+            for (int j = 0; j < CH; j++)
+                v[j] = q0 + j < n ? *reinterpret_cast<const float2*>(hp + (size_t)(q0 + j) * PSZ + 2 * AG + h * D + c0)
+                                  : make_float2(0.0f, 0.0f);
+#pragma unroll
+            for (int j = 0; j < CH; j++) {
+                if (q0 + j >= n) break;
+                const float w = wts[q0 + j];
+                A0 = fmaf(v[j].x, w, A0);
+                A1 = fmaf(v[j].y, w, A1);
+            }
+        }
+    }
+    const size_t oi = (size_t)(g * a.G + h) * D + c0;
+    store_out<ODT>(a.out, oi, A0 / L);
+    store_out<ODT>(a.out, oi + 1, A1 / L);
 }
 
 // ---- host side -------------------------------------------------------------------------
 
 static size_t a_al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-// Partial slots and tickets per KV head of the merge tree over bph block partials.
-static void merge_tree_slots(int bph, int& pslots, int& tslots) {
-    pslots = 0;
-    tslots = 0;
-    for (int n = bph; n > 1; n = (n + 7) / 8) {
-        pslots += n;
-        tslots += (n + 7) / 8;
-    }
-}
-
 struct AttnWs {
-    size_t part, tickets, status, total;
-    int pslots, tslots;
+    size_t part, total;
 };
 
 static AttnWs attn_ws(int kv_len, int kv_heads, int d) {
     AttnWs w;
     const int bph = (int)cdiv(kv_len, AKB);
-    merge_tree_slots(bph, w.pslots, w.tslots);
     w.part = 0;
-    w.tickets = a_al256((size_t)kv_heads * w.pslots * (2 * AG + AG * (size_t)d) * sizeof(float));
-    w.status = w.tickets + (size_t)kv_heads * std::max(w.tslots, 1) * A_TICKET_STRIDE * sizeof(uint32_t);
-    w.total = w.status + 256;
+    w.total = a_al256((size_t)kv_heads * (bph > 1 ? bph : 1) * (2 * AG + AG * (size_t)d) * sizeof(float));
     return w;
 }
 
 template <int D, int QDT, int ODT>
 static int launch_attn_t(const AttnArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL((attn_decode_kernel<D, QDT, ODT>), dim3(a.bph, a.Hkv), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_decode_kernel<D, QDT, ODT>), dim3(a.bph, a.Hkv), dim3(AW * 64), 0, st, a);
+    if (a.bph > 1) {
+        if (int rc = launched("oom_attn_decode_paged")) return rc;
+        hipLaunchKernelGGL((attn_merge_kernel<D, ODT>), dim3(a.Hkv, a.G), dim3(64), 0, st, a);
+    }
     return launched("oom_attn_decode_paged");
 }
 
@@ -422,6 +450,7 @@ extern "C" int oom_attn_decode_paged(const void* q, int q_dtype, const uint16_t*
                 "oom_attn_decode_paged: heads must be a multiple of kv_heads, at most 8 query heads per KV head");
     OOM_REQUIRE(page_size >= 16 && page_size % 16 == 0, "oom_attn_decode_paged: page_size must be a multiple of 16");
     OOM_REQUIRE(kv_len >= 1 && n_pages >= 1, "oom_attn_decode_paged: kv_len and n_pages must be >= 1");
+    OOM_REQUIRE(kv_len <= A_MAXB * AKB, "oom_attn_decode_paged: kv_len above 2 Mi keys");
     OOM_REQUIRE((int64_t)page_size * kv_heads * d * 2 < (1ll << 31), "oom_attn_decode_paged: page too large");
     OOM_REQUIRE(q_dtype == OOM_F32 || q_dtype == OOM_BF16, "oom_attn_decode_paged: q_dtype");
     OOM_REQUIRE(out_dtype == OOM_F32 || out_dtype == OOM_BF16, "oom_attn_decode_paged: out_dtype");
@@ -444,13 +473,9 @@ extern "C" int oom_attn_decode_paged(const void* q, int q_dtype, const uint16_t*
     a.Hkv = kv_heads;
     a.G = heads / kv_heads;
     a.bph = (int)cdiv(kv_len, AKB);
-    a.pslots = w.pslots;
-    a.tslots = w.tslots;
     a.scale = scale;
     a.out = out;
     a.part = reinterpret_cast<float*>(base + w.part);
-    a.tickets = reinterpret_cast<uint32_t*>(base + w.tickets);
-    a.status = reinterpret_cast<uint32_t*>(base + w.status);
     hipStream_t st = as_stream(stream);
     if (q_dtype == OOM_BF16)
         return out_dtype == OOM_BF16 ? launch_attn_t<128, OOM_BF16, OOM_BF16>(a, st)

@@ -57,6 +57,8 @@ CASES = [
     (4, 4, 128, 300, 16, "f32"),      # one query head per KV head
     (24, 4, 128, 2100, 16, "bf16"),   # six query heads per KV head
     (8, 2, 128, 4097, 64, "f32"),
+    (8, 1, 128, 32769, 16, "f32"),    # 33 blocks: merge groups of 32 and 1, then a second level
+    (16, 2, 128, 70000, 16, "bf16"),  # 69 blocks: three groups, two levels
 ]
 
 
