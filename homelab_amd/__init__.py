@@ -17,6 +17,7 @@ OK = 0
 ERR_ARG, ERR_WORKSPACE, ERR_LAUNCH, ERR_KERNEL = -1, -2, -3, -4
 F32, BF16 = 0, 1
 SCALE_ROW, SCALE_1X128, SCALE_128X128 = 0, 1, 2
+EXPERT_EXACT, EXPERT_BF16 = 0, 1  # the prefill down projection's activation precision
 
 _lib = None
 
@@ -64,7 +65,7 @@ SIGNATURES = {
     "oom_quantize_rows_fp8": (I32, [P, I32, I64, I64, P, P, P]),
     "oom_moe_grouped_gemm_fp8": (I32, [P, P, P, I32, I32, P, P, I32, P, I64, I64, I64, I64, P]),
     "oom_moe_prefill_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
-    "oom_moe_prefill_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, P, P, P, I32, P, SZ, P]),
+    "oom_moe_prefill_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, I32, P, P, P, I32, P, SZ, P]),
     "oom_attn_decode_workspace_size": (SZ, [I32, I32, I32, I32]),
     "oom_attn_decode_paged": (I32, [P, I32, P, P, P, I32, I32, I32, I32, I32, I32, F, P, I32, P, SZ, P]),
     "oom_copy_queue_create": (I32, [P]),
@@ -341,10 +342,11 @@ def moe_prefill_fp8_workspace_size(T: int, E: int, k: int, geo: Fp8Record) -> in
     return int(lib().oom_moe_prefill_fp8_workspace_size(T, E, k, ctypes.byref(geo)))
 
 
-def moe_prefill_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, out, ws, stream=None) -> None:
+def moe_prefill_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, out, ws, stream=None,
+                    precision: int = EXPERT_EXACT) -> None:
     T, E = logits.shape
     check(lib().oom_moe_prefill_fp8(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k, ctypes.byref(geo),
-                                    _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
+                                    precision, _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
                                     ws.numel() * ws.element_size(), _stream(stream)))
 
 

@@ -1,8 +1,8 @@
 // Prefill MoE on gfx950: per-token e4m3 activation quantiser, FP8 x FP8 grouped GEMM on
 // the matrix cores (v_mfma_scale_f32_16x16x128_f8f6f4, unit block scales), the gate/up
-// pass with SwiGLU in its epilogue, the down pass over h kept at fp32 precision (two
-// bf16 terms on v_mfma_f32_16x16x32_bf16), and the whole prefill step (router, plan,
-// quantise, gate/up, down, combine) without a host round trip.
+// pass with SwiGLU in its epilogue, the down pass over h as one or two bf16 terms on
+// v_mfma_f32_16x16x32_bf16, and the whole prefill step (router, plan, quantise, gate/up,
+// down, combine) without a host round trip.
 //
 // Grouped GEMM: y[a, r] = xs(a) * sum_kb ws(r, kb) * sum_{c in kb} e4m3(xq[row(a), c]) *
 // e4m3(W[r, c]) for the assignments a of each expert (the semantics of
@@ -16,14 +16,15 @@
 //    assignment) and the weight rows in LDS (rows padded to 144 bytes), and the next
 //    step's global loads are in flight while the current step runs on the matrix cores.
 //  * Gate/up: both weight tiles share the activation tile; the epilogue forms
-//    h = silu(g) * u and writes it as two bf16 planes, hi = bf16(h) and lo = bf16(h - hi)
-//    (16 significant bits, relative error <= 2^-17): h is not quantised again, as the
-//    reference keeps it in fp32 for its exact tiled path (ExpertPrecision::Exact,
-//    crates/oominf-core/src/backend.rs:144-149; crates/oominf-cuda/kernels/moe.cu:166-335
-//    splits fp32 activations into exact bf16 terms the same way).
-//  * Down: A = the h planes, B = e4m3 weight rows converted exactly to bf16 in registers;
-//    both terms run on the bf16 matrix cores, fp32 accumulate, the weight's 128 x 128 block
-//    scale applied to each 128-column block sum.
+//    h = silu(g) * u and writes hi = bf16(h) and, for the exact precision, lo =
+//    bf16(h - hi) (16 significant bits, relative error <= 2^-17): h is not quantised
+//    again. The two precisions are the reference's (ExpertPrecision,
+//    crates/oominf-core/src/backend.rs:142-149): Bf16 rounds the activations to bf16 for
+//    one matrix-core pass, Exact keeps them fp32 (crates/oominf-cuda/kernels/moe.cu:166-335
+//    splits them into exact bf16 terms the same way).
+//  * Down: A = the h term planes, B = e4m3 weight rows converted exactly to bf16 in
+//    registers; every term runs on the bf16 matrix cores, fp32 accumulate, the weight's
+//    128 x 128 block scale applied to each 128-column block sum.
 #include <algorithm>
 
 #include "router.hpp"
@@ -417,22 +418,24 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
                     const uint16_t hi = f32_to_bf16(h);
                     const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
                     g.hh[(int64_t)a * g.N + n] = hi;
-                    g.hl[(int64_t)a * g.N + n] = f32_to_bf16(h - bf16_to_f32(hi));
+                    if (g.hl) g.hl[(int64_t)a * g.N + n] = f32_to_bf16(h - bf16_to_f32(hi));
                 }
             }
     }
 }
 
-// ---- down pass over h as two bf16 terms ----------------------------------------------
+// ---- down pass over h as one or two bf16 terms ----------------------------------------
 //
-// y[a, r] = sum_kb ws(r, kb) * sum_{c in kb} (hi[a, c] + lo[a, c]) * e4m3(W[r, c]) for the
+// y[a, r] = sum_kb ws(r, kb) * sum_{c in kb} (hi[a, c] (+ lo[a, c])) * e4m3(W[r, c]) for the
 // assignments a of each expert (W = the down weights [N = hidden, K = inter]); e4m3 -> bf16
 // is exact and bf16 products are exact in fp32, so each 128-column block sum is an fp32 sum
-// of exact products, scaled by the weight's block scale as it joins the accumulator.
+// of exact products, scaled by the weight's block scale as it joins the accumulator. One
+// term (hi = bf16(h)) is the reference's ExpertPrecision::Bf16 arithmetic; two (hi + lo,
+// 16 significant bits of the fp32 h) stand for ExpertPrecision::Exact.
 //
 // K steps of 64 through three LDS stages (direct-to-LDS loads, as the FP8 passes): a stage
-// holds the hi and lo tiles (128 assignments x 64 bf16 = 128 bytes a row, 8 chunks, the
-// FP8 tiles' chunk swizzle) and the weight tile (128 rows x 64 bytes, 4 chunks, chunk c of
+// holds the h term tiles (128 assignments x 64 bf16 = 128 bytes a row, 8 chunks, the FP8
+// tiles' chunk swizzle) and the weight tile (128 rows x 64 bytes, 4 chunks, chunk c of
 // row r at 4 r + (c ^ ((r >> 2) & 3)), so the 16 rows of an operand read, and any 8 of
 // them, land in distinct 16-byte bank groups). Lane l of a wave takes K values
 // 16 (l / 16) .. + 16 of the step for its row (A: assignment l % 16 of a 16-row subtile,
@@ -441,9 +444,12 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
 constexpr int GBK2 = 64;                       // K step of the down pass
 constexpr int D_HT = GBM * GBK2 * 2;           // bytes of one h term tile
 constexpr int D_WT = GBN * GBK2;               // bytes of the weight tile
-constexpr int D_SBYTES = 2 * D_HT + D_WT;      // one stage's operands
-constexpr int D_STOT = D_SBYTES + GTHREADS * 4;  // + the weight scale (64 words a wave)
-constexpr int D_LPS = 2 * 2 + 1 + 1;           // loads a wave issues per stage
+template <int TERMS>
+constexpr int d_sbytes() { return TERMS * D_HT + D_WT; }        // one stage's operands
+template <int TERMS>
+constexpr int d_stot() { return d_sbytes<TERMS>() + GTHREADS * 4; }  // + the weight scale (64 words a wave)
+template <int TERMS>
+constexpr int d_lps() { return 2 * TERMS + 1 + 1; }             // loads a wave issues per stage
 
 typedef __bf16 gbf16x8 __attribute__((ext_vector_type(8)));
 
@@ -451,45 +457,91 @@ __device__ __forceinline__ int wchunk_pos(int r, int c) { return 4 * r + (c ^ ((
 
 struct DSrc {
     __amdgpu_buffer_rsrc_t hr, wr, sr;
-    int ho[2], wo;  // step-0 byte offsets (the two terms share ho: hl is at hh + plane bytes)
+    int ho[2], wo;  // step-0 byte offsets (the terms share ho: hl is at hh + plane bytes)
     int hl_off;     // bytes from hh to hl
     int so;         // step-0 byte offset of this lane's weight scale (G_OOB: none)
 };
 
+template <int TERMS>
 __device__ __forceinline__ void d_issue(const DSrc& s, int kb, int nkb, uint8_t* sb, float* scw, int wave) {
     const bool ok = kb < nkb;
     const int k0 = kb * GBK2 * 2;  // bytes into an h row
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+    for (int t = 0; t < TERMS; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
             dma16(s.hr, sb + t * D_HT + (2 * wave + j) * 1024, ok ? s.ho[j] + t * s.hl_off + k0 : G_OOB);
-    dma16(s.wr, sb + 2 * D_HT + wave * 1024, ok ? s.wo + kb * GBK2 : G_OOB);
+    dma16(s.wr, sb + TERMS * D_HT + wave * 1024, ok ? s.wo + kb * GBK2 : G_OOB);
     dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
 }
 
-// One K step: blk += the step's products (both terms); every second step (and the last)
+// One step's operand reads from stage buffer sb, as one block of ds_reads the compiler
+// does not see as LDS loads: its wait-count pass cannot tell at the loop head which
+// stage buffer a direct-to-LDS load in flight writes, and would wait for all of them
+// (the next stages' too) before the first read. The step's own loads are complete by
+// then: each wave waited for its loads of the stage (wait_vm) before the block barrier.
+// A: h term t, row half hf of M subtile ms (ms: +2048 bytes, t: +D_HT); B: weight rows
+// of N subtile ns (+1024 bytes each); then this wave's weight block scale.
+template <int TERMS>
+__device__ __forceinline__ void d_reads(const uint8_t* sb, int wm, int wn, int wave, int lane,
+                                        uint4 (&ra)[2][TERMS][2], uint4 (&rb)[4], float& ws) {
+    typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
+    const uint32_t base = (uint32_t)(uintptr_t)(lds_cptr)sb;
+    const int g = lane >> 4, row = 32 * wm + (lane & 15), wrow = 64 * wn + (lane & 15);
+    const uint32_t a0 = base + 16 * chunk_pos(row, 2 * g), a1 = base + 16 * chunk_pos(row, 2 * g + 1);
+    const uint32_t bb = base + TERMS * D_HT + 16 * wchunk_pos(wrow, g);
+    const uint32_t sc = base + d_sbytes<TERMS>() + 4 * 64 * wave;
+    if constexpr (TERMS == 2) {
+        asm volatile(
+            "ds_read_b128 %0, %13\n\t"
+            "ds_read_b128 %1, %14\n\t"
+            "ds_read_b128 %2, %13 offset:2048\n\t"
+            "ds_read_b128 %3, %14 offset:2048\n\t"
+            "ds_read_b128 %4, %13 offset:16384\n\t"
+            "ds_read_b128 %5, %14 offset:16384\n\t"
+            "ds_read_b128 %6, %13 offset:18432\n\t"
+            "ds_read_b128 %7, %14 offset:18432\n\t"
+            "ds_read_b128 %8, %15\n\t"
+            "ds_read_b128 %9, %15 offset:1024\n\t"
+            "ds_read_b128 %10, %15 offset:2048\n\t"
+            "ds_read_b128 %11, %15 offset:3072\n\t"
+            "ds_read_b32 %12, %16\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=v"(ra[0][0][0]), "=v"(ra[0][0][1]), "=v"(ra[1][0][0]), "=v"(ra[1][0][1]), "=v"(ra[0][1][0]),
+              "=v"(ra[0][1][1]), "=v"(ra[1][1][0]), "=v"(ra[1][1][1]), "=v"(rb[0]), "=v"(rb[1]), "=v"(rb[2]),
+              "=v"(rb[3]), "=v"(ws)
+            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %9\n\t"
+            "ds_read_b128 %1, %10\n\t"
+            "ds_read_b128 %2, %9 offset:2048\n\t"
+            "ds_read_b128 %3, %10 offset:2048\n\t"
+            "ds_read_b128 %4, %11\n\t"
+            "ds_read_b128 %5, %11 offset:1024\n\t"
+            "ds_read_b128 %6, %11 offset:2048\n\t"
+            "ds_read_b128 %7, %11 offset:3072\n\t"
+            "ds_read_b32 %8, %12\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=v"(ra[0][0][0]), "=v"(ra[0][0][1]), "=v"(ra[1][0][0]), "=v"(ra[1][0][1]), "=v"(rb[0]), "=v"(rb[1]),
+              "=v"(rb[2]), "=v"(rb[3]), "=v"(ws)
+            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
+            : "memory");
+    }
+}
+
+// One K step: blk += the step's products (every term); every second step (and the last)
 // the 128-column block sum joins acc, scaled by the weight's block scale.
-__device__ __forceinline__ void d_step(const uint8_t* sb, const float* scw, int wm, int wn, int wave, int lane,
-                                       bool fold, gf32x4 (&blk)[2][4], float (&acc)[2][4][4]) {
-    const int g = lane >> 4;
-    gbf16x8 a[2][2][2];  // [ms][term][half]
-#pragma unroll
-    for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int row = 32 * wm + 16 * ms + (lane & 15);
-            const uint8_t* base = sb + t * D_HT;
-            const uint4 lo = *reinterpret_cast<const uint4*>(base + 16 * chunk_pos(row, 2 * g));
-            const uint4 hi = *reinterpret_cast<const uint4*>(base + 16 * chunk_pos(row, 2 * g + 1));
-            a[ms][t][0] = __builtin_bit_cast(gbf16x8, lo);
-            a[ms][t][1] = __builtin_bit_cast(gbf16x8, hi);
-        }
+template <int TERMS>
+__device__ __forceinline__ void d_step(const uint8_t* sb, int wm, int wn, int wave, int lane, bool fold,
+                                       gf32x4 (&blk)[2][4], float (&acc)[2][4][4]) {
+    uint4 ra[2][TERMS][2], rb[4];
+    float ws;
+    d_reads<TERMS>(sb, wm, wn, wave, lane, ra, rb, ws);
 #pragma unroll
     for (int ns = 0; ns < 4; ns++) {
-        const int row = 64 * wn + 16 * ns + (lane & 15);
-        const uint4 w = *reinterpret_cast<const uint4*>(sb + 2 * D_HT + 16 * wchunk_pos(row, g));
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        const uint32_t ww[4] = {rb[ns].x, rb[ns].y, rb[ns].z, rb[ns].w};
         gbf16x8 b[2];
 #pragma unroll
         for (int hf = 0; hf < 2; hf++)
@@ -507,11 +559,11 @@ __device__ __forceinline__ void d_step(const uint8_t* sb, const float* scw, int 
 #pragma unroll
             for (int hf = 0; hf < 2; hf++)
 #pragma unroll
-                for (int t = 0; t < 2; t++)
-                    blk[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ms][t][hf], b[hf], blk[ms][ns], 0, 0, 0);
+                for (int t = 0; t < TERMS; t++)
+                    blk[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gbf16x8, ra[ms][t][hf]),
+                                                                         b[hf], blk[ms][ns], 0, 0, 0);
     }
     if (fold) {
-        const float ws = scw[64 * wave];
 #pragma unroll
         for (int ms = 0; ms < 2; ms++)
 #pragma unroll
@@ -523,9 +575,15 @@ __device__ __forceinline__ void d_step(const uint8_t* sb, const float* scw, int 
     }
 }
 
-// Down pass: tiles from the device tile table in XCD runs, as grouped_gemm_kernel.
+// Down pass: tiles from the device tile table in XCD runs, as grouped_gemm_kernel, but with
+// the N-tile fastest: the blocks an XCD runs together take the N-tiles of one M-tile, so
+// that tile's h planes come into the XCD's L2 once and serve all of them. (M-tile fastest
+// re-fetched every M-tile's h from beyond the L2 for each N-tile: 3.2 GB a 2048-token step
+// with two terms.)
+template <int TERMS>
 __global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
-    __shared__ __align__(16) uint8_t sb0[D_STOT], sb1[D_STOT], sb2[D_STOT];
+    constexpr int STOT = d_stot<TERMS>(), SBYTES = d_sbytes<TERMS>();
+    __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT], sb2[STOT];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
@@ -534,15 +592,15 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
     if ((L >> 3) >= C) return;
     const int w = (L & 7) * C + (L >> 3);
     if (w >= W) return;
-    const int nt = w / MT, mt = w - nt * MT;
+    const int mt = w / NT, nt = w - mt * NT;
     const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBN;
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
     const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
     const int nkb = (int)(g.K / GBK2);
     DSrc src;
-    // the two h planes as one resource (hl follows hh by hl_off bytes)
-    src.hl_off = (int)((const uint8_t*)g.hl - (const uint8_t*)g.hh);
+    // the h planes as one resource (hl follows hh by hl_off bytes)
+    src.hl_off = TERMS == 2 ? (int)((const uint8_t*)g.hl - (const uint8_t*)g.hh) : 0;
     src.hr = __builtin_amdgcn_make_buffer_rsrc(g.hh, (short)0, 0x7fff0000, G_BUF_FLAGS);
     src.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, (int)(g.w_off + g.N * g.K),
                                                G_BUF_FLAGS);
@@ -570,18 +628,18 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[ms][ns][e] = 0.0f;
         }
-#define D_SW(B) reinterpret_cast<float*>((B) + D_SBYTES)
+#define D_SW(B) reinterpret_cast<float*>((B) + SBYTES)
 #define D_STEP(SB, NSB)                                                                                  \
     {                                                                                                    \
-        wait_vm<D_LPS>();                                                                                \
+        wait_vm<d_lps<TERMS>()>();                                                                       \
         g_barrier();                                                                                     \
-        d_issue(src, kb + 2, nkb, NSB, D_SW(NSB), wave);                                                 \
-        d_step(SB, D_SW(SB), wm, wn, wave, lane, (kb & 1) || kb + 1 == nkb, blk, acc);                  \
+        d_issue<TERMS>(src, kb + 2, nkb, NSB, D_SW(NSB), wave);                                          \
+        d_step<TERMS>(SB, wm, wn, wave, lane, (kb & 1) || kb + 1 == nkb, blk, acc);                      \
         if (++kb == nkb) break;                                                                          \
     }
     int kb = 0;
-    d_issue(src, 0, nkb, sb0, D_SW(sb0), wave);
-    d_issue(src, 1, nkb, sb1, D_SW(sb1), wave);
+    d_issue<TERMS>(src, 0, nkb, sb0, D_SW(sb0), wave);
+    d_issue<TERMS>(src, 1, nkb, sb1, D_SW(sb1), wave);
     for (;;) {
         D_STEP(sb0, sb2)
         D_STEP(sb1, sb0)
@@ -612,8 +670,9 @@ int launch_grouped(const GArgs& a, int mode, dim3 grid, hipStream_t st) {
     return launched("grouped_gemm_fp8");
 }
 
-int launch_grouped_down(const GArgs& a, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL(grouped_down_bf16_kernel, grid, dim3(GTHREADS), 0, st, a);
+int launch_grouped_down(const GArgs& a, int terms, dim3 grid, hipStream_t st) {
+    if (terms == 2) hipLaunchKernelGGL(grouped_down_bf16_kernel<2>, grid, dim3(GTHREADS), 0, st, a);
+    else hipLaunchKernelGGL(grouped_down_bf16_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
     return launched("grouped_down_bf16");
 }
 
@@ -641,7 +700,7 @@ int launch_combine(const float* y, const int32_t* slot, const float* w, void* ou
 int check_geo(const OomFp8Record* g, const char* who);
 
 // Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | hh | hl | y (hh and hl:
-// the bf16 hi and lo terms of h [A, inter]).
+// the bf16 hi and lo terms of h [A, inter]; hl is written for the exact precision only).
 struct PrefillWs {
     size_t plan, recs, xq, xs, tiles, hh, hl, y, total;
     int max_tiles;
@@ -713,8 +772,8 @@ extern "C" size_t oom_moe_prefill_fp8_workspace_size(int T, int E, int k, const 
 }
 
 extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T,
-                                   int E, int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out,
-                                   int out_dtype, void* ws, size_t ws_bytes, void* stream) {
+                                   int E, int k, const OomFp8Record* geo, int precision, int32_t* ids, float* weights,
+                                   void* out, int out_dtype, void* ws, size_t ws_bytes, void* stream) {
     using namespace oom;
     if (int rc = check_geo(geo, "oom_moe_prefill_fp8")) return rc;
     OOM_REQUIRE(geo->hidden % 128 == 0 && geo->inter % 128 == 0,
@@ -728,6 +787,7 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     OOM_REQUIRE(k >= 1 && k <= 32 && E >= k && E <= 8192, "oom_moe_prefill_fp8: router top-k > 32 or experts > 8192");
     OOM_REQUIRE(x_dtype == OOM_F32 || x_dtype == OOM_BF16, "oom_moe_prefill_fp8: x_dtype");
     OOM_REQUIRE(out_dtype == OOM_F32 || out_dtype == OOM_BF16, "oom_moe_prefill_fp8: out_dtype");
+    OOM_REQUIRE(precision == OOM_EXPERT_EXACT || precision == OOM_EXPERT_BF16, "oom_moe_prefill_fp8: precision");
     OOM_REQUIRE(logits && x && all_recs && ids && weights && out, "oom_moe_prefill_fp8: null buffer");
     const PrefillWs w = prefill_ws(T, E, k, *geo);
     if (!ws || ws_bytes < w.total)
@@ -766,7 +826,7 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     a.w2_off = geo->up_weight;
     a.s2_off = geo->up_scale;
     a.hh = hh;
-    a.hl = hl;
+    a.hl = precision == OOM_EXPERT_EXACT ? hl : nullptr;
     // 8 spare rows of blocks: the XCD-run order needs the grid to cover 8 ceil(W / 8) slots
     if (int rc = launch_grouped(a, 1, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles + 8, 1), st)) return rc;
     GArgs d{};
@@ -781,7 +841,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     d.hh = hh;
     d.hl = hl;
     d.y = y;
-    if (int rc = launch_grouped_down(d, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles + 8, 1), st))
+    const int terms = precision == OOM_EXPERT_EXACT ? 2 : 1;
+    if (int rc = launch_grouped_down(d, terms, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles + 8, 1), st))
         return rc;
     return launch_combine(y, pv.slot_assign(), weights, out, out_dtype, T, (int)geo->hidden, k, st);
 }

@@ -263,17 +263,24 @@ int oom_moe_grouped_gemm_fp8(const uint64_t* recs, const int32_t* off, const int
                              int max_per_expert, const uint8_t* xq, const float* x_scale, int x_group, float* y,
                              int64_t N, int64_t K, int64_t w_off, int64_t s_off, void* stream);
 
+/* Activation precision of the prefill's down projection: the reference's ExpertPrecision
+ * (crates/oominf-core/src/backend.rs:142-149). OOM_EXPERT_BF16 rounds h to bf16 (one
+ * matrix-core pass); OOM_EXPERT_EXACT keeps 16 significant bits of the fp32 h as two
+ * bf16 terms (two passes). */
+#define OOM_EXPERT_EXACT 0
+#define OOM_EXPERT_BF16 1
+
 /* One prefill MoE FFN step on the device, with no host synchronisation: router top-k,
  * routing plan, x quantised per token to e4m3, gate and up grouped GEMMs with
- * h = silu(g) * u quantised per (assignment, 128 columns) in the same pass, down grouped
- * GEMM, slot-order weighted combine. logits f32 [T, E]; x [T, hidden] in x_dtype; out
- * [T, hidden] in out_dtype; ids / weights as oom_router_topk. hidden and inter multiples
- * of 128. The tiled prefill of Moe::forward (crates/oominf-models-qwen/src/moe.rs:700,
+ * h = silu(g) * u formed in the same pass (in `precision`), down grouped GEMM on the bf16
+ * matrix cores, slot-order weighted combine. logits f32 [T, E]; x [T, hidden] in x_dtype;
+ * out [T, hidden] in out_dtype; ids / weights as oom_router_topk. hidden and inter
+ * multiples of 128. The tiled prefill of Moe::forward (crates/oominf-models-qwen/src/moe.rs:700,
  * 746-758: run_group over moe_tiled and moe_swiglu_range) with FP8 activations. */
 size_t oom_moe_prefill_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo);
 int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T, int E,
-                        int k, const OomFp8Record* geo, int32_t* ids, float* weights, void* out, int out_dtype,
-                        void* ws, size_t ws_bytes, void* stream);
+                        int k, const OomFp8Record* geo, int precision, int32_t* ids, float* weights, void* out,
+                        int out_dtype, void* ws, size_t ws_bytes, void* stream);
 
 /* Paged GQA decode attention for one query token: out[h, :] = sum_j softmax_j(q_h . k_j
  * * scale) v_j over the kv_len keys, query head h reading KV head h / (heads / kv_heads).

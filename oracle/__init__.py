@@ -137,7 +137,7 @@ def lib() -> ctypes.CDLL:
             "oracle_moe_down_nvfp4": (None, [P, P, I32, P, P, P]),
             "oracle_moe_decode_nvfp4": (I32, [P, P, P, I32, I32, I32, P, P, P, P]),
             "oracle_grouped_gemm_fp8": (None, [P, P, P, I32, P, P, I32, P, I64, I64, I64, I64]),
-            "oracle_moe_prefill_fp8": (I32, [P, P, P, I32, I32, I32, P, P, P, P]),
+            "oracle_moe_prefill_fp8": (I32, [P, P, P, I32, I32, I32, P, I32, P, P, P]),
             "oracle_attn_decode_paged": (None, [P, P, P, P, I32, I32, I32, I32, I32, F, P]),
             "oracle_host_experts": (I32, [P, P, P, P, I32, P, P, I32]),
             "oracle_host_has_avx512": (I32, []),
@@ -453,7 +453,9 @@ def grouped_gemm_fp8(recs, off, rows, xq, x_scale, x_group, N, K, w_off, s_off) 
     return y
 
 
-def moe_prefill(logits: np.ndarray, x: np.ndarray, all_recs, k: int, geo: Fp8Record):
+def moe_prefill(logits: np.ndarray, x: np.ndarray, all_recs, k: int, geo: Fp8Record, h_bf16: bool = False):
+    """The whole prefill step; h_bf16 rounds h to bf16 before the down projection (the
+    reference's ExpertPrecision::Bf16), else h stays fp32 (ExpertPrecision::Exact)."""
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     x = np.ascontiguousarray(x, dtype=np.float32)
     T, E = logits.shape
@@ -461,7 +463,8 @@ def moe_prefill(logits: np.ndarray, x: np.ndarray, all_recs, k: int, geo: Fp8Rec
     w = np.empty((T, k), dtype=np.float32)
     out = np.empty((T, geo.hidden), dtype=np.float32)
     table = _ptrs(all_recs)
-    n_e = lib().oracle_moe_prefill_fp8(_p(logits), _p(x), _p(table), T, E, k, ctypes.byref(geo), _p(ids), _p(w), _p(out))
+    n_e = lib().oracle_moe_prefill_fp8(_p(logits), _p(x), _p(table), T, E, k, ctypes.byref(geo), int(h_bf16), _p(ids),
+                                       _p(w), _p(out))
     assert n_e >= 0
     return ids, w, out
 

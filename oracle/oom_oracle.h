@@ -170,12 +170,13 @@ void oracle_grouped_gemm_fp8(const uint8_t* const* recs, const int32_t* off, con
 
 /* Whole prefill MoE FFN over the routed assignments of T tokens: x fp32 [T, H]
  * quantised per token, gate and up grouped GEMMs, h = silu(g) * u kept in fp32 (the
- * reference's exact tiled path, ExpertPrecision::Exact), the down projection as
- * oracle_moe_down_fp8, slot-order combine.
+ * reference's exact tiled path, ExpertPrecision::Exact) or, with h_bf16, rounded to bf16
+ * to nearest even (ExpertPrecision::Bf16), the down projection as oracle_moe_down_fp8,
+ * slot-order combine.
  * crates/oominf-models-qwen/src/moe.rs:746-758 (tiled run_group) + :700.
  * Returns n_e or -1. */
 int oracle_moe_prefill_fp8(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
-                           const OomFp8Record* geo, int32_t* ids, float* weights, float* out);
+                           const OomFp8Record* geo, int h_bf16, int32_t* ids, float* weights, float* out);
 
 /* ---- paged GQA decode attention ---------------------------------------- */
 

@@ -360,7 +360,7 @@ void oracle_grouped_gemm_fp8(const uint8_t* const* recs, const int32_t* off, con
 }
 
 int oracle_moe_prefill_fp8(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
-                           const OomFp8Record* geo, int32_t* ids, float* weights, float* out) {
+                           const OomFp8Record* geo, int h_bf16, int32_t* ids, float* weights, float* out) {
     int A = T * k;
     int64_t H = geo->hidden, I = geo->inter;
     oracle_router_topk(logits, T, E, k, ids, weights);
@@ -383,10 +383,13 @@ int oracle_moe_prefill_fp8(const float* logits, const float* x, const uint8_t* c
     oracle_grouped_gemm_fp8(recs, off, tok, n_e, xq, xs, 0, g, I, H, geo->gate_weight, geo->gate_scale);
     oracle_grouped_gemm_fp8(recs, off, tok, n_e, xq, xs, 0, u, I, H, geo->up_weight, geo->up_scale);
     for (size_t i = 0; i < (size_t)A * (size_t)I; i++) g[i] = siluf(g[i]) * u[i];
-    /* h stays fp32 into the down projection, as the reference's exact tiled path keeps its
+    /* h into the down projection: fp32, as the reference's exact tiled path keeps its
      * activations (ExpertPrecision::Exact, crates/oominf-core/src/backend.rs:144-149;
-     * crates/oominf-cuda/kernels/moe.cu:166-335 with three bf16 terms): the decode path's
+     * crates/oominf-cuda/kernels/moe.cu:166-335 with three bf16 terms), or rounded to bf16
+     * (ExpertPrecision::Bf16, one tensor-core pass; h_bf16 set); then the decode path's
      * down, per-128-column block sums times the block scale. */
+    if (h_bf16)
+        for (size_t i = 0; i < (size_t)A * (size_t)I; i++) g[i] = oracle_bf16_to_f32(oracle_bf16_from_f32(g[i]));
     float* y = (float*)malloc(sizeof(float) * (size_t)A * (size_t)H);
     oracle_moe_down_fp8(recs, off, n_e, g, y, geo);
     oracle_moe_combine_slots(y, slot, weights, out, T, (int)H, k);

@@ -4,8 +4,9 @@ matrix cores, whole prefill MoE step) through the C ABI, against the oracle.
 Bars: quantised codes and scales bit-exact; grouped GEMM worst |got - f64| / sum |x w|
 < 3e-5 (the reference's own gate for its tiled path is 2e-6, crates/oominf-cuda/tests/moe_tiled.rs:174-223,
 for a bf16-exact sum; the FP8 matrix core's block sum is coarser, see the test); prefill
-outputs (bf16) end to end within rtol 2e-2 / atol 1e-3 of the oracle's whole prefill (h in
-fp32, the reference's exact path), router ids bit-exact.
+outputs (bf16) end to end within rtol 2e-2 / atol 1e-3 of the oracle's whole prefill in the
+same precision (exact: h in fp32, the reference's default path; bf16: h rounded to bf16),
+router ids bit-exact.
 """
 import numpy as np
 import pytest
@@ -143,31 +144,37 @@ def prefill_workspace(ws, T, E, k, H, I):
 MFMA_BAR = 3e-5  # |block sum - exact| / sum |x w| of the FP8 matrix core (test_grouped_gemm_matches_oracle)
 
 
-def check_h(h, hi, lo, g, u, gabs, uabs):
-    """The GPU's h against the oracle's g, u: hi is bf16(h) and lo bf16(h - hi) of one fp32
-    h, and h sits within what the FP8 matrix core's block sums allow (g and u each within
-    MFMA_BAR * sum |x w| of the oracle's, carried through silu(g) * u) plus the two terms'
-    rounding (2^-16 of |h|)."""
+def check_h(h, hi, lo, g, u, gabs, uabs, exact=True):
+    """The GPU's h against the oracle's g, u: hi is bf16(h) and (exact) lo bf16(h - hi) of
+    one fp32 h, and h sits within what the FP8 matrix core's block sums allow (g and u each
+    within MFMA_BAR * sum |x w| of the oracle's, carried through silu(g) * u) plus the
+    terms' rounding (2^-16 of |h| with two terms, 2^-8 with hi alone)."""
     assert np.array_equal(oracle.bf16_to_f32(oracle.bf16_from_f32(hi)), hi)
-    assert np.all(np.abs(lo) <= np.abs(hi) * 2.0 ** -8 * 1.01 + 1e-38), "lo is not the residual of hi"
+    if exact:
+        assert np.all(np.abs(lo) <= np.abs(hi) * 2.0 ** -8 * 1.01 + 1e-38), "lo is not the residual of hi"
     g64, u64 = g.astype(np.float64), u.astype(np.float64)
     sig = 1.0 / (1.0 + np.exp(-g64))
     h64 = g64 * sig * u64
     dh = MFMA_BAR * (np.abs(sig * (1 + g64 * (1 - sig)) * u64) * gabs + np.abs(g64 * sig) * uabs)
     err = np.abs(h.astype(np.float64) - h64)
-    ok = err <= dh + 2.0 ** -16 * np.abs(h64) + 1e-30
+    ok = err <= dh + (2.0 ** -16 if exact else 2.0 ** -8) * np.abs(h64) + 1e-30
     assert np.all(ok), f"{(~ok).sum()} of {h.size} h values outside the matrix-core bound; worst excess " \
                        f"{(err - dh)[~ok].max():.3e}"
     return float((err / np.maximum(dh, 1e-30)).max())
 
 
-def prefill_check(hip, geo, recs, logits, xb, k, sample=None):
+def prefill_check(hip, geo, recs, logits, xb, k, sample=None, precision=None):
     """GPU prefill against the oracle: router ids exact and weights to fp32 rounding; x
     codes and scales exact; h within the FP8 matrix core's bound of the oracle's fp32 h;
     the down projection and slot-order combine from the GPU's h within 2e-5 of scale of the
-    oracle's (the bf16 two-term down); and the output end to end within rtol 2e-2 /
-    atol 1e-3 of the oracle's whole prefill (oracle.moe_prefill, h in fp32)."""
+    oracle's (bf16 terms, exact products); and the output end to end within rtol 2e-2 /
+    atol 1e-3 of the oracle's whole prefill in the same precision (oracle.moe_prefill:
+    h in fp32, the reference's default exact path, or rounded to bf16)."""
     import torch
+
+    if precision is None:
+        precision = hip.EXPERT_EXACT
+    exact = precision == hip.EXPERT_EXACT
 
     T, E = logits.shape
     H, I = geo.hidden, geo.inter
@@ -180,8 +187,8 @@ def prefill_check(hip, geo, recs, logits, xb, k, sample=None):
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
     out32 = torch.empty((T, H), dtype=torch.float32, device="cuda")
     xd = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
-    hip.moe_prefill_fp8(dev(logits), xd, addrs, k, hgeo, ids, w, out32, ws)
-    hip.moe_prefill_fp8(dev(logits), xd, addrs, k, hgeo, ids, w, out, ws)
+    hip.moe_prefill_fp8(dev(logits), xd, addrs, k, hgeo, ids, w, out32, ws, precision=precision)
+    hip.moe_prefill_fp8(dev(logits), xd, addrs, k, hgeo, ids, w, out, ws, precision=precision)
     torch.cuda.synchronize()
     host = recs if isinstance(recs, list) else [r for r in buf.cpu().numpy()]
     rows = np.arange(T) if sample is None else np.asarray(sample)
@@ -215,42 +222,48 @@ def prefill_check(hip, geo, recs, logits, xb, k, sample=None):
         xa = xabs[tok[a]].astype(np.float32)
         gabs[n] = np.abs(wg) @ xa
         uabs[n] = np.abs(wu) @ xa
-    h_used = check_h(st["h"][sel], st["hi"][sel], st["lo"][sel], g, u, gabs, uabs)
+    h_gpu = st["h"][sel] if exact else st["hi"][sel]
+    h_used = check_h(h_gpu, st["hi"][sel], st["lo"][sel], g, u, gabs, uabs, exact)
     # down + combine from the GPU's h: the oracle's down over the same h (the bf16 terms
-    # carry 16 bits of h; the products are exact; only the summation order differs)
-    y = oracle.moe_down(recs_sel, off1, st["h"][sel], geo)
+    # carry 16 or 8 bits of h; the products are exact; only the summation order differs)
+    y = oracle.moe_down(recs_sel, off1, h_gpu, geo)
     want_gh = oracle.moe_combine_slots(y, np.arange(len(sel), dtype=np.int32).reshape(len(rows), k), want_w)
     got32 = out32.cpu().numpy()[rows]
     err = np.abs(got32 - want_gh).max()
     assert err <= 2e-5 * np.abs(want_gh).max(), f"down + combine from the GPU's h: {err:.3e}"
-    # end to end against the oracle's whole prefill (its own h, in fp32): the bar
-    _, _, pure = oracle.moe_prefill(logits[rows], x[rows], host, k, geo)
+    # end to end against the oracle's whole prefill in the same precision: the bar (for
+    # the exact precision, h in fp32 as the reference's default path keeps it; for bf16,
+    # h rounded to bf16 as the reference's ExpertPrecision::Bf16, which at the full shape is
+    # itself a few 1e-3 from the fp32-h result, past atol 1e-3)
+    _, _, pure = oracle.moe_prefill(logits[rows], x[rows], host, k, geo, h_bf16=not exact)
     got = out.float().cpu().numpy()[rows]
     bad = ~np.isclose(got, pure, rtol=RTOL, atol=ATOL)
     assert not bad.any(), f"end to end: {bad.sum()} of {bad.size} outside rtol {RTOL} / atol {ATOL}; " \
                           f"worst {np.abs(got - pure)[bad].max():.3e}"
-    print(f"prefill: h within {h_used:.2f} of the matrix-core bound; end to end worst abs "
-          f"{np.abs(got - pure).max():.2e}, f32 worst abs {np.abs(got32 - pure).max():.2e}")
+    print(f"prefill ({'exact' if exact else 'bf16'}): h within {h_used:.2f} of the matrix-core bound; end to end "
+          f"worst abs {np.abs(got - pure).max():.2e}, f32 worst abs {np.abs(got32 - pure).max():.2e}")
 
 
+@pytest.mark.parametrize("prec", ["bf16", "exact"])
 @pytest.mark.parametrize("T,E,k,H,I", [(64, 16, 4, 512, 256), (7, 8, 2, 256, 128), (300, 32, 8, 1024, 384)])
-def test_prefill_small(hip, T, E, k, H, I):
-    print(f"prefill T={T} E={E} k={k} H={H} I={I}", flush=True)
+def test_prefill_small(hip, T, E, k, H, I, prec):
+    print(f"prefill T={T} E={E} k={k} H={H} I={I} precision={prec}", flush=True)
     geo = oracle.record_geometry(H, I)
     logits = synth.decode_logits(77 + T, T, E, 1.1)
     recs = synth.expert_records(geo, 77 + T, E)
     xb = synth.activations_bf16(77 + T, T, H)
-    prefill_check(hip, geo, recs, logits, xb, k)
+    prefill_check(hip, geo, recs, logits, xb, k, precision=hip.EXPERT_EXACT if prec == "exact" else hip.EXPERT_BF16)
 
 
-def test_prefill_full_shape_sampled_tokens(hip):
+@pytest.mark.parametrize("prec", ["bf16", "exact"])
+def test_prefill_full_shape_sampled_tokens(hip, prec):
     """2048 tokens, 128 experts (all routed), top-8 with a Zipf(1.1) bias, hidden 4096,
     inter 1536. A token's output depends only on its own row, routing and the experts
     it picks, so the oracle checks a sample of 12 tokens of the full step."""
     import torch
 
     T, E, k, H, I = 2048, 128, 8, 4096, 1536
-    print("prefill full shape", flush=True)
+    print(f"prefill full shape, precision {prec}", flush=True)
     geo = oracle.record_geometry(H, I)
     stride = oracle.record_stride(geo)
     g = torch.Generator(device="cuda")
@@ -270,4 +283,5 @@ def test_prefill_full_shape_sampled_tokens(hip):
     logits = synth.decode_logits(31, T, E, 1.1)
     xb = synth.activations_bf16(31, T, H)
     sample = np.array([0, 1, 2, 100, 511, 777, 1024, 1500, 1800, 2045, 2046, 2047])
-    prefill_check(hip, geo, (buf, addrs), logits, xb, k, sample)
+    prefill_check(hip, geo, (buf, addrs), logits, xb, k, sample,
+                  precision=hip.EXPERT_EXACT if prec == "exact" else hip.EXPERT_BF16)
