@@ -68,6 +68,15 @@ SIGNATURES = {
     "oom_moe_prefill_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, I32, P, P, P, I32, P, SZ, P]),
     "oom_attn_decode_workspace_size": (SZ, [I32, I32, I32, I32]),
     "oom_attn_decode_paged": (I32, [P, I32, P, P, P, I32, I32, I32, I32, I32, I32, F, P, I32, P, SZ, P]),
+    "oom_kv_codebook_size": (SZ, []),
+    "oom_kv_codebooks": (I32, [P, SZ]),
+    "oom_kv_row_bytes": (SZ, [I32, I32]),
+    "oom_kv_rotate": (I32, [P, I32, I32, I32, P]),
+    "oom_kv_append": (I32, [P, P, I64, I32, I32, I32, I32, P, P]),
+    "oom_kv_read": (I32, [P, P, I32, I32, I32, I32, P, P]),
+    "oom_mask_compact": (I32, [P, P, I32, P]),
+    "oom_attn_decode_turbo_workspace_size": (SZ, [I32, I32, I32, I32]),
+    "oom_attn_decode_turbo": (I32, [P, P, P, I32, I32, P, P, I32, I32, I32, I32, F, P, P, SZ, P]),
     "oom_copy_queue_create": (I32, [P]),
     "oom_copy_queue_destroy": (I32, [P]),
     "oom_host_alloc": (I32, [P, SZ]),
@@ -325,6 +334,56 @@ def attn_decode_paged(q, k_pages, v_pages, page_table, kv_len: int, scale: float
     check(lib().oom_attn_decode_paged(_ptr(q), _dtype_code(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
                                       n_pages, page_size, kv_len, heads, kv_heads, d, scale, _ptr(out),
                                       _dtype_code(out), _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))
+
+
+# ---- Turbo KV cache and the d = 256, G = 12 decode attention ----
+
+def kv_codebooks():
+    """The codebook table (numpy f32, 508 levels) of oom_kv_codebooks."""
+    import numpy as np
+
+    n = int(lib().oom_kv_codebook_size())
+    t = np.empty(n, dtype=np.float32)
+    check(lib().oom_kv_codebooks(t.ctypes.data_as(ctypes.c_void_p), n))
+    return t
+
+
+def kv_row_bytes(d: int, bits: int) -> int:
+    return int(lib().oom_kv_row_bytes(d, bits))
+
+
+def kv_rotate(x, inverse: bool, stream=None) -> None:
+    d = x.shape[-1]
+    check(lib().oom_kv_rotate(_ptr(x), x.numel() // d, d, int(inverse), _stream(stream)))
+
+
+def kv_append(src, cache, start: int, bits: int, levels, stream=None) -> None:
+    """src f32 [t, kv_heads, d] at sequence position `start` of cache (u8 rows [len, kv_heads])."""
+    t, kv_heads, d = src.shape
+    check(lib().oom_kv_append(_ptr(src), _ptr(cache), start, t, kv_heads, d, bits, _ptr(levels), _stream(stream)))
+
+
+def kv_read(cache, dst, bits: int, levels, stream=None) -> None:
+    """dst f32 [len, kv_heads, d] from the first len * kv_heads rows of cache."""
+    ln, kv_heads, d = dst.shape
+    check(lib().oom_kv_read(_ptr(cache), _ptr(dst), ln, kv_heads, d, bits, _ptr(levels), _stream(stream)))
+
+
+def mask_compact(mask, sel, stream=None) -> None:
+    check(lib().oom_mask_compact(_ptr(mask), _ptr(sel), mask.numel(), _stream(stream)))
+
+
+def attn_decode_turbo_workspace_size(heads: int, kv_heads: int, d: int, kv_len: int) -> int:
+    return int(lib().oom_attn_decode_turbo_workspace_size(heads, kv_heads, d, kv_len))
+
+
+def attn_decode_turbo(q, k, v, k_bits: int, v_bits: int, levels, mask, kv_heads: int, kv_len: int, scale: float, out,
+                      ws, stream=None) -> None:
+    """q f32 [heads, 256]; k / v u8 cache rows [kv_len, kv_heads]; mask u8 [kv_len]; out f32 [heads, 256]."""
+    heads, d = q.shape
+    check(lib().oom_attn_decode_turbo(_ptr(q), _ptr(k), _ptr(v), k_bits, v_bits, _ptr(levels), _ptr(mask), heads,
+                                      kv_heads, d, kv_len, scale, _ptr(out), _ptr(ws), ws.numel() * ws.element_size(),
+                                      _stream(stream)))
 
 
 def quantize_rows_fp8(x, q, scale, stream=None) -> None:

@@ -299,6 +299,48 @@ int oom_attn_decode_paged(const void* q, int q_dtype, const uint16_t* k_pages, c
                           const int32_t* page_table, int n_pages, int page_size, int kv_len, int heads, int kv_heads,
                           int d, float scale, void* out, int out_dtype, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- Turbo KV cache and the D = 256, G = 12 decode attention ----
+ * KvFormat (crates/oominf-core/src/backend.rs:571-635): a cache row is one head vector of
+ * d coordinates; bits 0: d fp32 values; bits 2..8 (Turbo): the vector rotated by a fixed
+ * randomized Walsh-Hadamard transform, then per 32 coordinates an fp16 scale (their RMS;
+ * the scales padded to 16 bytes) and `bits` 32-bit words, word j holding bit j of the 32
+ * codebook indices. A cache holds rows [len, kv_heads]. `levels` is the device copy of
+ * oom_kv_codebooks' table (null for fp32 rows). */
+
+/* KvFormat::codebooks (backend.rs:637-700): the Lloyd-Max levels of a unit Gaussian for
+ * 2..8 bits, ascending, concatenated (the 2^b levels for b bits start at 2^b - 4); 508
+ * floats into `levels` (n >= oom_kv_codebook_size()). Computed on the host once. */
+size_t oom_kv_codebook_size(void);
+int oom_kv_codebooks(float* levels, size_t n);
+/* KvFormat::row_bytes (backend.rs:605-611); 0 for a shape the kernels do not take (d a
+ * multiple of 32 up to 256, a power of two for bits 2..8). */
+size_t oom_kv_row_bytes(int d, int bits);
+/* Gpu::kv_rotate (crates/oominf-cuda/src/attention.rs:476-496; attention.cu:63-73): rows
+ * [rows, d] f32 in place into (inverse 0) or out of (inverse 1) the rotated space. */
+int oom_kv_rotate(float* x, int rows, int d, int inverse, void* stream);
+/* Attention::kv_append (attention.rs:172-214; attention.cu:75-112): src f32 [t, kv_heads,
+ * d] appended at sequence position `start` (cache row start * kv_heads), rotated and
+ * quantised for bits 2..8. */
+int oom_kv_append(const float* src, uint8_t* cache, int64_t start, int t, int kv_heads, int d, int bits,
+                  const float* levels, void* stream);
+/* Attention::kv_read (attention.rs:216-254; attention.cu:114-131): len * kv_heads rows back
+ * as f32 [len, kv_heads, d], decoded and un-rotated. */
+int oom_kv_read(const uint8_t* cache, float* dst, int len, int kv_heads, int d, int bits, const float* levels,
+                void* stream);
+/* mask_compact (attention.cu:363-374): the positions j < n with mask[j] != 0, in order:
+ * sel[0] = count, sel[1 ..] = positions (sel: n + 1 int32). */
+int oom_mask_compact(const uint8_t* mask, int32_t* sel, int n, void* stream);
+/* One query token of Attention::attention with d = 256 and 12 query heads a KV head, the
+ * flash-decode path (attention.rs:265-346,365-447; attention.cu:584-686): q f32 [heads,
+ * 256] (rotated on the device for a Turbo cache), the keys j < kv_len with mask[j] != 0
+ * (u8 [kv_len]), out f32 [heads, 256] = sum_j softmax_j(q_h . k_j * scale) v_j (rotated
+ * back), query head h reading KV head h / 12. k_bits and v_bits both 0 or both 2..8.
+ * fp32 dot products, exp and accumulation. */
+size_t oom_attn_decode_turbo_workspace_size(int heads, int kv_heads, int d, int kv_len);
+int oom_attn_decode_turbo(const float* q, const uint8_t* k, const uint8_t* v, int k_bits, int v_bits,
+                          const float* levels, const uint8_t* mask, int heads, int kv_heads, int d, int kv_len,
+                          float scale, float* out, void* ws, size_t ws_bytes, void* stream);
+
 
 /* ---- copies beside compute (expert offload) ----
  * The Transfer trait (crates/oominf-core/src/backend.rs:945-1018; CUDA form

@@ -140,6 +140,15 @@ def lib() -> ctypes.CDLL:
             "oracle_moe_prefill_fp8": (I32, [P, P, P, I32, I32, I32, P, I32, P, P, P]),
             "oracle_attn_decode_paged": (None, [P, P, P, P, I32, I32, I32, I32, I32, F, P]),
             "oracle_host_experts": (I32, [P, P, P, P, I32, P, P, I32]),
+            "oracle_f16_from_f32": (ctypes.c_uint16, [F]),
+            "oracle_f16_to_f32": (F, [ctypes.c_uint16]),
+            "oracle_kv_codebooks": (None, [P]),
+            "oracle_kv_row_bytes": (ctypes.c_size_t, [I32, I32]),
+            "oracle_kv_rotate": (None, [P, I32, I32, I32]),
+            "oracle_kv_append": (None, [P, P, I64, I32, I32, I32, P]),
+            "oracle_kv_read": (None, [P, P, I32, I32, I32, P]),
+            "oracle_mask_compact": (I32, [P, P, I32]),
+            "oracle_attn_decode_turbo": (None, [P, P, P, I32, I32, P, P, I32, I32, I32, F, P]),
             "oracle_host_has_avx512": (I32, []),
         }
         for name, (res, args) in sig.items():
@@ -495,3 +504,73 @@ def host_experts(geo: Fp8Record, records, job_tokens, x: np.ndarray, threads: in
 
 def host_has_avx512() -> bool:
     return bool(lib().oracle_host_has_avx512())
+
+
+# ---- Turbo KV cache and the d = 256, G = 12 decode attention (turbo.c) ----
+
+_codebooks = None
+
+
+def kv_codebooks() -> np.ndarray:
+    """KvFormat::codebooks: 508 levels (2..8 bits, ascending, concatenated); the levels for
+    b bits start at 2^b - 4."""
+    global _codebooks
+    if _codebooks is None:
+        t = np.empty(508, dtype=np.float32)
+        lib().oracle_kv_codebooks(_p(t))
+        _codebooks = t
+    return _codebooks
+
+
+def f16_from_f32(x: float) -> int:
+    return int(lib().oracle_f16_from_f32(x))
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().oracle_f16_to_f32(h))
+
+
+def kv_row_bytes(d: int, bits: int) -> int:
+    return int(lib().oracle_kv_row_bytes(d, bits))
+
+
+def kv_rotate(x: np.ndarray, inverse: bool) -> np.ndarray:
+    y = np.array(x, dtype=np.float32, copy=True, order="C")
+    d = y.shape[-1]
+    lib().oracle_kv_rotate(_p(y), y.size // d, d, int(inverse))
+    return y
+
+
+def kv_append(src: np.ndarray, bits: int, cache: np.ndarray | None = None, row0: int = 0) -> np.ndarray:
+    """Rows of src (..., d) appended at cache row row0 (a fresh zeroed cache when None)."""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    d = src.shape[-1]
+    rows = src.size // d
+    rb = kv_row_bytes(d, bits)
+    if cache is None:
+        cache = np.zeros((row0 + rows) * rb, dtype=np.uint8)
+    lib().oracle_kv_append(_p(src), _p(cache), row0, rows, d, bits, _p(kv_codebooks()))
+    return cache
+
+
+def kv_read(cache: np.ndarray, rows: int, d: int, bits: int) -> np.ndarray:
+    out = np.empty((rows, d), dtype=np.float32)
+    lib().oracle_kv_read(_p(np.ascontiguousarray(cache, dtype=np.uint8)), _p(out), rows, d, bits, _p(kv_codebooks()))
+    return out
+
+
+def mask_compact(mask: np.ndarray) -> np.ndarray:
+    mask = np.ascontiguousarray(mask, dtype=np.uint8)
+    sel = np.zeros(mask.size + 1, dtype=np.int32)
+    lib().oracle_mask_compact(_p(mask), _p(sel), mask.size)
+    return sel
+
+
+def attn_decode_turbo(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, kb: int, vb: int, mask: np.ndarray,
+                      H: int, Hkv: int, kv_len: int, scale: float) -> np.ndarray:
+    out = np.empty((H, 256), dtype=np.float32)
+    lib().oracle_attn_decode_turbo(_p(np.ascontiguousarray(q, dtype=np.float32)),
+                                   _p(np.ascontiguousarray(k_cache, dtype=np.uint8)),
+                                   _p(np.ascontiguousarray(v_cache, dtype=np.uint8)), kb, vb, _p(kv_codebooks()),
+                                   _p(np.ascontiguousarray(mask, dtype=np.uint8)), H, Hkv, kv_len, scale, _p(out))
+    return out

@@ -206,6 +206,34 @@ int oracle_host_experts(const OomFp8Record* geo, const uint8_t* const* records, 
 /* Whether the AVX-512 kernels are in use on this CPU. */
 int oracle_host_has_avx512(void);
 
+/* ---- Turbo KV cache and the d = 256, G = 12 decode attention (turbo.c) ---- */
+
+/* fp16 bits of f, round to nearest even (IEEE binary16); and back, exactly. */
+uint16_t oracle_f16_from_f32(float f);
+float oracle_f16_to_f32(uint16_t h);
+/* KvFormat::codebooks (crates/oominf-core/src/backend.rs:637-700): 508 levels, the 2^b
+ * Lloyd-Max levels of a unit Gaussian for b = 2..8, ascending, concatenated. */
+void oracle_kv_codebooks(float* levels);
+/* KvFormat::row_bytes (backend.rs:605-611). */
+size_t oracle_kv_row_bytes(int D, int bits);
+/* kv_rotate (crates/oominf-cuda/kernels/attention.cu:63-73): rows [rows, D] in place. */
+void oracle_kv_rotate(float* x, int rows, int D, int inverse);
+/* kv_append (attention.cu:75-112): rows [rows, D] into cache rows row0 .. + rows. */
+void oracle_kv_append(const float* src, uint8_t* cache, int64_t row0, int rows, int D, int bits,
+                      const float* levels);
+/* kv_read (attention.cu:114-131). */
+void oracle_kv_read(const uint8_t* cache, float* dst, int rows, int D, int bits, const float* levels);
+/* mask_compact (attention.cu:363-374); returns the count. */
+int oracle_mask_compact(const uint8_t* mask, int32_t* sel, int n);
+/* Attention::attention for one token with d = 256, 12 query heads a KV head: q [H, 256]
+ * rotated for a Turbo cache, mask_compact, the partials of attn_decode_partial_g12 (P =
+ * ceil(min(kv_len, 4096) / 16) rounded up to 8, even chunks of the list, lane l of a
+ * partial owning d = l + 32 e), attn_decode_combine, the output rotated back
+ * (crates/oominf-cuda/src/attention.rs:265-447; attention.cu:584-686). */
+void oracle_attn_decode_turbo(const float* q, const uint8_t* k, const uint8_t* v, int kb, int vb,
+                              const float* levels, const uint8_t* mask, int H, int Hkv, int kv_len, float scale,
+                              float* out);
+
 #ifdef __cplusplus
 }
 #endif
