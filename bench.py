@@ -9,7 +9,7 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 256 MB Infinity Cache.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|prefill|gemv|copy]
+                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|turbo|prefill|gemv|copy]
 
 Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
 kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
@@ -438,6 +438,95 @@ def bench_attn(args):
         res["cpu_baseline"] = {"value": us, "unit": "us/step", "cores": threads, "kind": "port",
                                "sample": f"{n} runs of the same attention step, oracle restatement of the reference's "
                                          f"fp32 attention, one thread per KV head, on {cpu_model()}"}
+    return res
+
+
+def bench_turbo(args):
+    """The product's own decode attention, batch 1: 24 query heads over 2 KV heads,
+    head_dim 256, 32768 keys in a Turbo k8v6 cache (K rows 8-bit, V rows 6-bit Lloyd-Max
+    codes over the rotated vector, fp16 block RMS scales), f32 q and out, all keys
+    visible (mask of ones), through oom_attn_decode_turbo: q rotation, mask_compact, the
+    flash-decode partials, their combine and the inverse rotation, all timed."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    H, Hkv, D, L, KB, VB = 24, 2, 256, 32768, 8, 6
+    levels = torch.from_numpy(hip.kv_codebooks()).cuda()
+    krb, vrb = hip.kv_row_bytes(D, KB), hip.kv_row_bytes(D, VB)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    # twelve caches (30 MB each) rotate between steps so the rows stream from HBM, not the MALL
+    copies = 12
+    caches = []
+    src = torch.empty((L, Hkv, D), dtype=torch.float32, device="cuda")
+    for _ in range(copies):
+        kc = torch.empty(L * Hkv * krb, dtype=torch.uint8, device="cuda")
+        vc = torch.empty(L * Hkv * vrb, dtype=torch.uint8, device="cuda")
+        src.normal_(generator=g)
+        hip.kv_append(src, kc, 0, KB, levels)
+        src.normal_(generator=g)
+        hip.kv_append(src, vc, 0, VB, levels)
+        caches.append((kc, vc))
+    del src
+    q = torch.randn((H, D), generator=g, device="cuda")
+    mask = torch.ones(L, dtype=torch.uint8, device="cuda")
+    out = torch.empty((H, D), dtype=torch.float32, device="cuda")
+    ws = torch.zeros(hip.attn_decode_turbo_workspace_size(H, Hkv, D, L), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / 16.0
+    stream = torch.cuda.current_stream()
+    fn = hip.lib().oom_attn_decode_turbo
+    cargs = [(hip._ptr(q), hip._ptr(kc), hip._ptr(vc), KB, VB, hip._ptr(levels), hip._ptr(mask), H, Hkv, D, L, scale,
+              hip._ptr(out), hip._ptr(ws), ws.numel(), hip._stream(stream)) for kc, vc in caches]
+    hip.attn_decode_turbo(q, caches[0][0], caches[0][1], KB, VB, levels, mask, Hkv, L, scale, out, ws, stream)
+
+    def step(i):
+        rc = fn(*cargs[i % copies])
+        if rc:
+            hip.check(rc)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(args.steps):
+        step(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    bytes_step = L * Hkv * (krb + vrb) + L + 2 * H * D * 4
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    res = {
+        "metric": "Turbo k8v6 decode attention us/step + achieved HBM GB/s (% of MI355X peak), 1 GPU",
+        "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "k8v6 Lloyd-Max codes with fp16 scales, f32 q/softmax/accumulate/out", "data": "synthetic",
+        "config": {"workload": "decode attention, batch 1: 24 q heads over 2 KV heads, head_dim 256, 32768 keys, "
+                               "Turbo k8v6 rows of N(0,1) vectors, all keys visible; 12 caches rotate past the MALL",
+                   "heads": H, "kv_heads": Hkv, "head_dim": D, "kv_len": L, "k_bits": KB, "v_bits": VB,
+                   "row_bytes": [krb, vrb]},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": measured_traffic("turbo"), "kernel": "all kernels of oom_attn_decode_turbo (sum)",
+                     "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
+    }
+    if not args.no_cpu:
+        import oracle
+
+        qn, kn, vn, mn = q.cpu().numpy(), caches[0][0].cpu().numpy(), caches[0][1].cpu().numpy(), mask.cpu().numpy()
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            oracle.attn_decode_turbo(qn, kn, vn, KB, VB, mn, H, Hkv, L, scale)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds and n >= 2:
+                break
+        res["cpu_baseline"] = {"value": el / n * 1e6, "unit": "us/step", "cores": 1, "kind": "port",
+                               "sample": f"{n} runs of the same attention step, oracle restatement of the reference's "
+                                         f"Turbo row decode and fp32 flash-decode arithmetic, one thread, on "
+                                         f"{cpu_model()}"}
     return res
 
 
@@ -884,7 +973,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "offload", "attn",
-                                                            "prefill", "gemv", "copy"])
+                                                            "turbo", "prefill", "gemv", "copy"])
     ap.add_argument("--prefill-precision", default="exact", choices=["exact", "bf16"],
                     help="activation precision of the prefill's down projection (the reference's ExpertPrecision)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -904,6 +993,8 @@ def main():
                "copies": args.steps + 1}
     elif args.config == "attn":
         res = bench_attn(args)
+    elif args.config == "turbo":
+        res = bench_turbo(args)
     elif args.config == "gemv":
         res = bench_gemv(args)
     elif args.config == "prefill":

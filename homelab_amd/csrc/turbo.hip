@@ -24,7 +24,7 @@
 
 #include <hip/hip_fp16.h>
 
-#include "common.hpp"
+#include "stream.hpp"
 
 namespace oom {
 
@@ -33,7 +33,6 @@ constexpr int TQ_LEVELS = 508;        // levels for 2..8 bits: 4 + 8 + ... + 256
 constexpr int TQ_MASK_THREADS = 1024; // mask_compact's block
 constexpr int TQ_G = 12;              // query heads a KV head (the decode kernel's instance)
 constexpr int TQ_D = 256;             // head_dim of the decode kernel
-constexpr int TQ_HW = 8;              // partials (32-lane halves) a block
 
 __host__ __device__ inline int kv_scale_bytes(int D) { return ((D / 32) * 2 + 15) & ~15; }
 __host__ __device__ inline int kv_row_bytes(int D, int bits) {
@@ -174,121 +173,631 @@ __device__ unsigned block_scan(unsigned v, unsigned* wsum) {
     return before + x;
 }
 
+// Nonzero bytes of a dword: each byte's bits or-ed down to its bit 0, then counted.
+__device__ __forceinline__ unsigned nonzero_bytes(uint32_t x) {
+    x |= x >> 4;
+    x |= x >> 2;
+    x |= x >> 1;
+    return __popc(x & 0x01010101u);
+}
+
+// Mask bytes 16 q .. 16 q + 15 (zeros past n): one 16-byte load, or byte loads for a last
+// chunk that ends past n (the buffer's bounds check works on whole dwords).
+__device__ __forceinline__ uint4 mask_chunk(__amdgpu_buffer_rsrc_t mr, int q, int n) {
+    if (16 * q + 16 <= n) return ld16(mr, 16 * q);
+    uint32_t w[4] = {0, 0, 0, 0};
+    for (int j = 0; 16 * q + j < n; j++)
+        w[j >> 2] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(mr, 16 * q + j, 0, 0) << (8 * (j & 3));
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // The positions j < n with mask[j] set, in order: sel[0] = count, sel[1 ..] = positions.
-// One block of TQ_MASK_THREADS; each thread takes a contiguous slice and a prefix count
+// One block of TQ_MASK_THREADS; each thread takes a contiguous run of 16-byte chunks
+// (one buffer load each, zeros past n), counts its visible bytes, and a block prefix sum
 // places its positions.
 __global__ void __launch_bounds__(TQ_MASK_THREADS) mask_compact_kernel(const uint8_t* __restrict__ mask,
                                                                        int32_t* __restrict__ sel, int n) {
     __shared__ unsigned wsum[TQ_MASK_THREADS / 64];
-    const int per = (n + (int)blockDim.x - 1) / (int)blockDim.x;
-    const int lo = min(n, (int)threadIdx.x * per), hi = min(n, lo + per);
+    const __amdgpu_buffer_rsrc_t mr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(mask), (short)0, n,
+                                                                        BUF_FLAGS);
+    const int nchunks = (n + 15) / 16;
+    const int per = (nchunks + (int)blockDim.x - 1) / (int)blockDim.x;
+    const int lo = min(nchunks, (int)threadIdx.x * per), hi = min(nchunks, lo + per);
     unsigned c = 0;
-    for (int j = lo; j < hi; j++) c += mask[j] != 0;
+    for (int q = lo; q < hi; q++) {
+        const uint4 x = mask_chunk(mr, q, n);
+        c += nonzero_bytes(x.x) + nonzero_bytes(x.y) + nonzero_bytes(x.z) + nonzero_bytes(x.w);
+    }
     const unsigned incl = block_scan(c, wsum);
     unsigned at = incl - c;
-    for (int j = lo; j < hi; j++)
-        if (mask[j]) sel[1 + at++] = j;
+    for (int q = lo; q < hi; q++) {
+        const uint4 x = mask_chunk(mr, q, n);
+        const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            if ((w[j >> 2] >> (8 * (j & 3))) & 0xff) sel[1 + at++] = 16 * q + j;
+    }
     if (threadIdx.x == blockDim.x - 1) sel[0] = (int32_t)incl;
 }
 
+// ---- decode attention (d = 256, 12 query heads a KV head) ------------------------------
+//
+// Work split: keys go in groups of 16 consecutive positions; wave w of a KV head's W waves
+// takes groups w, w + W, w + 2 W, ..., one a round, so a block-sparse mask
+// spreads over the waves. A key that is masked (or past kv_len) gets probability exactly 0
+// and its rows are not read: the result is the softmax over the visible keys with no
+// compaction pass. Each block merges its waves' online-softmax states in LDS and writes
+// one partial a head; attn_turbo_combine_kernel merges the blocks' partials by
+// max-rescale and rotates the result back.
+//
+// Matrix layout (v_mfma_f32_16x16x4f32, fp32 products and sums; lane l = 16 r + m):
+// scores are formed transposed, S^T[key][head] = K Q^T over 16 keys and 16 head rows (12
+// used), four coordinates a step. Lane (m, r) supplies key m's coordinates 64 r .. 64 r +
+// 63 (Turbo blocks 2 r and 2 r + 1) and head m's same coordinates, and ends holding
+// S^T[4 r + e][m] -- already the A operand P[m][4 r + e] of O = P V. There lane (m, r)
+// supplies V[4 r + e][16 m + t] (half block 16 m .. 16 m + 15) and holds
+// O[4 r + e][16 m + t], t < 16.
+//
+// Decoding: a lane takes a block's bit planes (word j holds bit j of the 32 codes) and
+// transposes them to one code a byte with three field swaps between plane pairs (about
+// 1.5 VALU operations a coordinate), then looks the level up in an LDS copy of the
+// codebook and multiplies by the block's scale -- the same f32 product as the reference's
+// per-coordinate decode.
+constexpr int TT_WAVES = 8;  // waves a block: two a SIMD, so one wave's MFMAs overlap the other's decoding
+constexpr int TT_GPW = 2;    // groups of 16 keys a wave is sized for (one a round)
+constexpr int TT_QS = 260;   // LDS row stride (floats) of a query head
+constexpr int TQ_OOB = 0x70000000;  // an offset past every buffer here: loads read 0
+constexpr int TC_THREADS = 1024;    // combine block: 4 slices of the partials x 256 coordinates
+constexpr int TC_BATCH = 32;        // partials a combine thread loads at once
+
+typedef float tq_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t tq_u2 __attribute__((ext_vector_type(2)));
+
 struct TurboArgs {
-    const float* q;       // [H, D] (rotated for a Turbo cache)
-    const uint8_t* k;     // rows [kv_len, Hkv] of kv_row_bytes(D, kb)
-    const uint8_t* v;     // rows [kv_len, Hkv] of kv_row_bytes(D, vb)
-    const int32_t* sel;   // count, then the visible positions
-    const float* levels;  // the codebook table (null for fp32 rows)
-    float* part;          // [Hkv, P, G, D + 2]: acc[D], m, l
-    float* out;           // [H, D]
-    int Hkv, P, kb, vb;
+    const float* q;       // [Hkv * 12, 256] as given
+    const uint8_t* k;     // rows [kv_len, Hkv] of kv_row_bytes(256, kb)
+    const uint8_t* v;     // rows [kv_len, Hkv] of kv_row_bytes(256, vb)
+    const uint8_t* mask;  // [kv_len], nonzero = visible
+    const float* levels;  // the codebook table (Turbo rows)
+    float* part;          // [Hkv, nblk, 12, 256]: a block's un-normalised output
+    float* ml;            // [Hkv, nblk, 12, 2]: its max and sum of exponentials
+    float* out;           // [Hkv * 12, 256]
+    int Hkv, kv_len, nblk, kb, vb;
     float scale;
 };
 
-// Flash-decode partials of one query token: partial p = 8 blockIdx.x + half-wave takes an
-// even share of the visible positions and all G query heads of KV head blockIdx.y.
-template <int G>
-__global__ void __launch_bounds__(256) attn_turbo_partial_kernel(TurboArgs a) {
-    constexpr int D = TQ_D, E = D / 32;  // coordinates a lane
-    __shared__ float qs[G][32][E];       // qs[g][lane][e] = q[g][32 e + lane]
-    __shared__ float lvk[256], lvv[256];
-    const int tid = threadIdx.x, lane = tid & 31, hw = tid >> 5;
-    const int kvh = blockIdx.y, p = blockIdx.x * TQ_HW + hw;
-    if (a.kb)
-        for (int t = tid; t < (1 << a.kb); t += blockDim.x) lvk[t] = a.levels[codebook_offset(a.kb) + t];
-    if (a.vb)
-        for (int t = tid; t < (1 << a.vb); t += blockDim.x) lvv[t] = a.levels[codebook_offset(a.vb) + t];
-    for (int t = tid; t < G * D; t += blockDim.x) {
-        const int g = t / D, d = t % D;
-        qs[g][d & 31][d >> 5] = a.q[(size_t)kvh * G * D + t];
-    }
-    __syncthreads();
-    const int krow = kv_row_bytes(D, a.kb), vrow = kv_row_bytes(D, a.vb);
-    float acc[G][E], m[G], l[G];
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tq_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, BUF_FLAGS);
+}
+
+// Position (in the order the score steps read) of coordinate c of a query head: within
+// each 32-coordinate block, column 8 i + k is read at step 4 k + i.
+__device__ __forceinline__ int tq_qperm(int c) { return (c & ~31) + 4 * (c & 7) + ((c >> 3) & 3); }
+
+// Swaps S-bit fields between two bit-plane words (the three stages of tq_codes).
+template <int S>
+__device__ __forceinline__ void tq_swap(uint32_t& a, uint32_t& b) {
+    constexpr uint32_t M = S == 1 ? 0x55555555u : S == 2 ? 0x33333333u : 0x0F0F0F0Fu;
+    const uint32_t na = (a & ~(M << S)) | ((b << S) & (M << S));
+    const uint32_t nb = (b & ~M) | ((a >> S) & M);
+    a = na;
+    b = nb;
+}
+// Bit-matrix transpose: on entry bit c of w[j] is bit j of column c's code; on exit byte
+// i of w[k] is the code of column 8 i + k.
+__device__ __forceinline__ void tq_codes(uint32_t (&w)[8]) {
+    tq_swap<1>(w[0], w[1]);
+    tq_swap<1>(w[2], w[3]);
+    tq_swap<1>(w[4], w[5]);
+    tq_swap<1>(w[6], w[7]);
+    tq_swap<2>(w[0], w[2]);
+    tq_swap<2>(w[1], w[3]);
+    tq_swap<2>(w[4], w[6]);
+    tq_swap<2>(w[5], w[7]);
+    tq_swap<4>(w[0], w[4]);
+    tq_swap<4>(w[1], w[5]);
+    tq_swap<4>(w[2], w[6]);
+    tq_swap<4>(w[3], w[7]);
+}
+
+// The N bit planes of a block at byte `off` (N < 0: `rn` planes, read as 8 words with the
+// surplus cleared); planes N .. 7 are zero.
+template <int N>
+__device__ __forceinline__ void tq_planes(__amdgpu_buffer_rsrc_t r, int off, int rn, uint32_t (&w)[8]) {
+    static_assert(N < 0 || N == 6 || N == 8, "plane counts with a load pattern");
+    const uint4 a = ld16(r, off);
+    w[0] = a.x;
+    w[1] = a.y;
+    w[2] = a.z;
+    w[3] = a.w;
+    if constexpr (N == 6) {
+        const tq_u2 b = __builtin_amdgcn_raw_buffer_load_b64(r, off + 16, 0, 0);
+        w[4] = b[0];
+        w[5] = b[1];
+        w[6] = 0;
+        w[7] = 0;
+    } else {
+        const uint4 b = ld16(r, off + 16);
+        w[4] = b.x;
+        w[5] = b.y;
+        w[6] = b.z;
+        w[7] = b.w;
+        if constexpr (N < 0) {
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < E; e++) acc[g][e] = 0.0f;
-    }
-    const int count = a.sel[0];
-    const int chunk = (count + a.P - 1) / a.P;
-    const int i0 = min(count, p * chunk), i1 = min(count, i0 + chunk);
-    for (int i = i0; i < i1; i++) {
-        const int j = a.sel[1 + i];
-        const uint8_t* kr = a.k + ((size_t)j * a.Hkv + kvh) * krow;
-        const uint8_t* vr = a.v + ((size_t)j * a.Hkv + kvh) * vrow;
-        float kk[E], vv[E];
-#pragma unroll
-        for (int e = 0; e < E; e++) {
-            kk[e] = kv_value(kr, 32 * e + lane, D, a.kb, lvk);
-            vv[e] = kv_value(vr, 32 * e + lane, D, a.vb, lvv);
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float dot = 0.0f;
-#pragma unroll
-            for (int e = 0; e < E; e++) dot = fmaf(qs[g][lane][e], kk[e], dot);
-            dot = half_xor_sum(dot);
-            const float s = dot * a.scale;
-            const float mn = fmaxf(m[g], s);
-            const float corr = expf(m[g] - mn);
-            const float w = expf(s - mn);
-            l[g] = l[g] * corr + w;
-#pragma unroll
-            for (int e = 0; e < E; e++) acc[g][e] = fmaf(acc[g][e], corr, w * vv[e]);
-            m[g] = mn;
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        float* o = a.part + (((size_t)kvh * a.P + p) * G + g) * (D + 2);
-#pragma unroll
-        for (int e = 0; e < E; e++) o[32 * e + lane] = acc[g][e];
-        if (lane == 0) {
-            o[D] = m[g];
-            o[D + 1] = l[g];
+            for (int j = 2; j < 8; j++)
+                if (j >= rn) w[j] = 0;
         }
     }
 }
 
-// out[h, d] = sum_p e^(m_p - M) acc_p[d] / sum_p e^(m_p - M) l_p over the partials of head
-// h (a partial with no keys has m = -inf and weight 0). One block per head, one thread per d.
-template <int G>
-__global__ void __launch_bounds__(TQ_D) attn_turbo_combine_kernel(TurboArgs a) {
-    constexpr int D = TQ_D;
-    const int h = blockIdx.x, d = threadIdx.x, kvh = h / G, g = h % G;
-    float M = -INFINITY;
-    for (int p = 0; p < a.P; p++) M = fmaxf(M, a.part[(((size_t)kvh * a.P + p) * G + g) * (D + 2) + D]);
-    float num = 0.0f, den = 0.0f;
-    for (int p = 0; p < a.P; p++) {
-        const float* pr = a.part + (((size_t)kvh * a.P + p) * G + g) * (D + 2);
-        const float mp = pr[D];
-        if (mp == -INFINITY) continue;
-        const float w = expf(mp - M);
-        num = fmaf(w, pr[d], num);
-        den = fmaf(w, pr[D + 1], den);
+__device__ __forceinline__ float tq_half(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffff)));
+}
+
+// A group's K rows as this lane needs them (see the layout above) ...
+template <int KB>
+struct TqK {
+    uint32_t w[2][8];  // bit planes of key m's blocks 2 r, 2 r + 1
+    uint32_t s;        // their fp16 scales
+};
+template <>
+struct TqK<0> {
+    float k[64];  // key m, coordinates 64 r ..
+};
+// ... and its V rows.
+template <int VB>
+struct TqV {
+    uint32_t w[4][8];  // bit planes of block m / 2 of keys 4 r + e
+    uint32_t s[4];     // that block's fp16 scale
+};
+template <>
+struct TqV<0> {
+    float v[4][16];  // keys 4 r + e, coordinates 16 m ..
+};
+
+// Issues this lane's loads of one group's K rows (tv: the group's visibility bits;
+// invisible keys read nothing).
+template <int KB>
+__device__ __forceinline__ void tq_load_k(TqK<KB>& t, const TurboArgs& a, __amdgpu_buffer_rsrc_t kr, int grp,
+                                          uint32_t tv, int m, int r, int kvh, int kb, int krb) {
+    const int kpos = 16 * grp + m;
+    const int krow = (tv >> m) & 1 ? (kpos * a.Hkv + kvh) * krb : TQ_OOB;
+    if constexpr (KB == 0) {
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const uint4 x = ld16(kr, krow + 256 * r + 16 * q);
+            t.k[4 * q] = __uint_as_float(x.x);
+            t.k[4 * q + 1] = __uint_as_float(x.y);
+            t.k[4 * q + 2] = __uint_as_float(x.z);
+            t.k[4 * q + 3] = __uint_as_float(x.w);
+        }
+    } else {
+        t.s = __builtin_amdgcn_raw_buffer_load_b32(kr, krow + 4 * r, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 2; b++) tq_planes<KB>(kr, krow + 16 + (2 * r + b) * kb * 4, kb, t.w[b]);
     }
-    a.out[(size_t)h * D + d] = num / den;
+}
+
+// ... and of its V rows.
+template <int VB>
+__device__ __forceinline__ void tq_load_v(TqV<VB>& t, const TurboArgs& a, __amdgpu_buffer_rsrc_t vr, int grp,
+                                          uint32_t tv, int m, int r, int kvh, int vb, int vrb) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int vpos = 16 * grp + 4 * r + e;
+        const int vrow = (tv >> (4 * r + e)) & 1 ? (vpos * a.Hkv + kvh) * vrb : TQ_OOB;
+        if constexpr (VB == 0) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 x = ld16(vr, vrow + 64 * m + 16 * q);
+                t.v[e][4 * q] = __uint_as_float(x.x);
+                t.v[e][4 * q + 1] = __uint_as_float(x.y);
+                t.v[e][4 * q + 2] = __uint_as_float(x.z);
+                t.v[e][4 * q + 3] = __uint_as_float(x.w);
+            }
+        } else {
+            t.s[e] = __builtin_amdgcn_raw_buffer_load_b16(vr, vrow + 2 * (m >> 1), 0, 0);
+            tq_planes<VB>(vr, vrow + 16 + (m >> 1) * vb * 4, vb, t.w[e]);
+        }
+    }
+}
+
+// The level of the code in byte i of w: one SDWA shift (byte select and times 4) forms
+// the byte offset into the codebook's LDS copy.
+__device__ __forceinline__ float tq_level(const float* tab, uint32_t w, int i) {
+    uint32_t off;
+    if (i == 0)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(off) : "v"(w));
+    else if (i == 1)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(off) : "v"(w));
+    else if (i == 2)
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(off) : "v"(w));
+    else
+        asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(off) : "v"(w));
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + off);
+}
+
+// S^T[4 r + e][m] of one group: 64 steps of four coordinates. A block's 32 levels are
+// looked up together before its 32 steps, so the LDS latency is paid once a block.
+template <int KB>
+__device__ __forceinline__ tq_f4 tq_scores(const TqK<KB>& t, const float (*qsp)[TT_QS], const float* lvk, int m,
+                                           int r) {
+    tq_f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        float kv[32];
+        if constexpr (KB == 0) {
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) kv[4 * k + i] = t.k[32 * b + 8 * i + k];
+        } else {
+            uint32_t w[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) w[j] = t.w[b][j];
+            tq_codes(w);
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) kv[4 * k + i] = tq_level(lvk, w[k], i);
+            const float sc = tq_half(t.s >> (16 * b));
+#pragma unroll
+            for (int j = 0; j < 32; j++) kv[j] *= sc;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const tq_f4 q4 = *reinterpret_cast<const tq_f4*>(&qsp[m][64 * r + 32 * b + 4 * k]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[4 * k + i], q4[i], c, 0, 0, 0);
+        }
+    }
+    return c;
+}
+
+// o[t] += P V over one group: p[e] = P[m][4 r + e]. A key pair's 32 levels are looked up
+// together before its 32 steps.
+template <int VB>
+__device__ __forceinline__ void tq_pv(const TqV<VB>& t, const float (&p)[4], tq_f4 (&o)[16], const float* lvv, int m) {
+    const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;  // this lane's 16-bit half of each plane
+#pragma unroll
+    for (int pr = 0; pr < 2; pr++) {
+        const int e0 = 2 * pr, e1 = e0 + 1;
+        float v0[16], v1[16];
+        if constexpr (VB == 0) {
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                v0[c] = t.v[e0][c];
+                v1[c] = t.v[e1][c];
+            }
+        } else {
+            uint32_t w[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) w[j] = __builtin_amdgcn_perm(t.w[e1][j], t.w[e0][j], sel);
+            tq_codes(w);
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                v0[c] = tq_level(lvv, w[c & 7], c >> 3);
+                v1[c] = tq_level(lvv, w[c & 7], 2 + (c >> 3));
+            }
+            const float s0 = tq_half(t.s[e0]), s1 = tq_half(t.s[e1]);
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                v0[c] *= s0;
+                v1[c] *= s1;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[e0], v0[c], o[c], 0, 0, 0);
+            o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[e1], v1[c], o[c], 0, 0, 0);
+        }
+    }
+}
+
+// Mask byte of key (lane & 15) of round rho's group (0 past kv_len); the group's
+// visibility bits are the ballot of the 16 bytes, taken when they are needed so that no
+// earlier wait covers the load.
+__device__ __forceinline__ uint32_t tq_mask_byte(__amdgpu_buffer_rsrc_t mr, int kv_len, int ngroups, int wv, int W,
+                                                 int rho, int lane) {
+    const int grp = wv + rho * W, pos = 16 * grp + (lane & 15);
+    const bool ok = lane < 16 && grp < ngroups && pos < kv_len;
+    return __builtin_amdgcn_raw_buffer_load_b8(mr, ok ? pos : TQ_OOB, 0, 0);
+}
+__device__ __forceinline__ uint32_t tq_ballot(uint32_t b) { return (uint32_t)__ballot(b != 0); }
+
+struct TqLds {
+    float lvk[256], lvv[256];                                  // codebooks of the K and V rows
+    __attribute__((aligned(16))) float qsp[16][TT_QS];          // queries in score-step order
+    float red[TT_WAVES][TQ_G][2];                               // each wave's max and sum a head
+    __attribute__((aligned(16))) float osum[TT_WAVES][TQ_G][TQ_D];  // each wave's rescaled output
+};
+
+// The online softmax keeps a reference maximum per head and moves it only when a score
+// exceeds it by more than TQ_TAU (natural-log units): the exponentials stay below e^8 and
+// the accumulated output is rescaled rarely instead of every round.
+constexpr float TQ_TAU = 8.0f;
+
+template <int KB, int VB>
+__global__ void __launch_bounds__(TT_WAVES * 64) attn_turbo_kernel(TurboArgs a) {
+    constexpr bool ROT = KB != 0;
+    constexpr int D = TQ_D, G = TQ_G;
+    // one LDS object with the codebooks first: their addresses are constants that fold
+    // into the lookups' offset field
+    __shared__ TqLds sm;
+    float* lvk = sm.lvk;
+    float* lvv = sm.lvv;
+    float(*qsp)[TT_QS] = sm.qsp;
+    float(*red)[G][2] = sm.red;
+    float(*osum)[G][D] = sm.osum;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, r = lane >> 4;
+    const int kvh = blockIdx.y;
+    const int kb = KB >= 0 ? KB : a.kb, vb = VB >= 0 ? VB : a.vb;
+    const int krb = kv_row_bytes(D, kb), vrb = kv_row_bytes(D, vb);
+    const int W = a.nblk * TT_WAVES, wv = blockIdx.x * TT_WAVES + wave;
+    const int ngroups = (a.kv_len + 15) >> 4;
+    const __amdgpu_buffer_rsrc_t mr = tq_rsrc(a.mask, a.kv_len);
+    const __amdgpu_buffer_rsrc_t kr = tq_rsrc(a.k, a.kv_len * a.Hkv * krb);
+    const __amdgpu_buffer_rsrc_t vr = tq_rsrc(a.v, a.kv_len * a.Hkv * vrb);
+
+    // the small loads first (the first two rounds' mask bytes, this wave's query heads,
+    // the codebooks), branch-free; the first round's rows go out as soon as its mask bytes
+    // are in, and their latency hides behind the query rotation
+    const __amdgpu_buffer_rsrc_t qr = tq_rsrc(a.q + (size_t)kvh * G * D, G * D * 4);
+    const uint32_t b0 = tq_mask_byte(mr, a.kv_len, ngroups, wv, W, 0, lane);
+    const uint32_t b1 = tq_mask_byte(mr, a.kv_len, ngroups, wv, W, 1, lane);
+    // wave w rotates heads w and w + 8 (rows 12 .. 15 are zero); lane l holds coordinates
+    // 4 l .. 4 l + 3
+    uint4 qh[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int h = wave + TT_WAVES * j;
+        qh[j] = ld16(qr, h < G ? (h * D + 4 * lane) * 4 : TQ_OOB);
+    }
+    float lk = 0.0f, lv = 0.0f;
+    if constexpr (ROT) {
+        const __amdgpu_buffer_rsrc_t lr = tq_rsrc(a.levels, TQ_LEVELS * 4);
+        lk = ldf(lr, tid < (1 << kb) ? (codebook_offset(kb) + tid) * 4 : TQ_OOB);
+        lv = ldf(lr, tid < (1 << vb) ? (codebook_offset(vb) + tid) * 4 : TQ_OOB);
+    }
+    uint32_t vis = tq_ballot(b0);
+    TqK<KB> kbuf0, kbuf1;
+    TqV<VB> vbuf;
+    tq_load_k(kbuf0, a, kr, wv, vis, m, r, kvh, kb, krb);
+    tq_load_v(vbuf, a, vr, wv, vis, m, r, kvh, vb, vrb);
+    uint32_t vnext = tq_ballot(b1);
+
+    if constexpr (ROT) {
+        if (tid < 256) {
+            lvk[tid] = lk;
+            lvv[tid] = lv;
+        }
+    }
+    // a rotated cache gets rotated queries: signs, then the Walsh-Hadamard butterflies in
+    // the rotation's order (stages 1, 2 inside a lane, 4 .. 128 across lanes l ^ 1 ..
+    // l ^ 32); the 1/16 normalisation is folded into the score scale (a power of two:
+    // exact). The result goes to LDS in the order the score steps read it.
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        float x[4] = {__uint_as_float(qh[j].x), __uint_as_float(qh[j].y), __uint_as_float(qh[j].z),
+                      __uint_as_float(qh[j].w)};
+        if constexpr (ROT) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) x[i] *= kv_sign(4 * lane + i);
+            float y0 = x[0] + x[1], y1 = x[0] - x[1], y2 = x[2] + x[3], y3 = x[2] - x[3];
+            x[0] = y0 + y2;
+            x[2] = y0 - y2;
+            x[1] = y1 + y3;
+            x[3] = y1 - y3;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const bool upper = lane & o;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float y = __shfl_xor(x[i], o);
+                    x[i] = upper ? y - x[i] : x[i] + y;
+                }
+            }
+        }
+        const int h = wave + TT_WAVES * j;
+#pragma unroll
+        for (int i = 0; i < 4; i++) qsp[h][tq_qperm(4 * lane + i)] = x[i];
+    }
+    __syncthreads();
+    const float scale = ROT ? a.scale * (1.0f / 16.0f) : a.scale;
+
+    tq_f4 o[16];
+#pragma unroll
+    for (int c = 0; c < 16; c++) o[c] = tq_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float mrun = -INFINITY, lrun = 0.0f;  // reference maximum and sum of exponentials, head m
+    // A round: the next group's K rows go out (into the other K buffer); this group's
+    // scores; the online softmax; P V; the V buffer takes the next group's V rows. fp32
+    // rows (four times the registers) keep one K buffer, refilled after the scores.
+    constexpr bool KDB = KB != 0;
+    auto round = [&](int rho, const TqK<KB>& kcur, TqK<KB>& knext) {
+        const uint32_t bnn = tq_mask_byte(mr, a.kv_len, ngroups, wv, W, rho + 2, lane);
+        if constexpr (KDB) tq_load_k(knext, a, kr, wv + (rho + 1) * W, vnext, m, r, kvh, kb, krb);
+        tq_f4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (vis) sc = tq_scores(kcur, qsp, lvk, m, r);
+        if constexpr (!KDB) tq_load_k(knext, a, kr, wv + (rho + 1) * W, vnext, m, r, kvh, kb, krb);
+        float s[4], mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            s[e] = (vis >> (4 * r + e)) & 1 ? sc[e] * scale : -INFINITY;
+            mx = fmaxf(mx, s[e]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const bool grow = mx > mrun + TQ_TAU;  // (true for the first visible keys: mrun = -inf)
+        if (__ballot(grow)) {
+            const float mnew = grow ? mx : mrun;
+            const float corr = grow ? __expf(mrun - mnew) : 1.0f;  // 0 from -inf
+            lrun *= corr;
+            if (__ballot(grow && mrun != -INFINITY)) {  // o is still zero while mrun is -inf
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float ce = __shfl(corr, 4 * r + e);
+#pragma unroll
+                    for (int c = 0; c < 16; c++) o[c][e] *= ce;
+                }
+            }
+            mrun = mnew;
+        }
+        float p[4], ls = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            p[e] = s[e] == -INFINITY ? 0.0f : __expf(s[e] - mrun);
+            ls += p[e];
+        }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        lrun += ls;
+        if (vis) tq_pv(vbuf, p, o, lvv, m);
+        tq_load_v(vbuf, a, vr, wv + (rho + 1) * W, vnext, m, r, kvh, vb, vrb);
+        vis = vnext;
+        vnext = tq_ballot(bnn);
+    };
+    if constexpr (KDB) {
+        for (int rho = 0; wv + rho * W < ngroups; rho += 2) {
+            round(rho, kbuf0, kbuf1);
+            if (wv + (rho + 1) * W >= ngroups) break;
+            round(rho + 1, kbuf1, kbuf0);
+        }
+    } else {
+        for (int rho = 0; wv + rho * W < ngroups; rho++) round(rho, kbuf0, kbuf0);
+    }
+
+    // merge the block's waves: rescale each to the block max, sum in a fixed order
+    if (r == 0 && m < G) {
+        red[wave][m][0] = mrun;
+        red[wave][m][1] = lrun;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int h = 4 * r + e;
+        if (h < G) {
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < TT_WAVES; w++) M = fmaxf(M, red[w][h][0]);
+            const float mw = red[wave][h][0];
+            const float f = mw == -INFINITY ? 0.0f : __expf(mw - M);
+#pragma unroll
+            for (int c4 = 0; c4 < 4; c4++) {
+                const tq_f4 y = {o[4 * c4][e] * f, o[4 * c4 + 1][e] * f, o[4 * c4 + 2][e] * f, o[4 * c4 + 3][e] * f};
+                *reinterpret_cast<tq_f4*>(&osum[wave][h][16 * m + 4 * c4]) = y;
+            }
+        }
+    }
+    __syncthreads();
+    float* part = a.part + ((size_t)kvh * a.nblk + blockIdx.x) * G * D;
+    for (int u = tid; u < G * D; u += blockDim.x) {
+        const int h = u / D, c = u % D;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < TT_WAVES; w++) s += osum[w][h][c];
+        part[u] = s;
+    }
+    if (tid < G) {
+        float M = -INFINITY, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < TT_WAVES; w++) M = fmaxf(M, red[w][tid][0]);
+#pragma unroll
+        for (int w = 0; w < TT_WAVES; w++) {
+            const float mw = red[w][tid][0];
+            if (mw != -INFINITY) L += __expf(mw - M) * red[w][tid][1];
+        }
+        float* ml = a.ml + (((size_t)kvh * a.nblk + blockIdx.x) * G + tid) * 2;
+        ml[0] = M;
+        ml[1] = L;
+    }
+}
+
+// out[h] = sum_b e^(m_b - M) O_b / sum_b e^(m_b - M) l_b over the blocks' partials of head
+// h (a block with no visible key has m = -inf and weight 0), rotated back for a Turbo
+// cache (x = s . (H y) / 16). One block of 1024 threads a head: four slices of the
+// partials by 256 coordinates, each thread's loads in flight together.
+template <bool ROT>
+__global__ void __launch_bounds__(TC_THREADS) attn_turbo_combine_kernel(TurboArgs a) {
+    constexpr int D = TQ_D, G = TQ_G, SL = TC_THREADS / D;
+    __shared__ float wt[256];
+    __shared__ float rm[TC_THREADS / 64], rl[TC_THREADS / 64];
+    __shared__ float acc[SL][D];
+    const int h = blockIdx.x, kvh = h / G, g = h % G, tid = threadIdx.x, n = a.nblk;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int d = tid % D, sl = tid / D;
+    const __amdgpu_buffer_rsrc_t pr = tq_rsrc(a.part + (size_t)kvh * n * G * D, n * G * D * 4);
+    // the first TC_BATCH partials of this thread go out with the maxima and sums: one
+    // memory round trip for both
+    float x[TC_BATCH];
+#pragma unroll
+    for (int j = 0; j < TC_BATCH; j++) {
+        const int p = sl + SL * j;
+        x[j] = ldf(pr, p < n ? ((p * G + g) * D + d) * 4 : TQ_OOB);
+    }
+    const __amdgpu_buffer_rsrc_t mlr = tq_rsrc(a.ml + (size_t)kvh * n * G * 2, n * G * 2 * 4);
+    const float mld = ldf(mlr, tid < n ? (tid * G + g) * 8 : TQ_OOB);
+    const float lp = ldf(mlr, tid < n ? (tid * G + g) * 8 + 4 : TQ_OOB);
+    const float mp = tid < n ? mld : -INFINITY;
+    float M = wave_max(mp);
+    if (lane == 0) rm[wave] = M;
+    __syncthreads();
+    M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < TC_THREADS / 64; w++) M = fmaxf(M, rm[w]);
+    const float wp = mp == -INFINITY ? 0.0f : __expf(mp - M);
+    if (tid < 256) wt[tid] = wp;  // zero for tid >= n
+    float den = wave_sum(wp * lp);
+    if (lane == 0) rl[wave] = den;
+    __syncthreads();
+    den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < TC_THREADS / 64; w++) den += rl[w];
+    float num = 0.0f;
+#pragma unroll
+    for (int j = 0; j < TC_BATCH; j++) num = fmaf(wt[sl + SL * j], x[j], num);
+    for (int p0 = sl + SL * TC_BATCH; p0 < n; p0 += SL * TC_BATCH) {
+#pragma unroll
+        for (int j = 0; j < TC_BATCH; j++) {
+            const int p = p0 + SL * j;
+            x[j] = ldf(pr, p < n ? ((p * G + g) * D + d) * 4 : TQ_OOB);
+        }
+#pragma unroll
+        for (int j = 0; j < TC_BATCH; j++) {
+            const int p = p0 + SL * j;
+            num = fmaf(wt[p < n ? p : 0], x[j], num);
+        }
+    }
+    acc[sl][d] = num;
+    __syncthreads();
+    if (tid < D) {
+        float y = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SL; s++) y += acc[s][d];
+        acc[0][d] = y / den;
+    }
+    if constexpr (ROT) {
+        // the block's first D threads run the butterflies (tq_wht synchronises the block)
+        float* s = acc[0];
+        for (int hs = 1; hs < D; hs <<= 1) {
+            __syncthreads();
+            if (tid < D && (tid & hs) == 0) {
+                const float x0 = s[tid], x1 = s[tid + hs];
+                s[tid] = x0 + x1;
+                s[tid + hs] = x0 - x1;
+            }
+        }
+        __syncthreads();
+        if (tid < D) a.out[(size_t)h * D + tid] = s[tid] * kv_sign(tid) * (1.0f / 16.0f);
+    } else {
+        __syncthreads();
+        if (tid < D) a.out[(size_t)h * D + tid] = acc[0][tid];
+    }
 }
 
 // ---- host ---------------------------------------------------------------------------
@@ -357,25 +866,27 @@ static bool kv_row_shape(int d, int bits) {
     return d >= 32 && d % 32 == 0 && d <= TQ_MAXD && (bits == 0 || ((d & (d - 1)) == 0 && bits >= 2 && bits <= 8));
 }
 
-// Partials of the decode attention: about 16 visible keys each, at most 4096 keys
-// counted, a multiple of the block's 8 (attention.rs:417-419).
-static int turbo_partials(int kv_len) {
-    const int p = (std::min(kv_len, 4096) + 15) / 16;
-    return (p + TQ_HW - 1) / TQ_HW * TQ_HW;
+// Blocks a KV head of the decode attention: enough that every wave has TT_GPW groups of
+// 16 keys, at most 256 blocks over all KV heads (one a CU).
+static int turbo_blocks(int kv_len, int kv_heads) {
+    const int groups = (kv_len + 15) / 16;
+    const int want = (groups + TT_WAVES * TT_GPW - 1) / (TT_WAVES * TT_GPW);
+    return std::max(1, std::min(want, std::max(1, 256 / kv_heads)));
 }
 
 struct TurboWs {
-    size_t sel, qrot, part, total;
+    size_t part, ml, total;
+    int nblk;
 };
 
 static size_t t_al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-static TurboWs turbo_ws(int heads, int kv_heads, int d, int kv_len) {
+static TurboWs turbo_ws(int kv_heads, int kv_len) {
     TurboWs w;
-    w.sel = 0;
-    w.qrot = t_al256((size_t)(kv_len + 1) * 4);
-    w.part = w.qrot + t_al256((size_t)heads * d * 4);
-    w.total = w.part + t_al256((size_t)kv_heads * turbo_partials(kv_len) * (heads / kv_heads) * (d + 2) * 4);
+    w.nblk = turbo_blocks(kv_len, kv_heads);
+    w.part = 0;
+    w.ml = t_al256((size_t)kv_heads * w.nblk * TQ_G * TQ_D * 4);
+    w.total = w.ml + t_al256((size_t)kv_heads * w.nblk * TQ_G * 2 * 4);
     return w;
 }
 
@@ -437,14 +948,14 @@ extern "C" int oom_kv_read(const uint8_t* cache, float* dst, int len, int kv_hea
 
 extern "C" int oom_mask_compact(const uint8_t* mask, int32_t* sel, int n, void* stream) {
     using namespace oom;
-    OOM_REQUIRE(n >= 0 && mask && sel, "oom_mask_compact: null buffer or negative length");
+    OOM_REQUIRE(n >= 0 && n < 0x7fff0000 && mask && sel, "oom_mask_compact: null buffer or length out of range");
     hipLaunchKernelGGL(mask_compact_kernel, dim3(1), dim3(TQ_MASK_THREADS), 0, as_stream(stream), mask, sel, n);
     return launched("oom_mask_compact");
 }
 
 extern "C" size_t oom_attn_decode_turbo_workspace_size(int heads, int kv_heads, int d, int kv_len) {
     if (heads < 1 || kv_heads < 1 || d < 1 || kv_len < 1 || heads % kv_heads) return 0;
-    return oom::turbo_ws(heads, kv_heads, d, kv_len).total;
+    return oom::turbo_ws(kv_heads, kv_len).total;
 }
 
 extern "C" int oom_attn_decode_turbo(const float* q, const uint8_t* k, const uint8_t* v, int k_bits, int v_bits,
@@ -456,46 +967,37 @@ extern "C" int oom_attn_decode_turbo(const float* q, const uint8_t* k, const uin
     OOM_REQUIRE(kv_row_shape(d, k_bits) && kv_row_shape(d, v_bits) && (k_bits == 0) == (v_bits == 0),
                 "oom_attn_decode_turbo: k_bits and v_bits both 0 (fp32) or both 2..8");
     OOM_REQUIRE(kv_len >= 1, "oom_attn_decode_turbo: kv_len must be >= 1");
-    OOM_REQUIRE((int64_t)kv_len * kv_heads * kv_row_bytes(d, std::max(k_bits, v_bits)) < (1ll << 40),
-                "oom_attn_decode_turbo: cache too large");
+    OOM_REQUIRE((int64_t)kv_len * kv_heads * kv_row_bytes(d, std::max(k_bits, v_bits)) < TQ_OOB,
+                "oom_attn_decode_turbo: cache too large (rows of one cache under 1.75 GiB)");
     OOM_REQUIRE(q && k && v && mask && out && (k_bits == 0 || levels), "oom_attn_decode_turbo: null buffer");
-    const TurboWs w = turbo_ws(heads, kv_heads, d, kv_len);
+    const TurboWs w = turbo_ws(kv_heads, kv_len);
     if (!ws || ws_bytes < w.total)
         return fail(OOM_ERR_WORKSPACE,
                     "oom_attn_decode_turbo: workspace smaller than oom_attn_decode_turbo_workspace_size()");
     OOM_REQUIRE(aligned(ws, 256), "oom_attn_decode_turbo: workspace must be 256-byte aligned");
     uint8_t* base = reinterpret_cast<uint8_t*>(ws);
     hipStream_t st = as_stream(stream);
-    const bool rotated = k_bits != 0;
     TurboArgs a{};
     a.q = q;
-    if (rotated) {
-        float* qr = reinterpret_cast<float*>(base + w.qrot);
-        if (hipMemcpyAsync(qr, q, (size_t)heads * d * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
-            return launched("oom_attn_decode_turbo");
-        hipLaunchKernelGGL(kv_rotate_kernel, dim3((unsigned)heads), dim3(d), 0, st, qr, d, 0);
-        if (int rc = launched("oom_attn_decode_turbo")) return rc;
-        a.q = qr;
-    }
-    int32_t* sel = reinterpret_cast<int32_t*>(base + w.sel);
-    hipLaunchKernelGGL(mask_compact_kernel, dim3(1), dim3(TQ_MASK_THREADS), 0, st, mask, sel, kv_len);
-    if (int rc = launched("oom_attn_decode_turbo")) return rc;
     a.k = k;
     a.v = v;
-    a.sel = sel;
+    a.mask = mask;
     a.levels = levels;
     a.part = reinterpret_cast<float*>(base + w.part);
+    a.ml = reinterpret_cast<float*>(base + w.ml);
     a.out = out;
     a.Hkv = kv_heads;
-    a.P = turbo_partials(kv_len);
+    a.kv_len = kv_len;
+    a.nblk = w.nblk;
     a.kb = k_bits;
     a.vb = v_bits;
     a.scale = scale;
-    hipLaunchKernelGGL(attn_turbo_partial_kernel<TQ_G>, dim3((unsigned)(a.P / TQ_HW), (unsigned)kv_heads), dim3(256), 0,
-                       st, a);
+    const dim3 grid((unsigned)w.nblk, (unsigned)kv_heads), block(TT_WAVES * 64);
+    if (k_bits == 0) hipLaunchKernelGGL((attn_turbo_kernel<0, 0>), grid, block, 0, st, a);
+    else if (k_bits == 8 && v_bits == 6) hipLaunchKernelGGL((attn_turbo_kernel<8, 6>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((attn_turbo_kernel<-1, -1>), grid, block, 0, st, a);
     if (int rc = launched("oom_attn_decode_turbo")) return rc;
-    hipLaunchKernelGGL(attn_turbo_combine_kernel<TQ_G>, dim3((unsigned)heads), dim3(TQ_D), 0, st, a);
-    if (int rc = launched("oom_attn_decode_turbo")) return rc;
-    if (rotated) hipLaunchKernelGGL(kv_rotate_kernel, dim3((unsigned)heads), dim3(d), 0, st, out, d, 1);
+    if (k_bits == 0) hipLaunchKernelGGL(attn_turbo_combine_kernel<false>, dim3((unsigned)heads), dim3(TC_THREADS), 0, st, a);
+    else hipLaunchKernelGGL(attn_turbo_combine_kernel<true>, dim3((unsigned)heads), dim3(TC_THREADS), 0, st, a);
     return launched("oom_attn_decode_turbo");
 }
