@@ -66,6 +66,8 @@ SIGNATURES = {
     "oom_moe_grouped_gemm_fp8": (I32, [P, P, P, I32, I32, P, P, I32, P, I64, I64, I64, I64, P]),
     "oom_moe_prefill_fp8_workspace_size": (SZ, [I32, I32, I32, P]),
     "oom_moe_prefill_fp8": (I32, [P, P, I32, P, I32, I32, I32, P, I32, P, P, P, I32, P, SZ, P]),
+    "oom_moe_tiled_nvfp4": (I32, [P, P, P, I32, I32, P, P, I32, I32, I64, I64, I32, I32, P]),
+    "oom_moe_swiglu_range": (I32, [P, P, P, I64, I64, P]),
     "oom_attn_decode_workspace_size": (SZ, [I32, I32, I32, I32]),
     "oom_attn_decode_paged": (I32, [P, I32, P, P, P, I32, I32, I32, I32, I32, I32, F, P, I32, P, SZ, P]),
     "oom_kv_codebook_size": (SZ, []),
@@ -407,6 +409,17 @@ def moe_prefill_fp8(logits, x, all_recs, k: int, geo: Fp8Record, ids, weights, o
     check(lib().oom_moe_prefill_fp8(_ptr(logits), _ptr(x), _dtype_code(x), _ptr(all_recs), T, E, k, ctypes.byref(geo),
                                     precision, _ptr(ids), _ptr(weights), _ptr(out), _dtype_code(out), _ptr(ws),
                                     ws.numel() * ws.element_size(), _stream(stream)))
+
+
+def moe_tiled_nvfp4(recs, off, rows, n_experts: int, max_per_expert: int, x, y, n: int, k: int, w_off: int,
+                    s_off: int, s2_idx: int, precision: int = EXPERT_EXACT, stream=None) -> None:
+    """y f32 [A, n] = x[row(a)] . W_e^T for one NVFP4 projection (w_off, s_off, s2_idx)."""
+    check(lib().oom_moe_tiled_nvfp4(_ptr(recs), _ptr(off), _ptr(rows), n_experts, max_per_expert, _ptr(x), _ptr(y), n,
+                                    k, w_off, s_off, s2_idx, precision, _stream(stream)))
+
+
+def moe_swiglu_range(g, u, h, start: int, end: int, stream=None) -> None:
+    check(lib().oom_moe_swiglu_range(_ptr(g), _ptr(u), _ptr(h), start, end, _stream(stream)))
 
 
 # ---- copies beside compute: the Transfer trait (crates/oominf-core/src/backend.rs:945-1018) ----

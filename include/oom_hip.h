@@ -282,6 +282,26 @@ int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dtype, const u
                         int k, const OomFp8Record* geo, int precision, int32_t* ids, float* weights, void* out,
                         int out_dtype, void* ws, size_t ws_bytes, void* stream);
 
+/* Tiled grouped GEMM of one NVFP4 projection (prefill): y[a, r] = x[row(a)] . W_e[r] for
+ * the assignments a in [off[e], off[e + 1]) of each of n_experts experts, row(a) = rows[a]
+ * (rows null: a), W_e the projection (codes at byte w_off, e4m3 scales at byte s_off,
+ * weight_scale_2 at float s2_idx of expert e's record recs[e]; layout
+ * nvfp4-modelopt-g16, n rows of k inputs), decoded exactly to bf16 with scale_2 applied
+ * to the fp32 result. x f32 [*, k] (16-byte aligned); y f32 [A, n]. precision
+ * OOM_EXPERT_EXACT splits x into three exact bf16 terms (an fp32 GEMM in another
+ * summation order); OOM_EXPERT_BF16 rounds x to bf16 (one matrix-core pass). k a
+ * multiple of 32; max_per_expert bounds any expert's assignment count (the grid).
+ * Replaces Experts::moe_tiled (crates/oominf-core/src/backend.rs:869-886;
+ * crates/oominf-cuda/src/experts.rs:214-267; crates/oominf-cuda/kernels/moe.cu:166-335). */
+int oom_moe_tiled_nvfp4(const uint64_t* recs, const int32_t* off, const int32_t* rows, int n_experts,
+                        int max_per_expert, const float* x, float* y, int n, int k, int64_t w_off, int64_t s_off,
+                        int s2_idx, int precision, void* stream);
+
+/* h[i] = silu(g[i]) * u[i] for i in [start, end), silu(v) = v / (1 + e^-v), fp32.
+ * Replaces Experts::moe_swiglu_range (crates/oominf-core/src/backend.rs:887-895;
+ * crates/oominf-cuda/src/experts.rs:269-299; crates/oominf-cuda/kernels/moe.cu:338-341). */
+int oom_moe_swiglu_range(const float* g, const float* u, float* h, int64_t start, int64_t end, void* stream);
+
 /* Paged GQA decode attention for one query token: out[h, :] = sum_j softmax_j(q_h . k_j
  * * scale) v_j over the kv_len keys, query head h reading KV head h / (heads / kv_heads).
  * q [heads, d] in q_dtype; k_pages and v_pages bf16 [n_pages, page_size, kv_heads, d]

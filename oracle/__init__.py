@@ -149,6 +149,7 @@ def lib() -> ctypes.CDLL:
             "oracle_kv_read": (None, [P, P, I32, I32, I32, P]),
             "oracle_mask_compact": (I32, [P, P, I32]),
             "oracle_attn_decode_turbo": (None, [P, P, P, I32, I32, P, P, I32, I32, I32, F, P]),
+            "oracle_moe_tiled_nvfp4": (None, [P, P, P, I32, P, P, I64, I64, I64, I64, I32, I32]),
             "oracle_host_has_avx512": (I32, []),
         }
         for name, (res, args) in sig.items():
@@ -425,6 +426,19 @@ def moe_gate_up_nvfp4(recs, off, assign_tok, x: np.ndarray, geo: Nvfp4Record) ->
                                    _p(np.ascontiguousarray(assign_tok, dtype=np.int32)), len(recs), _p(x), _p(h),
                                    ctypes.byref(geo))
     return h
+
+
+def moe_tiled_nvfp4(recs, off, rows, x: np.ndarray, N: int, K: int, w_off: int, s_off: int, s2_idx: int,
+                    terms: int) -> np.ndarray:
+    """y f32 [A, N] of one NVFP4 projection over host records (uint8 arrays), x f32 [*, K]."""
+    off = np.ascontiguousarray(off, dtype=np.int32)
+    A = int(off[-1])
+    y = np.zeros((A, N), dtype=np.float32)
+    tab = _ptrs(recs) if len(recs) else np.zeros(1, dtype=np.uint64)
+    lib().oracle_moe_tiled_nvfp4(_p(tab), _p(off), None if rows is None else _p(np.ascontiguousarray(rows, np.int32)),
+                                 len(recs), _p(np.ascontiguousarray(x, dtype=np.float32)), _p(y), N, K, w_off, s_off,
+                                 s2_idx, terms)
+    return y
 
 
 def moe_down_nvfp4(recs, off, h: np.ndarray, geo: Nvfp4Record) -> np.ndarray:

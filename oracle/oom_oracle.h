@@ -151,6 +151,12 @@ void oracle_moe_gate_up_nvfp4(const uint8_t* const* recs, const int32_t* off, co
                               const float* x, float* h, const OomNvfp4Record* geo);
 void oracle_moe_down_nvfp4(const uint8_t* const* recs, const int32_t* off, int n_e, const float* h, float* y,
                            const OomNvfp4Record* geo);
+/* The tiled NVFP4 grouped GEMM of one projection (moe.cu:166-335): y[a, r] = x[row(a)] .
+ * W_e[r] * s2 with x as `terms` bf16 terms (3: exact, 1: x rounded to bf16), fp32 sums;
+ * rows null: row(a) = a. x [*, K]; y [A, N]. */
+void oracle_moe_tiled_nvfp4(const uint8_t* const* recs, const int32_t* off, const int32_t* rows, int n_e,
+                            const float* x, float* y, int64_t N, int64_t K, int64_t w_off, int64_t s_off, int s2_idx,
+                            int terms);
 /* The whole routed decode step over NVFP4 records (router, plan, gate/up, down, combine). */
 int oracle_moe_decode_nvfp4(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
                             const OomNvfp4Record* geo, int32_t* ids, float* weights, float* out);

@@ -304,6 +304,51 @@ void oracle_moe_down_nvfp4(const uint8_t* const* recs, const int32_t* off, int n
     }
 }
 
+/* The tiled NVFP4 grouped GEMM of one projection (moe_tiled, crates/oominf-cuda/kernels/
+ * moe.cu:166-335): y[a, r] = (sum_c sum_p term_p(x[row(a), c]) * w(r, c)) * s2, with
+ * w(r, c) = e2m1(code) * e4m3(scale) exact (at most 6 significant bits: a bf16 value) and
+ * x split into `terms` bf16 terms, hi = bf16(x), each next term bf16 of the remainder
+ * (moe.cu:263-273; with three terms they sum to x exactly). The products are exact in
+ * fp32 and summed in fp32, term-major within each 16-column group and the groups in
+ * column order (the reference's tensor-core passes sum in their own order). The
+ * weight_scale_2 scalar sits at float s2_idx of the record. */
+void oracle_moe_tiled_nvfp4(const uint8_t* const* recs, const int32_t* off, const int32_t* rows, int n_e,
+                            const float* x, float* y, int64_t N, int64_t K, int64_t w_off, int64_t s_off, int s2_idx,
+                            int terms) {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+    float* xt = (float*)malloc(sizeof(float) * (size_t)K * 3);
+    for (int e = 0; e < n_e; e++) {
+        const uint8_t* rec = recs[e];
+        float s2 = rec_f32(rec, s2_idx);
+        for (int a = off[e]; a < off[e + 1]; a++) {
+            const float* xr = x + (size_t)(rows ? rows[a] : a) * K;
+            for (int64_t c = 0; c < K; c++) {
+                float rem = xr[c];
+                for (int p = 0; p < terms; p++) {
+                    float tp = oracle_bf16_to_f32(oracle_bf16_from_f32(rem));
+                    xt[(size_t)p * K + c] = tp;
+                    rem -= tp;
+                }
+            }
+            for (int64_t r = 0; r < N; r++) {
+                const uint8_t* cw = rec + w_off + r * K / 2;
+                const uint8_t* sc = rec + s_off + r * K / 16;
+                for (int64_t c = 0; c < K; c++) {
+                    uint8_t code = (c & 1) ? (uint8_t)(cw[c / 2] >> 4) : (uint8_t)(cw[c / 2] & 15);
+                    wrow[c] = oracle_e2m1_to_f32(code) * oracle_e4m3_to_f32(sc[c / 16]);
+                }
+                float acc = 0.0f;
+                for (int64_t g = 0; g < K; g += 16)
+                    for (int p = 0; p < terms; p++)
+                        for (int64_t c = g; c < g + 16; c++) acc += xt[(size_t)p * K + c] * wrow[c];
+                y[(size_t)a * N + r] = acc * s2;
+            }
+        }
+    }
+    free(wrow);
+    free(xt);
+}
+
 int oracle_moe_decode_nvfp4(const float* logits, const float* x, const uint8_t* const* all_recs, int T, int E, int k,
                             const OomNvfp4Record* geo, int32_t* ids, float* weights, float* out) {
     int A = T * k;
