@@ -9,7 +9,7 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 256 MB Infinity Cache.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|turbo|prefill|gemv|copy]
+                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|turbo|prefill|nvfp4-prefill|gemv|copy]
 
 Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
 kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
@@ -679,6 +679,135 @@ def make_nvfp4_set(E, geo, stride, seed, torch):
     return buf
 
 
+def bench_nvfp4_prefill(args):
+    """The routed experts of one prefill group over NVFP4 records on the bf16 matrix cores,
+    the reference's tiled path (crates/oominf-models-qwen/src/moe.rs:746-758): gate and up
+    with oom_moe_tiled_nvfp4, oom_moe_swiglu_range, down with oom_moe_tiled_nvfp4, and the
+    slot-order combine. 2048 tokens, 512 experts top-10, hidden 2560, inter 640 (about 40
+    assignments an expert: the reference's prefill_throughput shape,
+    crates/oominf-cuda/tests/moe_tiled.rs:229-246). Routing and the plan are made once
+    before the timed steps; activations f32 x N(0, 1)."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    T, E, k, H, I = 2048, 512, 10, 2560, 640
+    exact = args.prefill_precision == "exact"
+    prec = hip.EXPERT_EXACT if exact else hip.EXPERT_BF16
+    geo = hip.nvfp4_geometry(H, I)
+    stride = hip.nvfp4_stride(geo)
+    log(f"bench: nvfp4 prefill T={T} E={E} k={k} H={H} I={I} {args.prefill_precision}; "
+        f"building {E * stride / 1e9:.2f} GB of records")
+    recset = make_nvfp4_set(E, geo, stride, 1357, torch)
+    addrs = torch.tensor([recset.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(71)
+    logits = torch.randn((T, E), generator=g, device="cuda")
+    x = torch.randn((T, H), generator=g, device="cuda")
+    A = T * k
+    ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    hip.router_topk(logits, ids, wts, k)
+    plan = torch.empty(hip.moe_plan_size(T, E, k), dtype=torch.int32, device="cuda")
+    recs = torch.empty(E, dtype=torch.int64, device="cuda")
+    hip.moe_plan(ids, E, addrs, plan, recs)
+    torch.cuda.synchronize()
+    hp = plan.cpu().numpy()
+    n_e = int(hp[0])
+    off_h = hp[1 + E:1 + E + n_e + 1]
+    max_n = int(np.diff(off_h).max())
+    off = plan[1 + E:]
+    assign_tok = plan[1 + E + E + 1:1 + E + E + 1 + A]
+    slot_assign = plan[1 + E + E + 1 + A:1 + E + E + 1 + 2 * A].view(T, k)
+    gbuf = torch.empty((A, I), dtype=torch.float32, device="cuda")
+    ubuf = torch.empty_like(gbuf)
+    hbuf = torch.empty_like(gbuf)
+    ybuf = torch.empty((A, H), dtype=torch.float32, device="cuda")
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step():
+        hip.moe_tiled_nvfp4(recs, off, assign_tok, n_e, max_n, x, gbuf, I, H, geo.gate_weight, geo.gate_scale,
+                            geo.scale2[0], prec, stream)
+        hip.moe_tiled_nvfp4(recs, off, assign_tok, n_e, max_n, x, ubuf, I, H, geo.up_weight, geo.up_scale,
+                            geo.scale2[1], prec, stream)
+        hip.moe_swiglu_range(gbuf, ubuf, hbuf, 0, A * I, stream)
+        hip.moe_tiled_nvfp4(recs, off, None, n_e, max_n, hbuf, ybuf, H, I, geo.down_weight, geo.down_scale,
+                            geo.scale2[2], prec, stream)
+        hip.moe_combine_slots(ybuf, slot_assign, wts, out, stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(args.steps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    per_expert = 3 * H * I // 2 + 3 * H * I // 16 + 12
+    bytes_step = n_e * per_expert + T * H * 4 + T * H * 2
+    terms = 3 if exact else 1
+    flops = 2.0 * A * 3 * H * I * terms  # the matrix-core work: three projections, one pass a term
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    res = {
+        "metric": "MoE NVFP4 prefill (tiled, bf16 matrix cores) us/step + roofline fraction, 1 GPU",
+        "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "nvfp4 weights decoded exactly to bf16, f32 activations as " +
+                 ("three exact bf16 terms" if exact else "bf16") + ", fp32 accumulate",
+        "data": "synthetic",
+        "config": {"workload": "routed experts of a 2048-token prefill group over nvfp4-modelopt-g16 records: 512 "
+                               "experts top-10, hidden 2560, inter 640, random codes and scales, N(0,1) logits and "
+                               "x; gate, up, SwiGLU, down, slot-order combine (routing made once)",
+                   "tokens": T, "experts": E, "top_k": k, "hidden": H, "inter": I, "distinct_experts": n_e,
+                   "max_per_expert": max_n, "expert_precision": args.prefill_precision,
+                   "tokens_per_s": T / (ms * 1e-3), "hbm_gbs": gbs},
+        "roofline": ({"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                      "frac": tflops / PEAK_BF16_TFLOPS} if exact else
+                     {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS})
+        | {"traffic": measured_traffic("nvfp4_prefill"), "kernel": "moe_tiled_nvfp4_kernel (three launches a step)",
+           "algorithmic_bytes_per_step": bytes_step, "matrix_flops_per_step": flops},
+    }
+    if not args.no_cpu:
+        import oracle
+
+        # the oracle's single-thread restatement of the same three projections over a sample
+        # of 8 experts' assignments, scaled to the step's n_e experts
+        host = recset.cpu().numpy()
+        ids_h, wh = ids.cpu().numpy(), wts.cpu().numpy()
+        xs = x.cpu().numpy()
+        S = 8
+        sexp = hp[1:1 + n_e][:S]
+        soff = off_h[:S + 1] - off_h[0]
+        stok = hp[1 + E + E + 1:1 + E + E + 1 + A][off_h[0]:off_h[S]]
+        srecs = [host[int(e)] for e in sexp]
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            gg = oracle.moe_tiled_nvfp4(srecs, soff, stok, xs, I, H, geo.gate_weight, geo.gate_scale, geo.scale2[0],
+                                        terms)
+            uu = oracle.moe_tiled_nvfp4(srecs, soff, stok, xs, I, H, geo.up_weight, geo.up_scale, geo.scale2[1],
+                                        terms)
+            hh = (gg / (1.0 + np.exp(-gg)) * uu).astype(np.float32)
+            oracle.moe_tiled_nvfp4(srecs, soff, None, hh, H, I, geo.down_weight, geo.down_scale, geo.scale2[2], terms)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds and reps >= 1:
+                break
+        per = el / reps * (A / max(1, int(soff[-1])))
+        res["cpu_baseline"] = {"value": per * 1e6, "unit": "us/step", "cores": 1, "kind": "port",
+                               "sample": f"{reps} runs of gate, up, SwiGLU and down for 8 experts' "
+                                         f"{int(soff[-1])} assignments with the oracle's restatement of the "
+                                         f"reference's tiled arithmetic, scaled to the step's {A} assignments, "
+                                         f"on {cpu_model()}"}
+        del ids_h, wh
+    return res
+
+
 def bench_nvfp4(args):
     """One routed MoE decode step over NVFP4 (nvfp4-modelopt-g16) records at the released
     model's routed geometry: 512 experts, top-10, hidden 2560, inter 640, batch 1, fresh
@@ -973,7 +1102,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "offload", "attn",
-                                                            "turbo", "prefill", "gemv", "copy"])
+                                                            "turbo", "prefill", "nvfp4-prefill", "gemv", "copy"])
     ap.add_argument("--prefill-precision", default="exact", choices=["exact", "bf16"],
                     help="activation precision of the prefill's down projection (the reference's ExpertPrecision)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -995,6 +1124,8 @@ def main():
         res = bench_attn(args)
     elif args.config == "turbo":
         res = bench_turbo(args)
+    elif args.config == "nvfp4-prefill":
+        res = bench_nvfp4_prefill(args)
     elif args.config == "gemv":
         res = bench_gemv(args)
     elif args.config == "prefill":

@@ -16,8 +16,9 @@
 // (thread t: row t % 128, 16 columns, one 8-byte code load and one scale byte) and
 // splits the 64 x 32 activations into their terms in LDS, while the next step's global
 // loads are in flight. Wave w owns rows 32 w .. 32 w + 31 (two 16-row N subtiles) and all
-// 64 assignments (four 16-row M subtiles): per step 8 v_mfma_f32_16x16x32_bf16 a term,
-// M subtiles past the expert's assignments skipped. LDS rows are 40 bf16 (80 bytes), so
+// 64 assignments (four 16-row M subtiles; rows past the expert's assignments hold zeros):
+// per step 8 v_mfma_f32_16x16x32_bf16 a term, with no branch in the step, so the
+// compiler's waits for the load ring stay exact. LDS rows are 40 bf16 (80 bytes), so
 // the 16 rows of an operand read fall in distinct bank groups. Grid (ceil(N / 128),
 // ceil(max_per_expert / 64), n_experts), as the reference's.
 #include "stream.hpp"
@@ -27,7 +28,8 @@ namespace oom {
 constexpr int T4_BN = 128;       // weight rows a block
 constexpr int T4_BM = 64;        // assignments a block
 constexpr int T4_BK = 32;        // K step
-constexpr int T4_THREADS = 256;  // 4 waves
+constexpr int T4_THREADS = 256;  // 4 waves, 32 weight rows each
+constexpr int T4_NX = T4_BM * T4_BK / 4 / T4_THREADS;  // activation float4s a thread loads a step
 constexpr int T4_LS = 40;        // LDS row stride in bf16: 32 + 8
 
 typedef __bf16 t4bf16x8 __attribute__((ext_vector_type(8)));
@@ -44,24 +46,18 @@ struct TiledArgs {
     int s2_idx;            // its weight_scale_2, in floats from the record start
 };
 
-// bf16 bits of an f32 value that is a bf16 value (the weights here): its top half.
-__device__ __forceinline__ uint32_t t4_pack(float lo, float hi) {
-    return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
-}
+typedef __bf16 t4bf16x2 __attribute__((ext_vector_type(2)));
+typedef float t4f32x2 __attribute__((ext_vector_type(2)));
 
-// The term t of x: hi = bf16(x), then the same of each remainder (round to nearest even).
-template <int TERMS>
-__device__ __forceinline__ void t4_split(float x, uint16_t (&t)[TERMS]) {
-    float r = x;
-#pragma unroll
-    for (int p = 0; p < TERMS; p++) {
-        t[p] = f32_to_bf16(r);
-        r -= bf16_to_f32(t[p]);
-    }
+// Two f32 values as packed bf16 (v_cvt_pk_bf16_f32, round to nearest even; exact for the
+// weights here, which are bf16 values).
+__device__ __forceinline__ uint32_t t4_cvt(float lo, float hi) {
+    const t4f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, t4bf16x2));
 }
 
 template <int TERMS>
-__global__ void __launch_bounds__(T4_THREADS) moe_tiled_nvfp4_kernel(TiledArgs g) {
+__global__ void __launch_bounds__(T4_THREADS, 2) moe_tiled_nvfp4_kernel(TiledArgs g) {
     __shared__ __align__(16) uint16_t wsh[2][T4_BN][T4_LS];
     __shared__ __align__(16) uint16_t xsh[2][TERMS][T4_BM][T4_LS];
     const int e = blockIdx.z;
@@ -77,7 +73,7 @@ __global__ void __launch_bounds__(T4_THREADS) moe_tiled_nvfp4_kernel(TiledArgs g
 
     // ---- this thread's loads: weight row r0 + tid % 128, columns 16 (tid / 128) .. of a
     // step; activations idx = tid + 256 i (i < 2): assignment idx / 8, columns 4 (idx % 8) ..
-    const int wr = tid & (T4_BN - 1), wh = tid >> 7;
+    const int wr = tid & (T4_BN - 1), wh = tid / T4_BN;
     const bool wok = r0 + wr < g.N;
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(rec + g.w_off), (short)0, (int)((int64_t)g.N * g.K / 2), BUF_FLAGS);
@@ -85,28 +81,36 @@ __global__ void __launch_bounds__(T4_THREADS) moe_tiled_nvfp4_kernel(TiledArgs g
         const_cast<uint8_t*>(rec + g.s_off), (short)0, (int)((int64_t)g.N * g.K / 16), BUF_FLAGS);
     const int cbase = wok ? (r0 + wr) * (g.K / 2) + 8 * wh : OOB;
     const int sbase = wok ? (r0 + wr) * (g.K / 16) + wh : OOB;
-    const float* xrow[2];
+    // activation rows: past the expert's assignments a row reads assignment a_begin's row
+    // (a valid address) and the value is dropped after the load, so no load is branched
+    const float* xrow[T4_NX];
+    bool xok[T4_NX];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < T4_NX; i++) {
         const int t = (tid + i * T4_THREADS) >> 3;
-        xrow[i] = t < nt ? g.x + (int64_t)(g.rows ? g.rows[a_begin + t] : a_begin + t) * g.K : nullptr;
+        xok[i] = t < nt;
+        const int a = a_begin + (xok[i] ? t : 0);
+        xrow[i] = g.x + (int64_t)(g.rows ? g.rows[a] : a) * g.K + ((tid + i * T4_THREADS) & 7) * 4;
     }
-    auto load = [&](int kb, uint2& codes, uint32_t& sb, float4 (&xv)[2]) {
-        const int k0 = kb * T4_BK;
+    struct Ld {
+        uint2 codes;
+        uint32_t sb;
+        float4 xv[T4_NX];
+    };
+    // step kb's loads (kb clamped to the last step: the ring's loads past the end repeat it)
+    auto load = [&](int kb, Ld& l) {
+        const int k0 = min(kb, nkb - 1) * T4_BK;
         const auto c = __builtin_amdgcn_raw_buffer_load_b64(cr, cbase == OOB ? OOB : cbase + k0 / 2, 0, 0);
-        codes = make_uint2(c[0], c[1]);
-        sb = __builtin_amdgcn_raw_buffer_load_b8(sr, sbase == OOB ? OOB : sbase + k0 / 16, 0, 0);
+        l.codes = make_uint2(c[0], c[1]);
+        l.sb = __builtin_amdgcn_raw_buffer_load_b8(sr, sbase == OOB ? OOB : sbase + k0 / 16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int kq = ((tid + i * T4_THREADS) & 7) * 4;
-            xv[i] = xrow[i] ? *reinterpret_cast<const float4*>(xrow[i] + k0 + kq) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int i = 0; i < T4_NX; i++) l.xv[i] = *reinterpret_cast<const float4*>(xrow[i] + k0);
     };
     // decoded weights and split activations of a step into LDS buffer b
-    auto stage = [&](int b, const uint2& codes, uint32_t sb, const float4 (&xv)[2]) {
-        const float sc = __builtin_amdgcn_cvt_f32_fp8((int)sb, 0);
+    auto stage = [&](int b, const Ld& l) {
+        const float sc = __builtin_amdgcn_cvt_f32_fp8((int)l.sb, 0);
         uint32_t packed[8];
-        const uint32_t cw[2] = {codes.x, codes.y};
+        const uint32_t cw[2] = {l.codes.x, l.codes.y};
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             // byte q of word i: columns 8 i + 2 q (low nibble) and 8 i + 2 q + 1
@@ -114,26 +118,32 @@ __global__ void __launch_bounds__(T4_THREADS) moe_tiled_nvfp4_kernel(TiledArgs g
             const auto p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(cw[i], 1.0f, 1);
             const auto p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(cw[i], 1.0f, 2);
             const auto p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(cw[i], 1.0f, 3);
-            packed[4 * i] = t4_pack(p0[0] * sc, p0[1] * sc);
-            packed[4 * i + 1] = t4_pack(p1[0] * sc, p1[1] * sc);
-            packed[4 * i + 2] = t4_pack(p2[0] * sc, p2[1] * sc);
-            packed[4 * i + 3] = t4_pack(p3[0] * sc, p3[1] * sc);
+            packed[4 * i] = t4_cvt(p0[0] * sc, p0[1] * sc);
+            packed[4 * i + 1] = t4_cvt(p1[0] * sc, p1[1] * sc);
+            packed[4 * i + 2] = t4_cvt(p2[0] * sc, p2[1] * sc);
+            packed[4 * i + 3] = t4_cvt(p3[0] * sc, p3[1] * sc);
         }
         uint4* dst = reinterpret_cast<uint4*>(&wsh[b][wr][16 * wh]);
         dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
         dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+        // activations as terms, two values a conversion: the remainder of a round to
+        // nearest is exact in f32
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < T4_NX; i++) {
             const int idx = tid + i * T4_THREADS, t = idx >> 3, kq = (idx & 7) * 4;
-            const float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-            uint16_t parts[4][TERMS];
+            const float4 x4 = xok[i] ? l.xv[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float v[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
-            for (int c = 0; c < 4; c++) t4_split<TERMS>(v[c], parts[c]);
-#pragma unroll
-            for (int p = 0; p < TERMS; p++)
-                *reinterpret_cast<uint2*>(&xsh[b][p][t][kq]) =
-                    make_uint2((uint32_t)parts[0][p] | ((uint32_t)parts[1][p] << 16),
-                               (uint32_t)parts[2][p] | ((uint32_t)parts[3][p] << 16));
+            for (int p = 0; p < TERMS; p++) {
+                const uint32_t w0 = t4_cvt(v[0], v[1]), w1 = t4_cvt(v[2], v[3]);
+                *reinterpret_cast<uint2*>(&xsh[b][p][t][kq]) = make_uint2(w0, w1);
+                if (p + 1 < TERMS) {
+                    v[0] -= __uint_as_float(w0 << 16);
+                    v[1] -= __uint_as_float(w0 & 0xffff0000u);
+                    v[2] -= __uint_as_float(w1 << 16);
+                    v[3] -= __uint_as_float(w1 & 0xffff0000u);
+                }
+            }
         }
     };
 
@@ -142,24 +152,16 @@ __global__ void __launch_bounds__(T4_THREADS) moe_tiled_nvfp4_kernel(TiledArgs g
     for (int ms = 0; ms < 4; ms++)
 #pragma unroll
         for (int ns = 0; ns < 2; ns++) acc[ms][ns] = t4f4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int msn = (nt + 15) >> 4;  // M subtiles holding assignments (block-uniform)
     const int kl = 8 * (lane >> 4);  // this lane's 8 columns of a step
-    uint2 codes;
-    uint32_t sb;
-    float4 xv[2];
-    load(0, codes, sb, xv);
-    for (int kb = 0; kb < nkb; kb++) {
-        const int b = kb & 1;
-        stage(b, codes, sb, xv);
-        __syncthreads();
-        if (kb + 1 < nkb) load(kb + 1, codes, sb, xv);
+    // a ring of four steps' loads in registers: step kb stages slot kb % 4 and refills it
+    // with step kb + 4, so each step's loads have three steps of work to land in
+    auto mfmas = [&](int b) {
         t4bf16x8 bop[2];
 #pragma unroll
         for (int ns = 0; ns < 2; ns++)
             bop[ns] = *reinterpret_cast<const t4bf16x8*>(&wsh[b][32 * wave + 16 * ns + (lane & 15)][kl]);
 #pragma unroll
         for (int ms = 0; ms < 4; ms++) {
-            if (ms >= msn) break;
 #pragma unroll
             for (int p = 0; p < TERMS; p++) {
                 const t4bf16x8 aop = *reinterpret_cast<const t4bf16x8*>(&xsh[b][p][16 * ms + (lane & 15)][kl]);
@@ -168,7 +170,28 @@ __global__ void __launch_bounds__(T4_THREADS) moe_tiled_nvfp4_kernel(TiledArgs g
                     acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[ns], acc[ms][ns], 0, 0, 0);
             }
         }
+    };
+    Ld l0, l1, l2, l3;
+    load(0, l0);
+    load(1, l1);
+    load(2, l2);
+    load(3, l3);
+#define T4_STEP(R)                  \
+    {                               \
+        stage(kb & 1, R);           \
+        __syncthreads();            \
+        load(kb + 4, R);            \
+        mfmas(kb & 1);              \
+        if (++kb == nkb) break;     \
     }
+    int kb = 0;
+    for (;;) {
+        T4_STEP(l0)
+        T4_STEP(l1)
+        T4_STEP(l2)
+        T4_STEP(l3)
+    }
+#undef T4_STEP
     // ---- y = acc * scale_2: lane l holds assignments 16 ms + 4 (l / 16) + i, row 16 ns + l % 16
 #pragma unroll
     for (int ms = 0; ms < 4; ms++)
