@@ -640,8 +640,9 @@ def bench_layer(args, T, config):
                    "distinct_experts_per_step": float(distinct.mean())},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
                      "traffic": measured_traffic(config),
-                     "kernel": "oom_moe_layer_decode_fp8 step (router and gate GEMVs, routed and shared decode "
-                               "kernels, gated combine)",
+                     "kernel": "oom_moe_layer_decode_fp8 step: the router GEMV, then one decode kernel with the "
+                               "shared expert, its gate logit and the gated add inside it "
+                               f"({'moe_decode_fused_kernel' if T == 1 else 'moe_batch_kernel'})",
                      "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
     }
     if not args.no_cpu:

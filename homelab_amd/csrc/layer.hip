@@ -7,7 +7,9 @@
 // One token with bf16 activations and a shared expert of the routed geometry takes two
 // launches: the router GEMV, then the one-token decode kernel with the shared expert as one
 // more plan slot (its gate/up rows beside the routed ones, one row pair of each down tile
-// per wave) and the gate logit and gated add inside it.
+// per wave) and the gate logit and gated add inside it. A batch of 2..16 such tokens takes
+// two as well: the router GEMV, then the batch kernel with the shared expert as one more
+// plan entry holding every token, the gate logits and the gated add inside it.
 //
 // Otherwise the shared expert is an FP8 record of the routed experts' format (gate, up, down
 // with 128 x 128 block scales, hidden x shared_inter). It runs through the same one-launch decode
@@ -15,6 +17,8 @@
 // step computes down(silu(x Wg^T) * (x Wu^T)) with weight 1, which is the reference's
 // gemm_w(gate_up) -> silu_mul_rows -> gemm_w(down) (moe.rs:507-513) in the same fp32
 // arithmetic, summed in another order.
+#include <algorithm>
+
 #include "common.hpp"
 
 extern "C" int oom_moe_decode_fp8(const float* logits, const void* x, int x_dtype, const uint64_t* all_recs, int T,
@@ -31,6 +35,12 @@ bool fused_shared_supported(int T, int E, int k, const OomFp8Record& g, const Oo
 int launch_fused_shared(const float* logits, const void* x, const uint64_t* all_recs, int E, int k,
                         const OomFp8Record& g, const uint64_t* shared_rec, const uint16_t* gate_w, float* gate,
                         int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st);
+bool batch_shared_supported(int T, int E, int k, const OomFp8Record& g, const OomFp8Record& sg, int xdt,
+                            const void* x);
+size_t batch_shared_workspace_size(int T, int k, const OomFp8Record& g);
+int launch_batch_shared(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
+                        const OomFp8Record& g, const uint64_t* shared_rec, const uint16_t* gate_w, int32_t* ids,
+                        float* weights, void* out, int odt, void* ws, hipStream_t st);
 
 // out[t, c] = routed[t, c] + sigmoid(gate[t]) * shared[t, c], sigmoid(v) = 1 / (1 + e^-v)
 // (crates/oominf-cuda/kernels/ops.cu:10,310-316). Four columns per thread.
@@ -84,8 +94,9 @@ static LayerWs layer_ws(int T, int E, int k, const OomFp8Record* geo, const OomF
     w.rgemv = 0;
     w.ggemv = gemv_region(E, (int64_t)H);
     w.decode = w.ggemv + gemv_region(1, (int64_t)H);
-    const size_t dec = std::max(oom_moe_decode_fp8_workspace_size(T, E, k, geo),
-                                oom_moe_decode_fp8_workspace_size(T, 1, 1, sgeo));
+    const size_t dec = std::max({oom_moe_decode_fp8_workspace_size(T, E, k, geo),
+                                 oom_moe_decode_fp8_workspace_size(T, 1, 1, sgeo),
+                                 batch_shared_workspace_size(T, k, *geo)});
     w.logits = w.decode + l_al256(dec);
     w.gate = w.logits + l_al256((size_t)T * E * sizeof(float));
     w.routed = w.gate + l_al256((size_t)T * sizeof(float));
@@ -153,6 +164,9 @@ extern "C" int oom_moe_layer_decode_fp8(const void* x, int x_dtype, const uint16
         return rc;
     if (fused_shared_supported(T, E, k, *geo, *shared_geo, x_dtype))
         return launch_fused_shared(logits, x, all_recs, E, k, *geo, shared_rec, shared_gate_w, gate, ids, weights, out,
+                                   out_dtype, dws, as_stream(stream));
+    if (batch_shared_supported(T, E, k, *geo, *shared_geo, x_dtype, x))
+        return launch_batch_shared(logits, x, all_recs, T, E, k, *geo, shared_rec, shared_gate_w, ids, weights, out,
                                    out_dtype, dws, as_stream(stream));
     if (int rc = oom_gemv_bf16(x, x_dtype, shared_gate_w, gate, OOM_F32, T, 1, H, base + w.ggemv, w.decode - w.ggemv,
                                stream))

@@ -28,6 +28,14 @@
 //  * A second grid barrier, then the combine: out[t] = sum over t's slots, in slot order,
 //    of w y, one lane per 4 rows of a token.
 // h and y move between blocks with device-coherent (sc1) stores and loads.
+//
+// With a shared expert of the routed geometry (SH, the decode layer's batch step) the plan
+// gains one entry after the routed experts: the shared record with all T tokens
+// (assignments A .. A + T), so its gate/up rows and down tiles are phase-1 and phase-2
+// items like the routed ones. Each block takes the tokens' gate logits x . gate_w from the
+// activations in LDS while wave 0 plans, and the combine ends with
+// out[t] = routed + sigmoid(gate[t]) * y_shared[t] (Moe::shared and moe_combine,
+// crates/oominf-models-qwen/src/moe.rs:498-527, crates/oominf-cuda/kernels/ops.cu:10,310-316).
 #include "router.hpp"
 #include "stream.hpp"
 
@@ -37,6 +45,7 @@ constexpr int B_W = 8;             // waves per block: two per SIMD
 constexpr int B_T = 16;            // tokens: one MFMA column tile
 constexpr int B_KMAX = 8;          // router top-k
 constexpr int B_AMAX = B_T * B_KMAX;
+constexpr int B_ASH = B_AMAX + B_T;  // with the shared expert's assignments
 constexpr int B_HMAX = 4096;
 constexpr int B_IMAX = 2048;
 constexpr int B_DEPTH = 8;         // K steps in flight per wave (3 loads each)
@@ -58,8 +67,12 @@ struct BArgs {
     int32_t* ids;
     float* weights;
     void* out;
-    float* h;  // [A, I]
-    float* y;  // [A, H]
+    float* h;  // [A (+ T with the shared expert), I]
+    float* y;  // [A (+ T), H]
+    // the shared expert (SH): its record address at shared_rec[0] (the routed geometry) and
+    // its bf16 gate row [H]
+    const uint64_t* shared_rec;
+    const uint16_t* gate_w;
     uint32_t* hdr;
     uint32_t* status;  // the device's status word: 1 if a wait gave up (results invalid)
     uint32_t spin;     // polls before a wait gives up
@@ -72,17 +85,18 @@ struct alignas(16) BLds {
         uint16_t x[B_T * B_XS];       // phase 1: the tokens' activations, bf16
         uint16_t hh[2][B_T * B_HS];   // phase 2: the staged expert's h, hi and lo bf16 terms
     } u;
-    uint64_t recs[256];
+    uint64_t recs[257];  // entry E: the shared expert's record
     uint64_t keys[B_W][B_KMAX];  // routing scratch of each wave
     float p[B_W][B_KMAX];
     uint32_t mask[256];          // tokens routed to each expert, one bit per token
     int base[256];               // first assignment of each expert
     int ids[B_AMAX];
     float w[B_AMAX];
-    int experts[B_AMAX];
-    int off[B_AMAX + 1];
-    int assign_tok[B_AMAX];
+    int experts[B_AMAX + 1];
+    int off[B_AMAX + 2];
+    int assign_tok[B_ASH];
     int slot_assign[B_AMAX];
+    float gate[B_T];  // the shared expert's gate logits
     int n_e;
 };
 static_assert(offsetof(BLds, u) == 0 && (B_XS * 2) % 16 == 0 && (B_HS * 2) % 16 == 0 &&
@@ -263,7 +277,36 @@ __device__ __forceinline__ void batch_picks(const uint64_t (&key)[EQ], uint64_t 
     wave_lds_order();  // keys and p are free for the wave's next token
 }
 
-template <int EQ, int ODT>
+// The shared expert's gate logits L.gate[t] = x[t] . gate_w for tokens t0, t0 + step, ..
+// from the activations in LDS (zeros past H): lane l takes columns 8 (l + 64 c) .. + 8.
+__device__ __forceinline__ void batch_gate(const BArgs& a, BLds& L, int t0, int step, int lane) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.gate_w), (short)0, a.H * 2, BUF_FLAGS);
+    constexpr int NC = B_HMAX / 512;
+    uint4 g[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int col = (lane + 64 * c) * 8;
+        g[c] = ld16(r, col < a.H ? col * 2 : OOB);
+    }
+    for (int t = t0; t < a.T; t += step) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(&L.u.x[t * B_XS + (lane + 64 * c) * 8]);
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, gw[4] = {g[c].x, g[c].y, g[c].z, g[c].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc = fmaf(__uint_as_float(gw[i] << 16), __uint_as_float(xw[i] << 16), acc);
+                acc = fmaf(__uint_as_float(gw[i] & 0xffff0000u), __uint_as_float(xw[i] & 0xffff0000u), acc);
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) L.gate[t] = acc;
+    }
+}
+
+template <int EQ, int ODT, bool SH>
 __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const uint32_t bbase1 = grid_barrier_base(a.hdr + WS_BAR / 4), bbase2 = grid_barrier_base(a.hdr + WS_BAR2 / 4);
     __shared__ BLds L;
@@ -281,6 +324,9 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
             lv[j][q] = t < T && e < E ? a.logits[(size_t)t * E + e] : -INFINITY;
         }
     if (tid < E) L.recs[tid] = a.all_recs[tid];
+    if constexpr (SH) {
+        if (tid == E) L.recs[E] = a.shared_rec[0];
+    }
     L.mask[tid] = 0u;
     // activations: thread tid takes columns 8 (tid + NT c) .. + 8 of every token row (zeros
     // past T and H), 16 loads in flight per pass
@@ -344,7 +390,15 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         if (lane == 63) {
             L.n_e = ip;
             L.off[ip] = ic;
+            if constexpr (SH) {
+                // the shared expert after the routed ones: record E, assignments A .. A + T
+                L.experts[ip] = E;
+                L.off[ip + 1] = ic + T;
+                L.n_e = ip + 1;
+            }
         }
+    } else if constexpr (SH) {
+        batch_gate(a, L, wave - 1, B_W - 1, lane);
     }
     __syncthreads();
     for (int s = tid; s < A; s += NT) {
@@ -352,6 +406,9 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         const int pos = L.base[e] + __builtin_popcount(L.mask[e] & ((1u << t) - 1u));
         L.slot_assign[s] = pos;
         L.assign_tok[pos] = t;
+    }
+    if constexpr (SH) {
+        if (tid < T) L.assign_tok[A + tid] = tid;
     }
     __syncthreads();
     if (blockIdx.x == 0)
@@ -362,8 +419,9 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const int n_e = L.n_e;
     const int NW = gridDim.x * B_W, gw = blockIdx.x * B_W + wave;
     const int nksH = (H + 127) >> 7, nksI = (I + 127) >> 7;
-    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, A * I * 4, BUF_FLAGS);
-    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, A * H * 4, BUF_FLAGS);
+    const int AS = A + (SH ? T : 0);  // rows of h and y
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, AS * I * 4, BUF_FLAGS);
+    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, AS * H * 4, BUF_FLAGS);
     const int m16 = lane & 15, kq = lane >> 4;
     // ---- phase 1: my items gw + n NW (n < mine), K steps in order; an issue cursor runs
     // B_DEPTH steps ahead of the consume cursor ----
@@ -508,17 +566,23 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const int nq4 = H >> 2;
     for (int g = gw * 64 + lane; g < T * nq4; g += NW * 64) {
         const int t = g / nq4, r = (g - t * nq4) * 4;
-        bu32x4 yv[B_KMAX];
+        bu32x4 yv[B_KMAX], ys;
 #pragma unroll
         for (int s = 0; s < B_KMAX; s++)
             yv[s] = __builtin_amdgcn_raw_buffer_load_b128(
                 yr, s < k ? (L.slot_assign[t * k + s] * H + r) * 4 : OOB, 0, BUF_SC1);
+        if constexpr (SH) ys = __builtin_amdgcn_raw_buffer_load_b128(yr, ((A + t) * H + r) * 4, 0, BUF_SC1);
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < B_KMAX; s++)
             if (s < k)
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[e] = fmaf(L.w[t * k + s], __uint_as_float(yv[s][e]), acc[e]);
+        if constexpr (SH) {
+            const float sg = 1.0f / (1.0f + expf(-L.gate[t]));  // sigmoid (ops.cu:10)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = acc[e] + sg * __uint_as_float(ys[e]);
+        }
 #pragma unroll
         for (int e = 0; e < 4; e++) store_out<ODT>(a.out, (size_t)t * H + r + e, acc[e]);
     }
@@ -532,8 +596,9 @@ struct BWs {
     size_t h, y, total;
 };
 
-static BWs batch_ws(int T, int k, const OomFp8Record& g) {
-    const size_t A = (size_t)T * k;
+// h and y rows: one per assignment, plus one per token for the shared expert (sh).
+static BWs batch_ws(int T, int k, const OomFp8Record& g, bool sh = false) {
+    const size_t A = (size_t)T * (k + (sh ? 1 : 0));
     BWs w;
     w.h = WS_HEADER;
     w.y = w.h + ((A * g.inter * sizeof(float) + 255) & ~size_t(255));
@@ -541,7 +606,7 @@ static BWs batch_ws(int T, int k, const OomFp8Record& g) {
     return w;
 }
 
-template <int EQ, int ODT>
+template <int EQ, int ODT, bool SH>
 static int batch_grid() {
     static thread_local int cached_dev = -1, cached = 0;
     int dev = 0;
@@ -549,7 +614,7 @@ static int batch_grid() {
     if (dev != cached_dev) {
         int cus = 0, per = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_batch_kernel<EQ, ODT>, 64 * B_W, 0) != hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_batch_kernel<EQ, ODT, SH>, 64 * B_W, 0) != hipSuccess)
             return 0;
         cached = cus * per;
         cached_dev = dev;
@@ -557,12 +622,20 @@ static int batch_grid() {
     return cached;
 }
 
-template <int EQ, int ODT>
+template <int EQ, int ODT, bool SH>
 static int launch_batch_t(const BArgs& a, hipStream_t st) {
-    const int grid = batch_grid<EQ, ODT>();
-    if (grid <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: occupancy query failed");
-    hipLaunchKernelGGL((moe_batch_kernel<EQ, ODT>), dim3(grid), dim3(64 * B_W), 0, st, a);
-    return launched("oom_moe_decode_fp8");
+    const char* who = SH ? "oom_moe_layer_decode_fp8" : "oom_moe_decode_fp8";
+    const int grid = batch_grid<EQ, ODT, SH>();
+    if (grid <= 0) return fail(OOM_ERR_LAUNCH, std::string(who) + ": occupancy query failed");
+    hipLaunchKernelGGL((moe_batch_kernel<EQ, ODT, SH>), dim3(grid), dim3(64 * B_W), 0, st, a);
+    return launched(who);
+}
+
+template <bool SH>
+static int launch_batch_any(const BArgs& a, int odt, hipStream_t st) {
+    if (a.E <= 128)
+        return odt == OOM_BF16 ? launch_batch_t<2, OOM_BF16, SH>(a, st) : launch_batch_t<2, OOM_F32, SH>(a, st);
+    return odt == OOM_BF16 ? launch_batch_t<4, OOM_BF16, SH>(a, st) : launch_batch_t<4, OOM_F32, SH>(a, st);
 }
 
 // Widths a multiple of 16 keep every 16-byte access inside its row; x 16-byte aligned.
@@ -575,9 +648,20 @@ bool batch_supported(int T, int E, int k, const OomFp8Record& g, int xdt, const 
 
 size_t batch_workspace_size(int T, int k, const OomFp8Record& g) { return batch_ws(T, k, g).total; }
 
-int launch_batch(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
-                 const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st) {
-    const BWs w = batch_ws(T, k, g);
+// The batch step with a shared expert of the routed geometry as one more plan entry.
+bool batch_shared_supported(int T, int E, int k, const OomFp8Record& g, const OomFp8Record& sg, int xdt,
+                            const void* x) {
+    return batch_supported(T, E, k, g, xdt, x) && (int64_t)T * (k + 1) * std::max(g.hidden, g.inter) * 4 < OOB &&
+           g.hidden == sg.hidden && g.inter == sg.inter && g.gate_weight == sg.gate_weight &&
+           g.gate_scale == sg.gate_scale && g.up_weight == sg.up_weight && g.up_scale == sg.up_scale &&
+           g.down_weight == sg.down_weight && g.down_scale == sg.down_scale;
+}
+
+size_t batch_shared_workspace_size(int T, int k, const OomFp8Record& g) { return batch_ws(T, k, g, true).total; }
+
+static BArgs batch_args(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
+                        const OomFp8Record& g, int32_t* ids, float* weights, void* out, void* ws, bool sh) {
+    const BWs w = batch_ws(T, k, g, sh);
     uint8_t* base = reinterpret_cast<uint8_t*>(ws);
     BArgs a;
     a.logits = logits;
@@ -603,9 +687,26 @@ int launch_batch(const float* logits, const void* x, const uint64_t* all_recs, i
     a.hdr = reinterpret_cast<uint32_t*>(base);
     a.status = status_word();
     a.spin = wait_limit();
+    a.shared_rec = nullptr;
+    a.gate_w = nullptr;
+    return a;
+}
+
+int launch_batch(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
+                 const OomFp8Record& g, int32_t* ids, float* weights, void* out, int odt, void* ws, hipStream_t st) {
+    const BArgs a = batch_args(logits, x, all_recs, T, E, k, g, ids, weights, out, ws, false);
     if (!a.status) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_fp8: the device status word has no address");
-    if (a.E <= 128) return odt == OOM_BF16 ? launch_batch_t<2, OOM_BF16>(a, st) : launch_batch_t<2, OOM_F32>(a, st);
-    return odt == OOM_BF16 ? launch_batch_t<4, OOM_BF16>(a, st) : launch_batch_t<4, OOM_F32>(a, st);
+    return launch_batch_any<false>(a, odt, st);
+}
+
+int launch_batch_shared(const float* logits, const void* x, const uint64_t* all_recs, int T, int E, int k,
+                        const OomFp8Record& g, const uint64_t* shared_rec, const uint16_t* gate_w, int32_t* ids,
+                        float* weights, void* out, int odt, void* ws, hipStream_t st) {
+    BArgs a = batch_args(logits, x, all_recs, T, E, k, g, ids, weights, out, ws, true);
+    if (!a.status) return fail(OOM_ERR_LAUNCH, "oom_moe_layer_decode_fp8: the device status word has no address");
+    a.shared_rec = shared_rec;
+    a.gate_w = gate_w;
+    return launch_batch_any<true>(a, odt, st);
 }
 
 }  // namespace oom

@@ -132,7 +132,8 @@ def test_combine_shared_parity(hip):
     (1, 128, 8, 4096, 1536, 1536, False),   # the benchmark's layer shape, one token (shared expert in the kernel)
     (1, 200, 6, 1024, 512, 512, False),     # one token, E > 128, k < 8: waves with only the shared rows
     (1, 64, 8, 2048, 1024, 2048, False),    # one token, a wider shared expert: its own launch
-    (16, 128, 8, 4096, 1536, 1536, False),  # 16 tokens (the matrix-core routed and shared steps)
+    (16, 128, 8, 4096, 1536, 1536, False),  # 16 tokens: the batch kernel with the shared expert as a plan entry
+    (5, 200, 6, 1024, 512, 512, False),     # the same with E > 128 and 5 tokens
     (4, 64, 6, 1024, 512, 768, False),      # a shared expert wider than the routed ones
     (3, 16, 4, 256, 128, 256, True),        # f32 activations (the general one-launch kernel)
 ])
@@ -186,7 +187,8 @@ def test_layer_decode_matches_oracle(hip, T, E, k, H, I, SI, xf32):
 def test_layer_batch_sizes_share_a_workspace(hip, SI):
     """Layer steps of 16, 1, 5, 16 and 2 tokens on one workspace made for 16, with no
     synchronisation between them (a decode batch that shrinks and grows); with SI = inter
-    the one-token steps carry the shared expert inside the decode kernel."""
+    every step carries the shared expert inside its decode kernel (the one-token or the
+    batch kernel)."""
     import torch
 
     E, k, H, I = 64, 8, 1024, 512
