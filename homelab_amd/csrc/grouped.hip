@@ -222,10 +222,11 @@ __device__ __forceinline__ gi32x8 gop(const uint8_t* base, int row, int lane) {
 }
 
 // One K step on the matrix cores from a stage buffer: acc += the block sums scaled by the
-// weight's block scale (and the row's activation group scale).
+// weight's block scale (and the row's activation group scale). act: the wave's 16-row M
+// subtiles that hold assignments (1 or 2; the others' products are never stored).
 template <int NB>
 __device__ __forceinline__ void g_step(const uint8_t* sb, const float* scx, const float* scw, bool xgrp, int wm,
-                                       int wn, int wave, int lane, float (&acc)[NB][2][4][4]) {
+                                       int wn, int wave, int lane, int act, float (&acc)[NB][2][4][4]) {
     // tile row r's group scale is word 64 (r / 16) + r % 16 of scx; the wave's weight
     // scales words 64 wave + m of scw
     float xsk[2][4];
@@ -248,6 +249,7 @@ __device__ __forceinline__ void g_step(const uint8_t* sb, const float* scx, cons
             const gi32x8 bop = gop(sb + GBM * GBK + m * GBN * GBK, 64 * wn + 16 * ns + (lane & 15), lane);
 #pragma unroll
             for (int ms = 0; ms < 2; ms++) {
+                if (ms >= act) continue;
                 const gf32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
                 const gf32x4 blk =
                     __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop[ms], bop, z, 0, 0, 0, 127, 0, 127);
@@ -341,6 +343,8 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
         src.xso = (int)((g.rows ? g.rows[a] : a) * nkb * 4);
     }
     src.so = lane < NB ? (int)((lane == 0 ? g.s_off : g.s2_off) + (int64_t)(n0 / 128) * nkb * 4) : G_OOB;
+    const int left = a1 - (a0 + m0) - 32 * wm;  // assignments from this wave's first row on
+    const int act = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : left <= 16 ? 1 : 2);
     // this lane's output rows (per 16-row M subtile ms, element e): assignment index
     int arow_out[2][4];
 #pragma unroll
@@ -365,7 +369,7 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
         wait_vm<WAIT>();                                                                            \
         g_barrier();                                                                                \
         g_issue<NB>(src, kb + NST - 1, nkb, NSB, G_SX(NSB), G_SW(NSB), wave);                       \
-        g_step<NB>(SB, G_SX(SB), G_SW(SB), xgrp, wm, wn, wave, lane, acc);                          \
+        if (act > 0) g_step<NB>(SB, G_SX(SB), G_SW(SB), xgrp, wm, wn, wave, lane, act, acc);        \
         if (++kb == nkb) break;                                                                     \
     }
     int kb = 0;
@@ -433,114 +437,125 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
 // term (hi = bf16(h)) is the reference's ExpertPrecision::Bf16 arithmetic; two (hi + lo,
 // 16 significant bits of the fp32 h) stand for ExpertPrecision::Exact.
 //
-// K steps of 64 through three LDS stages (direct-to-LDS loads, as the FP8 passes): a stage
-// holds the h term tiles (128 assignments x 64 bf16 = 128 bytes a row, 8 chunks, the FP8
-// tiles' chunk swizzle) and the weight tile (128 rows x 64 bytes, 4 chunks, chunk c of
-// row r at 4 r + (c ^ ((r >> 2) & 3)), so the 16 rows of an operand read, and any 8 of
-// them, land in distinct 16-byte bank groups). Lane l of a wave takes K values
+// Block tiles of 128 assignments x 256 outputs; wave (wm, wn) takes rows 32 wm .. + 32 and
+// outputs 128 wn .. + 128 (one 128-row weight scale block). K steps of 64 through three LDS
+// stages (direct-to-LDS loads, as the FP8 passes; 150 KB, one block a CU): a stage holds the
+// h term tiles (128 assignments x 64 bf16 = 128 bytes a row, 8 chunks, the FP8 tiles' chunk
+// swizzle), the weight tile (256 rows x 64 bytes, 4 chunks, chunk c of row r at
+// 4 r + (c ^ ((r >> 2) & 3)), so the 16 rows of an operand read, and any 8 of them, land in
+// distinct 16-byte bank groups) and the wave scales. Lane l of a wave takes K values
 // 16 (l / 16) .. + 16 of the step for its row (A: assignment l % 16 of a 16-row subtile,
 // B: weight row l % 16), as two 8-value halves, one per MFMA: the same K order on both
-// sides, so the contraction is the plain sum.
+// sides, so the contraction is the plain sum. The operand reads and the direct-to-LDS
+// writes are the kernel's limit: a wave reads its A rows once for 8 N subtiles (at 128 x 128
+// tiles it read them for 4, and the pass took 775 us a 2048-token step instead of 695).
 constexpr int GBK2 = 64;                       // K step of the down pass
 constexpr int D_HT = GBM * GBK2 * 2;           // bytes of one h term tile
-constexpr int D_WT = GBN * GBK2;               // bytes of the weight tile
-template <int TERMS>
-constexpr int d_sbytes() { return TERMS * D_HT + D_WT; }        // one stage's operands
-template <int TERMS>
-constexpr int d_stot() { return d_sbytes<TERMS>() + GTHREADS * 4; }  // + the weight scale (64 words a wave)
-template <int TERMS>
-constexpr int d_lps() { return 2 * TERMS + 1 + 1; }             // loads a wave issues per stage
 
 typedef __bf16 gbf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ int wchunk_pos(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
 
-struct DSrc {
+constexpr int GBNW = 256;                      // outputs per block tile
+constexpr int DW_WT = GBNW * GBK2;             // bytes of the weight tile
+template <int TERMS>
+constexpr int dw_sbytes() { return TERMS * D_HT + DW_WT; }
+template <int TERMS>
+constexpr int dw_stot() { return dw_sbytes<TERMS>() + GTHREADS * 4; }
+template <int TERMS>
+constexpr int dw_lps() { return 2 * TERMS + 2 + 1; }
+
+struct DWSrc {
     __amdgpu_buffer_rsrc_t hr, wr, sr;
-    int ho[2], wo;  // step-0 byte offsets (the terms share ho: hl is at hh + plane bytes)
-    int hl_off;     // bytes from hh to hl
-    int so;         // step-0 byte offset of this lane's weight scale (G_OOB: none)
+    int ho[2], wo[2];
+    int hl_off;
+    int so;
 };
 
 template <int TERMS>
-__device__ __forceinline__ void d_issue(const DSrc& s, int kb, int nkb, uint8_t* sb, float* scw, int wave) {
+__device__ __forceinline__ void dw_issue(const DWSrc& s, int kb, int nkb, uint8_t* sb, float* scw, int wave) {
     const bool ok = kb < nkb;
-    const int k0 = kb * GBK2 * 2;  // bytes into an h row
+    const int k0 = kb * GBK2 * 2;
 #pragma unroll
     for (int t = 0; t < TERMS; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
             dma16(s.hr, sb + t * D_HT + (2 * wave + j) * 1024, ok ? s.ho[j] + t * s.hl_off + k0 : G_OOB);
-    dma16(s.wr, sb + TERMS * D_HT + wave * 1024, ok ? s.wo + kb * GBK2 : G_OOB);
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        dma16(s.wr, sb + TERMS * D_HT + (2 * wave + j) * 1024, ok ? s.wo[j] + kb * GBK2 : G_OOB);
     dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
 }
 
-// One step's operand reads from stage buffer sb, as one block of ds_reads the compiler
-// does not see as LDS loads: its wait-count pass cannot tell at the loop head which
-// stage buffer a direct-to-LDS load in flight writes, and would wait for all of them
-// (the next stages' too) before the first read. The step's own loads are complete by
-// then: each wave waited for its loads of the stage (wait_vm) before the block barrier.
-// A: h term t, row half hf of M subtile ms (ms: +2048 bytes, t: +D_HT); B: weight rows
-// of N subtile ns (+1024 bytes each); then this wave's weight block scale.
+// A: h term t, row half hf of M subtile ms (+2048 bytes; t: +D_HT); B: weight rows of N subtile ns
+// (+1024 bytes each, 8 of them); then this wave's weight block scale.
 template <int TERMS>
-__device__ __forceinline__ void d_reads(const uint8_t* sb, int wm, int wn, int wave, int lane,
-                                        uint4 (&ra)[2][TERMS][2], uint4 (&rb)[4], float& ws) {
+__device__ __forceinline__ void dw_reads(const uint8_t* sb, int wm, int wn, int wave, int lane,
+                                         uint4 (&ra)[2][TERMS][2], uint4 (&rb)[8], float& ws) {
     typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
     const uint32_t base = (uint32_t)(uintptr_t)(lds_cptr)sb;
-    const int g = lane >> 4, row = 32 * wm + (lane & 15), wrow = 64 * wn + (lane & 15);
+    const int g = lane >> 4, row = 32 * wm + (lane & 15), wrow = 128 * wn + (lane & 15);
     const uint32_t a0 = base + 16 * chunk_pos(row, 2 * g), a1 = base + 16 * chunk_pos(row, 2 * g + 1);
     const uint32_t bb = base + TERMS * D_HT + 16 * wchunk_pos(wrow, g);
-    const uint32_t sc = base + d_sbytes<TERMS>() + 4 * 64 * wave;
+    const uint32_t sc = base + dw_sbytes<TERMS>() + 4 * 64 * wave;
     if constexpr (TERMS == 2) {
+        asm volatile(
+            "ds_read_b128 %0, %17\n\t"
+            "ds_read_b128 %1, %18\n\t"
+            "ds_read_b128 %2, %17 offset:2048\n\t"
+            "ds_read_b128 %3, %18 offset:2048\n\t"
+            "ds_read_b128 %4, %17 offset:16384\n\t"
+            "ds_read_b128 %5, %18 offset:16384\n\t"
+            "ds_read_b128 %6, %17 offset:18432\n\t"
+            "ds_read_b128 %7, %18 offset:18432\n\t"
+            "ds_read_b128 %8, %19\n\t"
+            "ds_read_b128 %9, %19 offset:1024\n\t"
+            "ds_read_b128 %10, %19 offset:2048\n\t"
+            "ds_read_b128 %11, %19 offset:3072\n\t"
+            "ds_read_b128 %12, %19 offset:4096\n\t"
+            "ds_read_b128 %13, %19 offset:5120\n\t"
+            "ds_read_b128 %14, %19 offset:6144\n\t"
+            "ds_read_b128 %15, %19 offset:7168\n\t"
+            "ds_read_b32 %16, %20\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(ra[0][1][0]),
+              "=&v"(ra[0][1][1]), "=&v"(ra[1][1][0]), "=&v"(ra[1][1][1]), "=&v"(rb[0]), "=&v"(rb[1]), "=&v"(rb[2]),
+              "=&v"(rb[3]), "=&v"(rb[4]), "=&v"(rb[5]), "=&v"(rb[6]), "=&v"(rb[7]), "=&v"(ws)
+            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
+            : "memory");
+    } else {
         asm volatile(
             "ds_read_b128 %0, %13\n\t"
             "ds_read_b128 %1, %14\n\t"
             "ds_read_b128 %2, %13 offset:2048\n\t"
             "ds_read_b128 %3, %14 offset:2048\n\t"
-            "ds_read_b128 %4, %13 offset:16384\n\t"
-            "ds_read_b128 %5, %14 offset:16384\n\t"
-            "ds_read_b128 %6, %13 offset:18432\n\t"
-            "ds_read_b128 %7, %14 offset:18432\n\t"
-            "ds_read_b128 %8, %15\n\t"
-            "ds_read_b128 %9, %15 offset:1024\n\t"
-            "ds_read_b128 %10, %15 offset:2048\n\t"
-            "ds_read_b128 %11, %15 offset:3072\n\t"
+            "ds_read_b128 %4, %15\n\t"
+            "ds_read_b128 %5, %15 offset:1024\n\t"
+            "ds_read_b128 %6, %15 offset:2048\n\t"
+            "ds_read_b128 %7, %15 offset:3072\n\t"
+            "ds_read_b128 %8, %15 offset:4096\n\t"
+            "ds_read_b128 %9, %15 offset:5120\n\t"
+            "ds_read_b128 %10, %15 offset:6144\n\t"
+            "ds_read_b128 %11, %15 offset:7168\n\t"
             "ds_read_b32 %12, %16\n\t"
             "s_waitcnt lgkmcnt(0)"
-            : "=v"(ra[0][0][0]), "=v"(ra[0][0][1]), "=v"(ra[1][0][0]), "=v"(ra[1][0][1]), "=v"(ra[0][1][0]),
-              "=v"(ra[0][1][1]), "=v"(ra[1][1][0]), "=v"(ra[1][1][1]), "=v"(rb[0]), "=v"(rb[1]), "=v"(rb[2]),
-              "=v"(rb[3]), "=v"(ws)
-            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
-            : "memory");
-    } else {
-        asm volatile(
-            "ds_read_b128 %0, %9\n\t"
-            "ds_read_b128 %1, %10\n\t"
-            "ds_read_b128 %2, %9 offset:2048\n\t"
-            "ds_read_b128 %3, %10 offset:2048\n\t"
-            "ds_read_b128 %4, %11\n\t"
-            "ds_read_b128 %5, %11 offset:1024\n\t"
-            "ds_read_b128 %6, %11 offset:2048\n\t"
-            "ds_read_b128 %7, %11 offset:3072\n\t"
-            "ds_read_b32 %8, %12\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=v"(ra[0][0][0]), "=v"(ra[0][0][1]), "=v"(ra[1][0][0]), "=v"(ra[1][0][1]), "=v"(rb[0]), "=v"(rb[1]),
-              "=v"(rb[2]), "=v"(rb[3]), "=v"(ws)
+            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(rb[0]), "=&v"(rb[1]),
+              "=&v"(rb[2]), "=&v"(rb[3]), "=&v"(rb[4]), "=&v"(rb[5]), "=&v"(rb[6]), "=&v"(rb[7]), "=&v"(ws)
             : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
             : "memory");
     }
 }
 
-// One K step: blk += the step's products (every term); every second step (and the last)
-// the 128-column block sum joins acc, scaled by the weight's block scale.
+// act: this wave's 16-row M subtiles that hold assignments (1 or 2; a subtile past the
+// expert's last assignment only repeats its first one, and its products are not stored).
 template <int TERMS>
-__device__ __forceinline__ void d_step(const uint8_t* sb, int wm, int wn, int wave, int lane, bool fold,
-                                       gf32x4 (&blk)[2][4], float (&acc)[2][4][4]) {
-    uint4 ra[2][TERMS][2], rb[4];
+__device__ __forceinline__ void dw_step(const uint8_t* sb, int wm, int wn, int wave, int lane, bool fold, int act,
+                                        gf32x4 (&blk)[2][8], float (&acc)[2][8][4]) {
+    uint4 ra[2][TERMS][2], rb[8];
     float ws;
-    d_reads<TERMS>(sb, wm, wn, wave, lane, ra, rb, ws);
+    dw_reads<TERMS>(sb, wm, wn, wave, lane, ra, rb, ws);
 #pragma unroll
-    for (int ns = 0; ns < 4; ns++) {
+    for (int ns = 0; ns < 8; ns++) {
         const uint32_t ww[4] = {rb[ns].x, rb[ns].y, rb[ns].z, rb[ns].w};
         gbf16x8 b[2];
 #pragma unroll
@@ -556,18 +571,19 @@ __device__ __forceinline__ void d_step(const uint8_t* sb, int wm, int wn, int wa
             }
 #pragma unroll
         for (int ms = 0; ms < 2; ms++)
+            if (ms < act)
 #pragma unroll
-            for (int hf = 0; hf < 2; hf++)
+                for (int hf = 0; hf < 2; hf++)
 #pragma unroll
-                for (int t = 0; t < TERMS; t++)
-                    blk[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gbf16x8, ra[ms][t][hf]),
-                                                                         b[hf], blk[ms][ns], 0, 0, 0);
+                    for (int t = 0; t < TERMS; t++)
+                        blk[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(gbf16x8, ra[ms][t][hf]), b[hf], blk[ms][ns], 0, 0, 0);
     }
     if (fold) {
 #pragma unroll
         for (int ms = 0; ms < 2; ms++)
 #pragma unroll
-            for (int ns = 0; ns < 4; ns++) {
+            for (int ns = 0; ns < 8; ns++) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[ms][ns][e] = fmaf(blk[ms][ns][e], ws, acc[ms][ns][e]);
                 blk[ms][ns] = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -575,14 +591,14 @@ __device__ __forceinline__ void d_step(const uint8_t* sb, int wm, int wn, int wa
     }
 }
 
-// Down pass: tiles from the device tile table in XCD runs, as grouped_gemm_kernel, but with
-// the N-tile fastest: the blocks an XCD runs together take the N-tiles of one M-tile, so
-// that tile's h planes come into the XCD's L2 once and serve all of them. (M-tile fastest
-// re-fetched every M-tile's h from beyond the L2 for each N-tile: 3.2 GB a 2048-token step
-// with two terms.)
+// Tiles from the device tile table in XCD runs, as grouped_gemm_kernel, but with the N-tile
+// fastest: the blocks an XCD runs together take the N-tiles of one M-tile, so that tile's h
+// planes come into the XCD's L2 once and serve all of them. (M-tile fastest re-fetched every
+// M-tile's h from beyond the L2 for each N-tile: 3.2 GB a 2048-token step with two terms.)
+// Outputs past N (hidden not a multiple of 256) read zero weights and are not stored.
 template <int TERMS>
-__global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
-    constexpr int STOT = d_stot<TERMS>(), SBYTES = d_sbytes<TERMS>();
+__global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
+    constexpr int STOT = dw_stot<TERMS>(), SBYTES = dw_sbytes<TERMS>();
     __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT], sb2[STOT];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -593,13 +609,12 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
     const int w = (L & 7) * C + (L >> 3);
     if (w >= W) return;
     const int mt = w / NT, nt = w - mt * NT;
-    const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBN;
+    const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBNW;
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
     const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
     const int nkb = (int)(g.K / GBK2);
-    DSrc src;
-    // the h planes as one resource (hl follows hh by hl_off bytes)
+    DWSrc src;
     src.hl_off = TERMS == 2 ? (int)((const uint8_t*)g.hl - (const uint8_t*)g.hh) : 0;
     src.hr = __builtin_amdgcn_make_buffer_rsrc(g.hh, (short)0, 0x7fff0000, G_BUF_FLAGS);
     src.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, (int)(g.w_off + g.N * g.K),
@@ -611,42 +626,44 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
         int a = a0 + m0 + r;
         if (a >= a1) a = a0;
         src.ho[j] = (int)(a * g.K * 2) + 16 * c;
-    }
-    {
-        const int p = wave * 64 + lane, r = p >> 2, c = (p & 3) ^ ((r >> 2) & 3);
-        src.wo = (int)(g.w_off + (int64_t)(n0 + r) * g.K) + 16 * c;
+        // weights: position (2 wave + j) 64 + lane = row p / 4, chunk (p % 4) ^ ((row >> 2) & 3)
+        const int p = (2 * wave + j) * 64 + lane, wr = p >> 2, wc = (p & 3) ^ ((wr >> 2) & 3);
+        src.wo[j] = (int)(g.w_off + (int64_t)(n0 + wr) * g.K) + 16 * wc;
     }
     src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
-    src.so = lane == 0 ? (int)(g.s_off + (int64_t)(n0 / 128) * (g.K / 128) * 4) : G_OOB;
-    float acc[2][4][4];
-    gf32x4 blk[2][4];
+    const int nw0 = n0 + 128 * wn;  // this wave's first output (its 128-row scale block)
+    const int left = a1 - (a0 + m0) - 32 * wm;  // assignments from this wave's first row on
+    const int act = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : left <= 16 ? 1 : 2);
+    src.so = lane == 0 && nw0 < g.N ? (int)(g.s_off + (int64_t)(nw0 / 128) * (g.K / 128) * 4) : G_OOB;
+    float acc[2][8][4];
+    gf32x4 blk[2][8];
 #pragma unroll
     for (int ms = 0; ms < 2; ms++)
 #pragma unroll
-        for (int ns = 0; ns < 4; ns++) {
+        for (int ns = 0; ns < 8; ns++) {
             blk[ms][ns] = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[ms][ns][e] = 0.0f;
         }
-#define D_SW(B) reinterpret_cast<float*>((B) + SBYTES)
-#define D_STEP(SB, NSB)                                                                                  \
+#define DW_SW(B) reinterpret_cast<float*>((B) + SBYTES)
+#define DW_STEP(SB, NSB)                                                                                 \
     {                                                                                                    \
-        wait_vm<d_lps<TERMS>()>();                                                                       \
+        wait_vm<dw_lps<TERMS>()>();                                                                      \
         g_barrier();                                                                                     \
-        d_issue<TERMS>(src, kb + 2, nkb, NSB, D_SW(NSB), wave);                                          \
-        d_step<TERMS>(SB, wm, wn, wave, lane, (kb & 1) || kb + 1 == nkb, blk, acc);                      \
+        dw_issue<TERMS>(src, kb + 2, nkb, NSB, DW_SW(NSB), wave);                                        \
+        if (act > 0) dw_step<TERMS>(SB, wm, wn, wave, lane, (kb & 1) || kb + 1 == nkb, act, blk, acc);   \
         if (++kb == nkb) break;                                                                          \
     }
     int kb = 0;
-    d_issue<TERMS>(src, 0, nkb, sb0, D_SW(sb0), wave);
-    d_issue<TERMS>(src, 1, nkb, sb1, D_SW(sb1), wave);
+    dw_issue<TERMS>(src, 0, nkb, sb0, DW_SW(sb0), wave);
+    dw_issue<TERMS>(src, 1, nkb, sb1, DW_SW(sb1), wave);
     for (;;) {
-        D_STEP(sb0, sb2)
-        D_STEP(sb1, sb0)
-        D_STEP(sb2, sb1)
+        DW_STEP(sb0, sb2)
+        DW_STEP(sb1, sb0)
+        DW_STEP(sb2, sb1)
     }
-#undef D_SW
-#undef D_STEP
+#undef DW_SW
+#undef DW_STEP
     wait_vm<0>();  // the zero-filled stages past the end have landed before the block ends
 #pragma unroll
     for (int ms = 0; ms < 2; ms++)
@@ -655,9 +672,9 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_bf16_kernel(GArgs g) {
             const int a = a0 + m0 + 32 * wm + 16 * ms + 4 * (lane >> 4) + e;
             if (a >= a1) continue;
 #pragma unroll
-            for (int ns = 0; ns < 4; ns++) {
-                const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
-                g.y[(int64_t)a * g.N + n] = acc[ms][ns][e];
+            for (int ns = 0; ns < 8; ns++) {
+                const int64_t n = nw0 + 16 * ns + (lane & 15);
+                if (n < g.N) g.y[(int64_t)a * g.N + n] = acc[ms][ns][e];
             }
         }
 }
@@ -671,8 +688,8 @@ int launch_grouped(const GArgs& a, int mode, dim3 grid, hipStream_t st) {
 }
 
 int launch_grouped_down(const GArgs& a, int terms, dim3 grid, hipStream_t st) {
-    if (terms == 2) hipLaunchKernelGGL(grouped_down_bf16_kernel<2>, grid, dim3(GTHREADS), 0, st, a);
-    else hipLaunchKernelGGL(grouped_down_bf16_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
+    if (terms == 2) hipLaunchKernelGGL(grouped_down_wide_kernel<2>, grid, dim3(GTHREADS), 0, st, a);
+    else hipLaunchKernelGGL(grouped_down_wide_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
     return launched("grouped_down_bf16");
 }
 
@@ -842,7 +859,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     d.hl = hl;
     d.y = y;
     const int terms = precision == OOM_EXPERT_EXACT ? 2 : 1;
-    if (int rc = launch_grouped_down(d, terms, dim3((unsigned)(geo->hidden / GBN), (unsigned)w.max_tiles + 8, 1), st))
+    if (int rc = launch_grouped_down(d, terms, dim3((unsigned)cdiv(geo->hidden, GBNW), (unsigned)w.max_tiles + 8, 1),
+                                     st))
         return rc;
     return launch_combine(y, pv.slot_assign(), weights, out, out_dtype, T, (int)geo->hidden, k, st);
 }
