@@ -87,6 +87,15 @@ extern "C" int oom_status(void* stream) {
 
 extern "C" const char* oom_last_error(void) { return oom::g_last_error.c_str(); }
 
+#ifdef OOM_STAMPS
+// The profiling build's stamp buffer (see stream.hpp); not part of the default library's ABI.
+namespace oom {
+static uint64_t* g_stamps = nullptr;
+uint64_t* stamps_buffer() { return g_stamps; }
+}  // namespace oom
+extern "C" void oom_debug_set_stamps(void* buf) { oom::g_stamps = reinterpret_cast<uint64_t*>(buf); }
+#endif
+
 extern "C" int oom_workspace_init(void* ws, size_t bytes, void* stream) {
     if (bytes == 0) return OOM_OK;
     OOM_REQUIRE(ws != nullptr, "oom_workspace_init: null workspace");

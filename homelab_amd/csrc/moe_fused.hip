@@ -70,6 +70,9 @@ struct FusedArgs {
     const uint64_t* shared_rec;
     const uint16_t* gate_w;
     float* gate;
+#ifdef OOM_STAMPS
+    uint64_t* stamps;  // phase timestamps of the one-token kernel (profiling build)
+#endif
 };
 
 // 16 consecutive activations of row `row` starting at column `col`, as fp32.
@@ -602,6 +605,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
     const uint32_t bbase = grid_barrier_base(a.bar);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if constexpr (TG == 1) OOM_STAMP(a.stamps, WB, 0);
     const int T = a.T, E = a.E, k = a.k, A = T * k;
     // the record table and (one token) the activations load while the router runs
     if (tid < E) pl.recs[tid] = a.all_recs[tid];
@@ -682,6 +686,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
         }
     }
     __syncthreads();
+    if constexpr (TG == 1) OOM_STAMP(a.stamps, WB, 1);  // routed and planned
     if (blockIdx.x == 0)
         for (int s = tid; s < A; s += blockDim.x) {
             a.ids[s] = pl.ids[s];
@@ -721,8 +726,10 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             gate1_load(a, pl, it0, NG, lane, w0);
             gate1_compute<XDT>(a, pl, it1, NG, w1, xr, lane);
         }
+        OOM_STAMP(a.stamps, WB, 2);  // gate/up items done, down weights in flight or in
         wait_mem();  // this wave's h stores (and loads) are complete before its block arrives
         grid_barrier(a, bbase);
+        OOM_STAMP(a.stamps, WB, 3);  // the grid barrier released
         // ---- phase 2, one token: the slot's h once, then per tile the 16 rows of each
         // expert into LDS and the slot-order combine by wave 0 ----
         __shared__ float ylds[FW1][2 * FD1_NP];
@@ -745,7 +752,9 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
                 down1_load<DCH>(a, pl, s0, tb, s0 < n_e, lane, d0);
                 if constexpr (SH) down_pair_load<DCH>(a, pl, k, tb, wave, true, lane, p0);
             }
+            if (tb == tb0) OOM_STAMP_AFTER(a.stamps, WB, 4, h0[DCH - 1][15]);  // the slot's h in
             const float y0 = down1_rows<DCH>(d0, h0, lane);
+            if (tb == tb0) OOM_STAMP_AFTER(a.stamps, WB, 5, y0);  // the tile's rows of the wave's slot
             if ((lane & 3) == 0) ylds[s0][prow] = y0;
             if constexpr (SH) {
                 const float ys = down_pair_row<DCH>(p0, hs, lane);
@@ -765,6 +774,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             }
             __syncthreads();
         }
+        OOM_STAMP(a.stamps, WB, 6);  // combined and stored
     } else {
         // ---- phase 1: gate/up + SwiGLU -> h, FG_R rows per item, tokens in groups of TG ----
         const int tiles_g = (int)((a.I + FG_R - 1) / FG_R), NG = n_e * tiles_g;
@@ -879,6 +889,9 @@ static FusedArgs fused_args(const float* logits, const void* x, const uint64_t* 
     a.shared_rec = nullptr;
     a.gate_w = nullptr;
     a.gate = nullptr;
+#ifdef OOM_STAMPS
+    a.stamps = stamps_buffer();
+#endif
     return a;
 }
 

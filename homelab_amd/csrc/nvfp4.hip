@@ -376,18 +376,23 @@ struct Fused4Args {
     uint32_t* bar;
     uint32_t* status;  // the device's status word: 1 if the grid barrier's wait gave up
     uint32_t spin;     // polls before a wait gives up
+#ifdef OOM_STAMPS
+    uint64_t* stamps;  // phase timestamps (profiling build)
+#endif
 };
 
 // Rows 0 .. rows - 1 of h (f32, width K) into LDS in stage4's lane order through
-// device-coherent 16-byte loads, four in flight per thread; zeros past K.
+// device-coherent 16-byte loads, eight in flight per thread (one round for 10 rows of 640:
+// each round costs a trip to the device's point of coherence); zeros past K.
 __device__ __forceinline__ void stage_rows_dev(float4* xs4, const float* h, int K, int CH, int rows) {
+    constexpr int R = 8;  // loads in flight per thread
     const int span = CH * 1024, nvec = rows * span / 4;
     const __amdgpu_buffer_rsrc_t hr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(h), (short)0, rows * K * 4, BUF_FLAGS);
-    for (int base = 0; base < nvec; base += 256 * 4) {
-        uint4 v[4];
+    for (int base = 0; base < nvec; base += 256 * R) {
+        uint4 v[R];
 #pragma unroll
-        for (int n = 0; n < 4; n++) {
+        for (int n = 0; n < R; n++) {
             const int i = base + (int)threadIdx.x + 256 * n;
             const int t = i * 4 / span, kk = i * 4 - t * span;
             const auto q = __builtin_amdgcn_raw_buffer_load_b128(hr, i < nvec && kk < K ? (t * K + kk) * 4 : OOB, 0,
@@ -395,7 +400,7 @@ __device__ __forceinline__ void stage_rows_dev(float4* xs4, const float* h, int 
             v[n] = make_uint4(q[0], q[1], q[2], q[3]);
         }
 #pragma unroll
-        for (int n = 0; n < 4; n++) {
+        for (int n = 0; n < R; n++) {
             const int i = base + (int)threadIdx.x + 256 * n;
             if (i >= nvec) break;
             const int t = i * 4 / span, kk = i * 4 - t * span;
@@ -478,12 +483,26 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const Rec4& g = a.g;
     const int k = a.k, H = g.H, I = g.I;
+    OOM_STAMP(a.stamps, N4_WAVES, 0);
     if (wave == 0) {
+        // every expert's record address (lane l holds experts l + 64 q) loads beside the
+        // logits, so no load waits on the picks
+        uint64_t rr[EQ];
+#pragma unroll
+        for (int q = 0; q < EQ; q++) rr[q] = lane + 64 * q < a.E ? a.all_recs[lane + 64 * q] : 0ull;
         int id = 0;
         float w = 0.0f;
         route_token_regs<EQ>(a.logits, a.E, k, lane, id, w);
+        // pick `lane`'s record: register id / 64 of lane id % 64
+        uint64_t rec = 0;
+#pragma unroll
+        for (int q = 0; q < EQ; q++) {
+            const uint64_t v = (uint64_t)__shfl((long long)rr[q], id & 63, 64);
+            if ((id >> 6) == q) rec = v;
+        }
+        OOM_STAMP_AFTER(a.stamps, N4_WAVES, 1, rec);  // routed (wave 0)
         if (lane < k) {
-            recs_l[lane] = a.all_recs[id];
+            recs_l[lane] = rec;
             w_l[lane] = w;
             if (blockIdx.x == 0) {
                 a.ids[lane] = id;
@@ -494,6 +513,7 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     const int CHH = (H + 1023) >> 10, CHI = (I + 1023) >> 10;
     stage4<XDT>(xs4, a.x, H, CHH, 1, [](int) { return 0; });
     __syncthreads();
+    OOM_STAMP(a.stamps, N4_WAVES, 2);  // x staged, the picks shared
     // ---- phase 1: h[s, j0 .. j0 + 2 N4_GP) per wave item ----
     const int ipe = (I + 2 * N4_GP - 1) / (2 * N4_GP), NG = k * ipe;
     const int NW = gridDim.x * N4_WAVES;
@@ -504,11 +524,14 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
         float* hs = a.h + (size_t)s * I;
         gu4_pass<1, 4>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
     }
+    OOM_STAMP(a.stamps, N4_WAVES, 3);  // gate/up items done
     wait_mem();  // this wave's h stores are complete before its block arrives
     grid_barrier_words(a.bar, bbase, a.status, a.spin);
+    OOM_STAMP(a.stamps, N4_WAVES, 4);  // the grid barrier released
     // ---- phase 2: the k h rows once, then per output tile the slot rows and the combine ----
     stage_rows_dev(xs4, a.h, I, CHI, k);
     __syncthreads();
+    OOM_STAMP(a.stamps, N4_WAVES, 5);  // h staged
     const int tiles = (H + 2 * N4_DP - 1) / (2 * N4_DP);
     for (int tb = blockIdx.x; tb < tiles; tb += gridDim.x) {
         const int r0 = tb * 2 * N4_DP;
@@ -534,7 +557,9 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
             store_out<ODT>(a.out, row, acc);
         }
         __syncthreads();
+        if (tb == (int)blockIdx.x) OOM_STAMP(a.stamps, N4_WAVES, 6);  // first tile combined
     }
+    OOM_STAMP(a.stamps, N4_WAVES, 7);
     grid_barrier_exit(a.bar);
 }
 
@@ -682,6 +707,9 @@ extern "C" int oom_moe_decode_nvfp4(const float* logits, const void* x, int x_dt
         if (!status) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_nvfp4: the device status word has no address");
         Fused4Args a{logits, x, all_recs, E, k, rec4_of(*geo), ids, weights, out, h,
                      reinterpret_cast<uint32_t*>(base + WS_BAR), status, wait_limit()};
+#ifdef OOM_STAMPS
+        a.stamps = stamps_buffer();
+#endif
         const size_t lds = fused4_lds(*geo, k);
         return x_dtype == OOM_BF16 ? launch_fused4_e<OOM_BF16>(a, out_dtype, lds, st)
                                    : launch_fused4_e<OOM_F32>(a, out_dtype, lds, st);

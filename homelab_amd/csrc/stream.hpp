@@ -28,6 +28,38 @@ constexpr int MAX_TILES = 4096 / 8;     // row tiles of 8 rows for hidden <= 409
 constexpr size_t WS_TICKETS = WS_BAR2 + BAR_WORDS * 4;            // MAX_TILES lines
 constexpr size_t WS_HEADER = (WS_TICKETS + (size_t)MAX_TILES * TICKET_STRIDE * 4 + 4095) & ~size_t(4095);
 
+// ---- phase timestamps (a profiling build only) -----------------------------------------
+// Built with -DOOM_STAMPS (stamps.py at the repository root builds that library apart from
+// liboom_hip.so), the one-launch decode kernels record the device's 100 MHz real-time clock
+// per wave at their phase boundaries: wave w of block b writes point p to
+// stamps[(b * waves + w) * STAMP_POINTS + p] (stamps: the buffer last handed to
+// oom_debug_set_stamps; none: nothing is written). The default build compiles none of it.
+constexpr int STAMP_POINTS = 8;
+#ifdef OOM_STAMPS
+uint64_t* stamps_buffer();
+#define OOM_STAMP(buf, waves, p)                                                                         \
+    do {                                                                                                 \
+        __builtin_amdgcn_sched_barrier(0);                                                               \
+        const uint64_t t_ = wall_clock64();                                                              \
+        if ((buf) && (threadIdx.x & 63) == 0)                                                            \
+            (buf)[((size_t)blockIdx.x * (waves) + (threadIdx.x >> 6)) * STAMP_POINTS + (p)] = t_;        \
+        __builtin_amdgcn_sched_barrier(0);                                                               \
+    } while (0)
+// the stamp after v is computed (v's producers complete first)
+#define OOM_STAMP_AFTER(buf, waves, p, v)      \
+    do {                                       \
+        asm volatile("" ::"v"(v));             \
+        OOM_STAMP(buf, waves, p);              \
+    } while (0)
+#else
+#define OOM_STAMP(buf, waves, p) \
+    do {                         \
+    } while (0)
+#define OOM_STAMP_AFTER(buf, waves, p, v) \
+    do {                                  \
+    } while (0)
+#endif
+
 // ---- loads ----------------------------------------------------------------------------
 
 __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, int off) {
