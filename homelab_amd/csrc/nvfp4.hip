@@ -529,17 +529,19 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     grid_barrier_words(a.bar, bbase, a.status, a.spin);
     OOM_STAMP(a.stamps, N4_WAVES, 4);  // the grid barrier released
     // ---- phase 2: the k h rows once, then per output tile the slot rows and the combine ----
+    // slots wave, wave + 4, ...: the next slot's loads are in flight while the current one
+    // is reduced (a slot past k loads through an empty resource: zeros, no access); the
+    // first tile's first slot loads before h is staged, so the two loads' latencies overlap
+    const int tiles = (H + 2 * N4_DP - 1) / (2 * N4_DP);
+    const auto rsrc_of = [&](int s) { return uniform_rsrc(recs_l[s < k ? s : 0], s < k ? g.bytes : 0); };
+    Dn4W wa, wb;
+    if ((int)blockIdx.x < tiles) dn4_load(wa, g, rsrc_of(wave), (int)blockIdx.x * 2 * N4_DP, lane);
     stage_rows_dev(xs4, a.h, I, CHI, k);
     __syncthreads();
     OOM_STAMP(a.stamps, N4_WAVES, 5);  // h staged
-    const int tiles = (H + 2 * N4_DP - 1) / (2 * N4_DP);
     for (int tb = blockIdx.x; tb < tiles; tb += gridDim.x) {
         const int r0 = tb * 2 * N4_DP;
-        // slots wave, wave + 4, ...: the next slot's loads are in flight while the current
-        // one is reduced (a slot past k loads through an empty resource: zeros, no access)
-        const auto rsrc_of = [&](int s) { return uniform_rsrc(recs_l[s < k ? s : 0], s < k ? g.bytes : 0); };
-        Dn4W wa, wb;
-        dn4_load(wa, g, rsrc_of(wave), r0, lane);
+        if (tb != (int)blockIdx.x) dn4_load(wa, g, rsrc_of(wave), r0, lane);
         for (int s = wave; s < k;) {
             dn4_load(wb, g, rsrc_of(s + N4_WAVES), r0, lane);
             dn4_compute(wa, xs4 + (size_t)s * CHI * 256, g, r0, lane, [&](int row, float v) { ylds[s][row - r0] = v; });
