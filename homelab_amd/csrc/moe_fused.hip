@@ -605,7 +605,10 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
     const uint32_t bbase = grid_barrier_base(a.bar);
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if constexpr (TG == 1) OOM_STAMP(a.stamps, WB, 0);
+    if constexpr (TG == 1) {
+        OOM_STAMP(a.stamps, WB, 0);
+        OOM_STAMP_WHERE(a.stamps, WB);
+    }
     const int T = a.T, E = a.E, k = a.k, A = T * k;
     // the record table and (one token) the activations load while the router runs
     if (tid < E) pl.recs[tid] = a.all_recs[tid];

@@ -51,7 +51,20 @@ uint64_t* stamps_buffer();
         asm volatile("" ::"v"(v));             \
         OOM_STAMP(buf, waves, p);              \
     } while (0)
+// where the wave runs, in the last point: XCC_ID (hardware register 20, bits 3:0) in bits
+// 32..35, HW_ID (register 4: wave 3:0, SIMD 5:4, CU 11:8, SH 12, SE 15:13) in bits 0..31
+#define OOM_STAMP_WHERE(buf, waves)                                                                      \
+    do {                                                                                                 \
+        const uint64_t x_ = (uint32_t)__builtin_amdgcn_s_getreg(20 | (15 << 11));                       \
+        const uint64_t h_ = (uint32_t)__builtin_amdgcn_s_getreg(4 | (31 << 11));                         \
+        if ((buf) && (threadIdx.x & 63) == 0)                                                            \
+            (buf)[((size_t)blockIdx.x * (waves) + (threadIdx.x >> 6)) * STAMP_POINTS + STAMP_POINTS - 1] = \
+                (x_ << 32) | h_;                                                                         \
+    } while (0)
 #else
+#define OOM_STAMP_WHERE(buf, waves) \
+    do {                            \
+    } while (0)
 #define OOM_STAMP(buf, waves, p) \
     do {                         \
     } while (0)

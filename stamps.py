@@ -32,6 +32,10 @@ NAMES = {
 }
 
 
+# the point whose per-block distribution is broken down by XCD (hardware id in the last point)
+WHERE_POINT = {"decode1": 2}
+
+
 def build_stamps():
     from homelab_amd import build as b
 
@@ -107,21 +111,29 @@ def main():
         step(i)
     torch.cuda.synchronize()
     lib.oom_debug_set_stamps(ctypes.c_void_p(buf.data_ptr()))
-    rel, spans = [], []
+    rel, spans, per_block = [], [], []
+    npt = len(NAMES[args.config])
     try:
         for i in range(args.warmup, args.warmup + args.calls):
             buf.zero_()
             torch.cuda.synchronize()
             step(i)
             torch.cuda.synchronize()
-            t = buf.cpu().numpy().reshape(blocks * waves, POINTS).astype(np.float64)
-            t = t[t[:, 0] > 0]  # the waves of the launched blocks
+            raw = buf.cpu().numpy().reshape(blocks, waves, POINTS)
+            launched = raw[:, 0, 0] > 0
+            raw = raw[launched]
+            t = raw.reshape(-1, POINTS).astype(np.float64)
             t0 = t[:, 0].min()
-            npt = len(NAMES[args.config])
             r = (t[:, :npt] - t0) * 0.01  # 100 MHz ticks -> us
             r[t[:, :npt] == 0] = np.nan  # a point the wave never passed (a block with no output tile)
             rel.append(r)
             spans.append(np.nanmax(r[:, npt - 1]))
+            if WHERE_POINT.get(args.config) is not None:
+                # per block: the last wave's stamp of the phase-end point, and where block ran
+                done = np.nanmax(r[:, WHERE_POINT[args.config]].reshape(-1, waves), axis=1)
+                where = raw[:, 0, POINTS - 1].astype(np.uint64)
+                per_block.append((done, (where >> np.uint64(32)) & np.uint64(15),
+                                  (where >> np.uint64(8)) & np.uint64(0xff)))
     finally:
         lib.oom_debug_set_stamps(None)
     status = hip.status()
@@ -133,6 +145,21 @@ def main():
         print(f"{name:<20} {v.min():8.2f} {np.percentile(v, 10):8.2f} {np.median(v):8.2f} {np.percentile(v, 90):8.2f}"
               f" {v.max():8.2f}   ({v.size // args.calls} waves a call)")
     print(f"call span (last wave's end): median {np.median(spans):.2f} us, min {min(spans):.2f}, max {max(spans):.2f}")
+    if per_block:
+        # the phase end per block (its last wave), by the XCD the block ran on
+        name = NAMES[args.config][WHERE_POINT[args.config]]
+        done = np.concatenate([d for d, _, _ in per_block])
+        xcc = np.concatenate([x for _, x, _ in per_block]).astype(int)
+        print(f"per block, {name} (its last wave): p10 {np.percentile(done, 10):.2f}, p50 {np.median(done):.2f}, "
+              f"p90 {np.percentile(done, 90):.2f}, max {done.max():.2f}")
+        for x in range(int(xcc.max()) + 1):
+            v = done[xcc == x]
+            if v.size:
+                print(f"  XCD {x}: {v.size // args.calls:4d} blocks a call, p50 {np.median(v):.2f}, "
+                      f"p90 {np.percentile(v, 90):.2f}, max {v.max():.2f}")
+        # does the same (XCD, SE/CU) finish last call after call?
+        last = [(int(x[np.argmax(d)]), int(c[np.argmax(d)])) for d, x, c in per_block]
+        print("  last block of each call (XCD, hw id bits 8..15):", " ".join(f"{x}/{c:02x}" for x, c in last))
     del keep
     return 0
 
