@@ -90,6 +90,64 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const void* __restrict_
     }
 }
 
+// The same quantiser for rows whose width is a multiple of 8 and at most QV_MAXC: one pass
+// over memory. Thread t holds chunks of 8 consecutive elements (16-byte bf16 or 2 x 16-byte
+// f32 loads) in registers, the row's absmax reduces over the block, and each chunk stores
+// its 8 codes as one 8-byte word. Same arithmetic as quant_rows_kernel (bit-identical codes
+// and scales).
+constexpr int QV_CH = 4;                 // chunks a thread
+constexpr int QV_MAXC = 256 * 8 * QV_CH; // widest row of the one-pass form
+template <int XDT>
+__global__ void __launch_bounds__(256) quant_rows_vec_kernel(const void* __restrict__ x, int64_t cols,
+                                                             uint8_t* __restrict__ q, float* __restrict__ scale) {
+    __shared__ float wmax[4];
+    const int64_t r = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float v[QV_CH][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QV_CH; j++) {
+        const int64_t c = (int64_t)(j * 256 + tid) * 8;
+        if (c < cols) {
+            if constexpr (XDT == OOM_BF16) {
+                const uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + r * cols + c);
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v[j][2 * i] = __uint_as_float(ww[i] << 16);
+                    v[j][2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+                }
+            } else {
+                const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + r * cols + c);
+                const float4 a = p[0], b = p[1];
+                v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
+                v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[j][i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) m = fmaxf(m, fabsf(v[j][i]));
+    }
+    m = wave_max(m);
+    if (lane == 0) wmax[wave] = m;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+    if (tid == 0) scale[r] = s;
+#pragma unroll
+    for (int j = 0; j < QV_CH; j++) {
+        const int64_t c = (int64_t)(j * 256 + tid) * 8;
+        if (c < cols) {
+            uint32_t p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[i] = e4m3_pair(v[j][2 * i] / s, v[j][2 * i + 1] / s);
+            *reinterpret_cast<uint2*>(q + r * cols + c) = make_uint2(p[0] | (p[1] << 16), p[2] | (p[3] << 16));
+        }
+    }
+}
+
 // ---- the tile table of a device plan: tile mt = (expert i, assignments from off[i] + m0).
 // One block of 1024 threads; experts in chunks of 1024 with a running carry.
 __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __restrict__ n_e_p,
@@ -695,6 +753,13 @@ int launch_grouped_down(const GArgs& a, int terms, dim3 grid, hipStream_t st) {
 
 int launch_quant_rows(const void* x, int xdt, int64_t rows, int64_t cols, uint8_t* q, float* s, hipStream_t st) {
     if (rows == 0) return OOM_OK;
+    if (cols % 8 == 0 && cols <= QV_MAXC && aligned(x, 16) && aligned(q, 8)) {
+        if (xdt == OOM_BF16)
+            hipLaunchKernelGGL(quant_rows_vec_kernel<OOM_BF16>, dim3((unsigned)rows), dim3(256), 0, st, x, cols, q, s);
+        else
+            hipLaunchKernelGGL(quant_rows_vec_kernel<OOM_F32>, dim3((unsigned)rows), dim3(256), 0, st, x, cols, q, s);
+        return launched("quantize_rows_fp8");
+    }
     if (xdt == OOM_BF16)
         hipLaunchKernelGGL(quant_rows_kernel<OOM_BF16>, dim3((unsigned)rows), dim3(256), 0, st, x, cols, q, s);
     else

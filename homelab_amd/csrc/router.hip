@@ -46,25 +46,99 @@ __device__ int block_exclusive_scan(int v, int* warp_tot, int& total) {
 
 // The routing plan of crates/oominf-models-qwen/src/moe.rs:539-582,638-649 with every
 // expert resident: slots grouped by expert in id order, each expert's slots in slot
-// order. One block of 1024 threads; LDS: count[E] (then start[E]), ids of one round.
+// order. One block of 1024 threads (16 waves).
+//
+// E <= PLAN_FAST_E: wave w owns the contiguous slots [w C, w C + C), C = A / 16 rounded up
+// to whole rounds of 64. Within a round, the lanes holding the same id find each other by
+// ballots over the id's bits (rank = peers below this lane, the lowest peer leads).
+// Pass 1 counts each id over the wave's slots into its row of wcnt[16][E] (the leader adds
+// the round's count); the column sums are the experts' counts, from which the experts,
+// offsets and start[e] follow; one scan down each column turns the rows into each wave's
+// first position per id (start[e] plus the waves before); pass 2 walks the slots again and
+// places them, the leader advancing the wave's position after the round. A wave's LDS
+// accesses run in program order, so the block syncs only between the phases. Ids load
+// PB rounds at a time, all in flight together.
+// Larger E: counts by LDS atomics, then positions in rounds of 1024 slots (a slot's rank
+// among the equal ids before it in the round).
+constexpr int PLAN_PB = 16;
 __global__ void __launch_bounds__(1024) moe_plan_kernel(const int32_t* __restrict__ ids, int A, int E, int k,
                                                         const uint64_t* __restrict__ all_recs, int32_t* plan_base,
                                                         uint64_t* __restrict__ recs) {
     extern __shared__ int lds[];
     int* count = lds;          // [E]; becomes start[E] in place
     int* start = lds;
-    int* round_ids = lds + E;  // [1024]
+    int* wcnt = lds + E;       // [16][E] (E <= PLAN_FAST_E)
+    int* round_ids = lds + E;  // [1024] (larger E)
     __shared__ int warp_tot[16];
     __shared__ int bad;
     PlanView plan{plan_base, E, A};
-    int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = (int)blockDim.x >> 6;
+    const bool fast = E <= PLAN_FAST_E;
+    const int nbits = 32 - __builtin_clz((unsigned)max(E - 1, 1));
+    const int chunk = (((A + nw - 1) / nw) + 63) & ~63;
+    const int s0 = min(A, wave * chunk), s1 = min(A, s0 + chunk);
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    // peers of this lane's id in the round (e < 0: none), its rank among them and their number
+    auto match = [&](int e, int& rank) -> int {
+        uint64_t peers = __ballot(e >= 0);
+        for (int b = 0; b < nbits; b++) {
+            const uint64_t bal = __ballot(e >= 0 && ((e >> b) & 1));
+            peers &= ((e >> b) & 1) ? bal : ~bal;
+        }
+        rank = (int)__builtin_popcountll(peers & below);
+        return (int)__builtin_popcountll(peers);
+    };
+    // this wave's ids of rounds b0 .. b0 + PLAN_PB (-1 past its slots)
+    auto load_ids = [&](int b0, int (&eb)[PLAN_PB]) {
+#pragma unroll
+        for (int r = 0; r < PLAN_PB; r++) {
+            const int sl = b0 + 64 * r + lane;
+            eb[r] = sl < s1 ? ids[sl] : -1;
+        }
+    };
     if (tid == 0) bad = 0;
     for (int e = tid; e < E; e += blockDim.x) count[e] = 0;
+    if (fast)
+        for (int i = lane; i < E; i += 64) wcnt[wave * E + i] = 0;
     __syncthreads();
-    for (int s = tid; s < A; s += blockDim.x) {
-        int e = ids[s];
-        if (e < 0 || e >= E) bad = 1;
-        else atomicAdd(&count[e], 1);
+    if (fast) {
+        for (int b0 = s0; b0 < s1; b0 += 64 * PLAN_PB) {
+            int eb[PLAN_PB];
+            load_ids(b0, eb);
+#pragma unroll
+            for (int r = 0; r < PLAN_PB; r++) {
+                if (b0 + 64 * r >= s1) break;  // wave-uniform
+                const bool in = b0 + 64 * r + lane < s1;
+                const bool ok = eb[r] >= 0 && eb[r] < E;
+                if (in && !ok) bad = 1;
+                int rank;
+                const int n = match(ok ? eb[r] : -1, rank);
+                if (ok && rank == 0) wcnt[wave * E + eb[r]] += n;
+                wave_lds_order();
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < E; i += blockDim.x) {
+            int c = 0;
+            for (int w = 0; w < nw; w++) c += wcnt[w * E + i];
+            count[i] = c;
+        }
+    } else {
+        for (int b0 = 0; b0 < A; b0 += (int)blockDim.x * PLAN_PB) {
+            int eb[PLAN_PB];
+#pragma unroll
+            for (int r = 0; r < PLAN_PB; r++) {
+                const int sl = b0 + r * (int)blockDim.x + tid;
+                eb[r] = sl < A ? ids[sl] : -1;
+            }
+#pragma unroll
+            for (int r = 0; r < PLAN_PB; r++) {
+                if (b0 + r * (int)blockDim.x + tid >= A) break;
+                const int e = eb[r];
+                if (e < 0 || e >= E) bad = 1;
+                else atomicAdd(&count[e], 1);
+            }
+        }
     }
     __syncthreads();
     if (bad) {
@@ -97,46 +171,44 @@ __global__ void __launch_bounds__(1024) moe_plan_kernel(const int32_t* __restric
     for (int i = n_e + tid; i <= E; i += blockDim.x) plan.off()[i] = A;
     if (tid == 0) *plan.n_e() = n_e;
     __syncthreads();
-    if (E <= PLAN_FAST_E) {
-        // Positions in rounds of 1024 slots. Within a wave, the lanes holding the same id
-        // find each other by ballots over the id's bits (rank = peers below this lane);
-        // per-wave counts per id in LDS give the waves before this one.
-        int* wcnt = lds + E;  // [16][E]
-        const int lane = tid & 63, wave = tid >> 6, nbits = 32 - __builtin_clz((unsigned)max(E - 1, 1));
-        for (int base = 0; base < A; base += blockDim.x) {
-            for (int i = tid; i < 16 * E; i += blockDim.x) wcnt[i] = 0;
-            __syncthreads();
-            const int s = base + tid;
-            const int e = s < A ? ids[s] : -1;
-            uint64_t peers = __ballot(e >= 0);
-            for (int b = 0; b < nbits; b++) {
-                const uint64_t bal = __ballot(e >= 0 && ((e >> b) & 1));
-                peers &= ((e >> b) & 1) ? bal : ~bal;
+    if (fast) {
+        for (int i = tid; i < E; i += blockDim.x) {
+            int acc = start[i];
+            for (int w = 0; w < nw; w++) {
+                const int c = wcnt[w * E + i];
+                wcnt[w * E + i] = acc;
+                acc += c;
             }
-            const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-            const int rank = (int)__builtin_popcountll(peers & below);
-            if (e >= 0 && rank == 0) wcnt[wave * E + e] = (int)__builtin_popcountll(peers);
-            __syncthreads();
-            if (e >= 0) {
-                int pos = start[e] + rank;
-                for (int w = 0; w < wave; w++) pos += wcnt[w * E + e];
-                plan.assign_tok()[pos] = s / k;
-                plan.slot_assign()[s] = pos;
+        }
+        __syncthreads();
+        for (int b0 = s0; b0 < s1; b0 += 64 * PLAN_PB) {
+            int eb[PLAN_PB];
+            load_ids(b0, eb);
+#pragma unroll
+            for (int r = 0; r < PLAN_PB; r++) {
+                if (b0 + 64 * r >= s1) break;  // wave-uniform
+                const int sl = b0 + 64 * r + lane, e = eb[r];
+                int rank;
+                const int n = match(e, rank);
+                if (e >= 0) {
+                    const int pos = wcnt[wave * E + e] + rank;
+                    plan.assign_tok()[pos] = sl / k;
+                    plan.slot_assign()[sl] = pos;
+                }
+                wave_lds_order();  // every lane has read the position before the leader advances it
+                if (e >= 0 && rank == 0) wcnt[wave * E + e] += n;
+                wave_lds_order();
             }
-            __syncthreads();
-            for (int i = tid; i < E; i += blockDim.x) {
-                int c = 0;
-                for (int w = 0; w < 16; w++) c += wcnt[w * E + i];
-                start[i] += c;
-            }
-            __syncthreads();
         }
         return;
     }
-    // Positions in rounds of blockDim slots: a slot's rank among the equal ids before it.
+    // Positions in rounds of blockDim slots: a slot's rank among the equal ids before it
+    // (each round's id loads one round ahead).
+    int e_next = tid < A ? ids[tid] : -1;
     for (int base = 0; base < A; base += blockDim.x) {
         int s = base + tid;
-        int e = s < A ? ids[s] : -1;
+        int e = s < A ? e_next : -1;
+        e_next = s + (int)blockDim.x < A ? ids[s + blockDim.x] : -1;
         round_ids[tid] = e;
         __syncthreads();
         int pos = 0;
