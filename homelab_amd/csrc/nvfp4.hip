@@ -348,8 +348,8 @@ static size_t stage_lds(int64_t width) { return (size_t)N4_TB * cdiv(width, 1024
 // ---- one token in one launch ---------------------------------------------------------------
 // The step of oom_moe_decode_nvfp4 for T = 1 as one persistent kernel, the same arithmetic
 // as the five-launch step (router, plan, gate/up, down, slot-order combine):
-//   - every block routes the token on wave 0 (route_token_regs: the router kernel's picks
-//     and weights) while its other waves stage x into LDS; with one token each picked
+//   - every block routes the token on wave 0 (route_picks: the router kernel's picks and
+//     weights, by a radix descent on ballots) while its other waves stage x into LDS; with one token each picked
 //     expert has one assignment, so h row s belongs to slot s and no plan is built;
 //   - phase 1: wave items (slot, 2 N4_GP intermediate rows) in global wave order, h stored
 //     device-coherent (waves of other XCDs read it after the barrier);
@@ -479,6 +479,9 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     extern __shared__ float4 xs4[];
     __shared__ uint64_t recs_l[N4F_KMAX];
     __shared__ float w_l[N4F_KMAX];
+    __shared__ uint64_t pk_keys[N4F_KMAX];  // routing scratch (route_picks)
+    __shared__ int pk_ids[N4F_KMAX];
+    __shared__ float pk_p[N4F_KMAX];
     __shared__ float ylds[N4F_KMAX][2 * N4_DP];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const Rec4& g = a.g;
@@ -492,7 +495,7 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
         for (int q = 0; q < EQ; q++) rr[q] = lane + 64 * q < a.E ? a.all_recs[lane + 64 * q] : 0ull;
         int id = 0;
         float w = 0.0f;
-        route_token_regs<EQ>(a.logits, a.E, k, lane, id, w);
+        route_picks<EQ>(a.logits, a.E, k, lane, pk_keys, pk_ids, pk_p, id, w);
         // pick `lane`'s record: register id / 64 of lane id % 64
         uint64_t rec = 0;
 #pragma unroll

@@ -161,6 +161,80 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ l, in
     if (lane < k) w_out = w_out / picked;
 }
 
+// route_token_regs's picks and weights for one token (E <= 64 EQ <= 512, k <= 64) without
+// k serial wave maxima: lane r < k ends with pick r's id and weight, bit for bit as
+// route_token_regs computes them. The probabilities and their sum follow route_token_regs;
+// each expert's key is 1 << 40 | p's bits << 9 | (511 - id) (larger p first, ties to the
+// lower id, as the reference's argmax), the k-th largest key comes from a radix descent on
+// ballots, the picks go to LDS in id order and rank themselves by key, and the weights
+// renormalise by the picks' sum in pick order. keys, ids and p are k-entry LDS scratch.
+template <int EQ>
+__device__ __forceinline__ void route_picks(const float* __restrict__ l, int E, int k, int lane, uint64_t* keys,
+                                            int* ids, float* p, int& id_out, float& w_out) {
+    static_assert(EQ == 4 || EQ == 8, "4 or 8 logits per lane");
+    float lv[EQ];
+    float m = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        lv[q] = lane + 64 * q < E ? l[lane + 64 * q] : -INFINITY;
+        m = fmaxf(m, lv[q]);
+    }
+    m = wave_max(m);
+    float ex[EQ], w8[8];
+#pragma unroll
+    for (int q = 0; q < EQ; q++) ex[q] = lane + 64 * q < E ? expf(lv[q] - m) : 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        float vt = 0.0f + ex[q];
+        if constexpr (EQ == 8) vt = vt + ex[q + 4];
+        const float s = sum32_xor_order(vt);
+        w8[2 * q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+        w8[2 * q + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+    }
+    const float sum = ((w8[0] + w8[4]) + (w8[2] + w8[6])) + ((w8[1] + w8[5]) + (w8[3] + w8[7]));
+    uint64_t key[EQ];
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        const int e = lane + 64 * q;
+        key[q] = e < E ? (1ull << 40) | ((uint64_t)__float_as_uint(ex[q] / sum) << 9) | (uint64_t)(511 - e) : 0ull;
+    }
+    uint64_t kth = 1ull << 40;
+    for (int b = 39; b >= 0; b--) {
+        const uint64_t cand = kth | (1ull << b);
+        int cnt = 0;
+#pragma unroll
+        for (int q = 0; q < EQ; q++) cnt += (int)__builtin_popcountll(__ballot(key[q] >= cand));
+        if (cnt >= k) {
+            kth = cand;
+            if (cnt == k) break;
+        }
+    }
+    int base = 0;
+#pragma unroll
+    for (int q = 0; q < EQ; q++) {
+        const uint64_t sel = __ballot(key[q] >= kth);
+        if (key[q] >= kth)
+            keys[base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sel >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sel, 0u))] =
+                key[q];
+        base += (int)__builtin_popcountll(sel);
+    }
+    wave_lds_order();
+    const uint64_t mine = lane < k ? keys[lane] : 0ull;
+    int rank = 0;
+    for (int j = 0; j < k; j++) rank += keys[j] > mine;
+    if (lane < k) {
+        ids[rank] = 511 - (int)(mine & 511u);
+        p[rank] = __uint_as_float((uint32_t)(mine >> 9) & 0x7fffffffu);
+    }
+    wave_lds_order();
+    float picked = 0.0f;
+    for (int r = 0; r < k; r++) picked += p[r];
+    if (lane < k) {
+        id_out = ids[lane];
+        w_out = p[lane] / picked;
+    }
+}
+
 // route_token_regs's routing of one token (E <= 64 EQ <= 256, k <= 8) without k serial
 // rounds, with the one-token plan in the same pass. Every expert gets a key that orders
 // as the reference's argmax does (larger p first, ties to the lower id): bit 39 set for
