@@ -5,9 +5,10 @@
 // Each device holds its own copy of `scratch` at its own address. The host-side name of
 // the array is not a device address, so the address is looked up once per device with
 // hipGetSymbolAddress (that device current) and only that address is handed to kernels.
-// The array is zero when the code object loads; every call that completes leaves the
-// header's barrier words and tickets at zero again (a call whose wait gave up too), and
-// the rest of the workspace is written before it is read, so no call clears anything.
+// The array is zero when the code object loads. The header's barrier counters only grow
+// and agree again whenever a call ends (a call whose wait gave up too), its tickets are
+// reset by their users, and the rest of the workspace is written before it is read, so
+// no call clears anything.
 // All calls on one device share the array: calls that overlap in time on one device
 // (two streams, two threads) race, so a caller orders them on one stream.
 #include <mutex>

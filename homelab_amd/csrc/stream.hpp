@@ -18,9 +18,9 @@ constexpr int BUF_SC1 = 16;            // cache-policy bit of a device-coherent 
 // Every decode workspace starts with this header at fixed offsets, whatever the step's
 // shape, so a workspace shared by steps of different shapes (batch 1 and batch 16 of one
 // model) never reads another layout's data as its state. Each counter has a 256-byte line
-// of its own: atomics and polls on one line serialise at the memory side. Barrier areas
-// and tickets are left at zero by every call that completes, so only a new workspace
-// needs clearing (oom_workspace_init).
+// of its own: atomics and polls on one line serialise at the memory side. A barrier area's
+// counters only grow and agree again whenever a call ends (grid_barrier.hpp), and tickets
+// are reset by their users, so only a new workspace needs clearing (oom_workspace_init).
 constexpr size_t WS_BAR = 0;                                      // barrier area of a kernel's first grid meeting
 constexpr size_t WS_BAR2 = WS_BAR + BAR_WORDS * 4;                // ... and of its second
 constexpr int TICKET_STRIDE = 64;
