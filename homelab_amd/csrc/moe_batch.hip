@@ -19,8 +19,9 @@
 //    wave's next K steps (B_DEPTH of them) are in flight meanwhile. At the item's end a
 //    lane swap meets gate and up: h = silu(g) * u, stored per token (16 bytes per lane).
 //  * A grid barrier (every block resident).
-//  * Phase 2: item = (expert, 16 output rows); block b takes a contiguous range of items,
-//    so it serves one or two experts: it stages that expert's h in LDS as h ~ hi + lo, two
+//  * Phase 2: item = (expert, 16 output rows); with at least 4 blocks an expert, each
+//    expert has a contiguous group of blocks that split its row tiles, otherwise block b
+//    takes a contiguous share of all items (one or two experts): a block stages its expert's h in LDS as h ~ hi + lo, two
 //    bf16 terms (lo = bf16(h - hi): 16 significant bits, relative error <= 2^-16), and its
 //    waves take the expert's row tiles. A K step is 8 MFMAs (hi and lo). y rows go out per
 //    assignment with no wait; the first K steps of the block's first tiles load before the
@@ -470,10 +471,27 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         }
     }
     // ---- phase 2: this block's items (slot, 16-row tile) first .. last, slot-major, in
-    // runs of one slot; the first run's first K steps load before the barrier ----
+    // runs of one slot; the first run's first K steps load before the barrier. With at
+    // least 4 blocks a slot, slot i has blocks i G / n_e .. (i + 1) G / n_e - 1 to itself
+    // and they split its tiles evenly, so every block stages one slot's h once: an even
+    // split of all items puts most blocks across two slots, and a second h staging on
+    // their path (measured at batch 16, ~32 slots: 141.6 -> 137.4 us a step). With fewer
+    // blocks a slot, each block takes an even share of all items: whole-slot groups then
+    // leave most blocks a few tiles above the average, which cost more than the second
+    // staging (the decode layer at batch 16, ~84 slots: 312.1 us that way, 316.1 us
+    // grouped) ----
     const int ntile = (H + B_TILE - 1) / B_TILE, ND = n_e * ntile;
-    const int per = (ND + gridDim.x - 1) / gridDim.x;
-    const int first = min(ND, (int)blockIdx.x * per), last = min(ND, first + per);
+    int first, last;
+    if ((int)gridDim.x >= 4 * n_e) {
+        const int G = (int)gridDim.x, b = (int)blockIdx.x;
+        const int si = ((b + 1) * n_e - 1) / G, b0 = si * G / n_e, nb = (si + 1) * G / n_e - b0, j = b - b0;
+        first = si * ntile + j * ntile / nb;
+        last = si * ntile + (j + 1) * ntile / nb;
+    } else {
+        const int per = (ND + gridDim.x - 1) / gridDim.x;
+        first = min(ND, (int)blockIdx.x * per);
+        last = min(ND, first + per);
+    }
     int r0 = first, i = 0, t0 = 0, t1 = 0, mt = 0, nq = 0;
     // the run at r0: slot i, tiles t0 .. t1; this wave's tiles t0 + wave + B_W m (m < mt),
     // K steps in order, issued B_DEPTH ahead of their use
