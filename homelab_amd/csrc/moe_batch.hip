@@ -330,18 +330,14 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     }
     L.mask[tid] = 0u;
     // activations: thread tid takes columns 8 (tid + NT c) .. + 8 of every token row (zeros
-    // past T and H), 16 loads in flight per pass
+    // past T and H); the loads stay in flight through the routing below and reach LDS after it
+    static_assert(B_HMAX / 8 / NT == 1, "one pass of activation loads");
+    const int xcol = tid * 8;
+    uint4 xv[B_T];
 #pragma unroll
-    for (int c = 0; c < B_HMAX / 8 / NT; c++) {
-        const int col = (tid + NT * c) * 8;
-        uint4 v[B_T];
-#pragma unroll
-        for (int u = 0; u < B_T; u++)
-            v[u] = u < T && col < H ? *reinterpret_cast<const uint4*>(a.x + (size_t)u * H + col) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int u = 0; u < B_T; u++) *reinterpret_cast<uint4*>(&L.u.x[u * B_XS + col]) = v[u];
-    }
-    __syncthreads();  // masks are zero
+    for (int u = 0; u < B_T; u++)
+        xv[u] = u < T && xcol < H ? *reinterpret_cast<const uint4*>(a.x + (size_t)u * H + xcol) : make_uint4(0, 0, 0, 0);
+    lds_barrier();  // masks are zero (the activation loads stay in flight)
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
         const int t = wave + B_W * j;
@@ -352,6 +348,8 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
             batch_picks<EQ>(key, kth, k, lane, L.keys[wave], L.p[wave], &L.ids[t * k], &L.w[t * k], L.mask, t);
         }
     }
+#pragma unroll
+    for (int u = 0; u < B_T; u++) *reinterpret_cast<uint4*>(&L.u.x[u * B_XS + xcol]) = xv[u];
     __syncthreads();
     // plan: assignments sorted by (expert, slot); expert e's run starts at the count of
     // assignments to lower ids, and the token order within it is the mask's bit order
