@@ -610,10 +610,18 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
         OOM_STAMP_WHERE(a.stamps, WB);
     }
     const int T = a.T, E = a.E, k = a.k, A = T * k;
-    // the record table and (one token) the activations load while the router runs
-    if (tid < E) pl.recs[tid] = a.all_recs[tid];
+    // one token: the routing wave's logits go out first, so its wait for them is one round
+    // trip behind nothing else; the record table (copied by the other waves: its LDS
+    // stores wait for their loads) and the activations load while the router runs
+    float lv0[EQ];
+    if constexpr (TG == 1) {
+        if (T == 1 && wave == 0) route_logits<EQ>(a.logits, E, lane, lv0);
+    }
+    constexpr int RT0 = TG == 1 ? 64 : 0;  // first thread of the record-table copy
+    static_assert(TG != 1 || 64 * FW1 >= 64 + F_EMAX + 1, "the other waves hold the record table");
+    if (tid >= RT0 && tid - RT0 < E) pl.recs[tid - RT0] = a.all_recs[tid - RT0];
     if constexpr (SH) {
-        if (tid == E) pl.recs[E] = a.shared_rec[0];
+        if (tid == RT0 + E) pl.recs[E] = a.shared_rec[0];
     }
     XRow<XDT> xr;
     if constexpr (TG == 1) xrow_load<XDT>(a.x, (int)a.H, lane, xr);
@@ -623,7 +631,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
         if (wave == 0) {
             // picks and plan in one pass (ballot radix selection); with one token the
             // plan's assignment i is expert slot i
-            route_select<EQ>(a.logits, E, k, lane, pl.keys, pl.p, pl.experts, pl.ids, pl.w, pl.slot_assign);
+            route_select<EQ>(lv0, E, k, lane, pl.keys, pl.p, pl.experts, pl.ids, pl.w, pl.slot_assign);
             if (lane < k) {
                 pl.off[lane] = lane;
                 pl.assign_tok[lane] = 0;

@@ -294,12 +294,17 @@ __device__ __forceinline__ uint64_t radix_kth(const uint64_t (&key)[EQ], int k) 
     return kth;
 }
 
+// The token's logits as route_select reads them: lane l holds expert l + 64 q in lv[q]
+// (-inf past E). Issued apart from route_select so a caller can put them in flight first.
 template <int EQ>
-__device__ __forceinline__ void route_select(const float* __restrict__ l, int E, int k, int lane, uint64_t* keys,
-                                             float* p, int* experts, int* ids, float* w, int* slot_assign) {
-    float lv[EQ];
+__device__ __forceinline__ void route_logits(const float* __restrict__ l, int E, int lane, float (&lv)[EQ]) {
 #pragma unroll
     for (int q = 0; q < EQ; q++) lv[q] = lane + 64 * q < E ? l[lane + 64 * q] : -INFINITY;
+}
+
+template <int EQ>
+__device__ __forceinline__ void route_select(const float (&lv)[EQ], int E, int k, int lane, uint64_t* keys,
+                                             float* p, int* experts, int* ids, float* w, int* slot_assign) {
     uint64_t key[EQ];
     route_keys<EQ>(lv, E, lane, key);
     const uint64_t kth = radix_kth<EQ>(key, k);
