@@ -77,6 +77,9 @@ struct BArgs {
     uint32_t* hdr;
     uint32_t* status;  // the device's status word: 1 if a wait gave up (results invalid)
     uint32_t spin;     // polls before a wait gives up
+#ifdef OOM_STAMPS
+    uint64_t* stamps;  // phase timestamps (profiling build)
+#endif
 };
 
 // The activation / h rows come first: their 16-byte LDS reads and writes need 16-byte
@@ -315,6 +318,8 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int T = a.T, E = a.E, k = a.k, A = T * k, H = a.H, I = a.I;
+    OOM_STAMP(a.stamps, B_W, 0);
+    OOM_STAMP_WHERE(a.stamps, B_W);
     // ---- set-up: this wave's tokens' logits (t = wave + B_W j) in flight first ----
     float lv[TPW][EQ];
 #pragma unroll
@@ -416,6 +421,7 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
             a.weights[s] = L.w[s];
         }
     const int n_e = L.n_e;
+    OOM_STAMP(a.stamps, B_W, 1);  // routed and planned
     const int NW = gridDim.x * B_W, gw = blockIdx.x * B_W + wave;
     const int nksH = (H + 127) >> 7, nksI = (I + 127) >> 7;
     const int AS = A + (SH ? T : 0);  // rows of h and y
@@ -520,8 +526,11 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         for (int d = 0; d < B_DEPTH; d++) issue(ring[d], bf32x4{0.0f, 0.0f, 0.0f, 0.0f});
     };
     start_run();
+    OOM_STAMP(a.stamps, B_W, 2);  // gate/up items done (the first run's down loads in flight)
     wait_mem();  // this wave's h stores are complete before its block arrives
     grid_barrier_words(a.hdr + WS_BAR / 4, bbase1, a.status, a.spin);
+    OOM_STAMP(a.stamps, B_W, 3);  // the first grid barrier released
+    bool staged_once = false;
     while (r0 < last) {
         // stage the slot's h: thread tid takes columns 4 (tid + NT c) .. + 4 of every
         // assignment (zeros past nb and I), 16 loads in flight per pass
@@ -552,6 +561,8 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
             }
         }
         __syncthreads();
+        if (!staged_once) OOM_STAMP(a.stamps, B_W, 4);  // the first run's h staged
+        staged_once = true;
         const int a0 = L.off[i], nb = L.off[i + 1] - a0, ho = m16 * B_HS + 32 * kq;
         int mc = 0, ksc = 0;
         bf32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -577,6 +588,7 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     }
     // ---- combine: out[t][r .. r + 4] = sum over the token's slots, in slot order, of w y;
     // one lane per 4 rows of a token, the slots' y loads all in flight ----
+    OOM_STAMP(a.stamps, B_W, 5);  // down tiles done
     wait_mem();
     grid_barrier_words(a.hdr + WS_BAR2 / 4, bbase2, a.status, a.spin);  // the second meeting's own area
     const int nq4 = H >> 2;
@@ -602,6 +614,7 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) store_out<ODT>(a.out, (size_t)t * H + r + e, acc[e]);
     }
+    OOM_STAMP(a.stamps, B_W, 6);  // combined and stored
     grid_barrier_exit(a.hdr + WS_BAR / 4);
     grid_barrier_exit(a.hdr + WS_BAR2 / 4);
 }
@@ -703,6 +716,9 @@ static BArgs batch_args(const float* logits, const void* x, const uint64_t* all_
     a.hdr = reinterpret_cast<uint32_t*>(base);
     a.status = status_word();
     a.spin = wait_limit();
+#ifdef OOM_STAMPS
+    a.stamps = stamps_buffer();
+#endif
     a.shared_rec = nullptr;
     a.gate_w = nullptr;
     return a;

@@ -3,6 +3,7 @@
     python stamps.py --build                 # here (CPU): homelab_amd/_build_stamps/liboom_hip_stamps.so
     python stamps.py decode1 [--calls 40]    # on the GPU: the FP8 decode step, batch 1
     python stamps.py nvfp4 [--calls 40]      # on the GPU: the NVFP4 decode step, batch 1
+    python stamps.py decode16 [--calls 40]   # on the GPU: the FP8 decode step, batch 16 (Zipf 1.1 routing)
 
 The profiling build compiles every kernel with -DOOM_STAMPS: the one-launch decode kernels
 then record the device's 100 MHz real-time clock per wave at their phase boundaries into a
@@ -29,11 +30,13 @@ NAMES = {
                 "tile rows done", "combined, stored"],
     "nvfp4": ["start", "routed (wave 0)", "x staged", "gate/up done", "barrier released", "h staged",
               "first tile combined", "end"],
+    "decode16": ["start", "routed and planned", "gate/up done", "barrier 1 released", "first run's h staged",
+                 "down tiles done", "combined, stored"],
 }
 
 
 # the point whose per-block distribution is broken down by XCD (hardware id in the last point)
-WHERE_POINT = {"decode1": 2}
+WHERE_POINT = {"decode1": 2, "decode16": 2}
 
 
 def build_stamps():
@@ -46,6 +49,27 @@ def workload(config, torch, hip, bench):
     """(step(i), waves per block of the config's kernel, the buffers to keep alive) of the
     config's bench workload."""
     g = torch.Generator(device="cuda")
+    if config == "decode16":
+        # the bench's batch-16 workload: Zipf(1.1)-biased logits, two expert sets alternating
+        E, k, H, I, T = 128, 8, 4096, 1536, 16
+        geo = hip.record_geometry(H, I)
+        stride = hip.record_stride(geo)
+        sets = [bench.make_expert_set(E, geo, stride, 1234 + s, torch) for s in range(2)]
+        g.manual_seed(99)
+        ws = torch.zeros(hip.moe_decode_fp8_workspace_size(T, E, k, geo), dtype=torch.uint8, device="cuda")
+        addrs = [torch.tensor([b.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
+                 for b in sets]
+        bias = torch.from_numpy(bench.zipf_bias(E, 1.1, 7)).cuda()
+        logits = (torch.randn((256, T, E), generator=g, device="cuda") + bias).contiguous()
+        x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+        out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+        w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+
+        def step16(i):
+            hip.moe_decode_fp8(logits[i % 256], x, addrs[i % 2], k, geo, ids, w, out, ws)
+
+        return step16, 8, (sets, addrs)
     if config == "decode1":
         E, k, H, I = 128, 8, 4096, 1536
         geo = hip.record_geometry(H, I)
@@ -80,7 +104,7 @@ def workload(config, torch, hip, bench):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("config", nargs="?", choices=["decode1", "nvfp4"])
+    ap.add_argument("config", nargs="?", choices=["decode1", "nvfp4", "decode16"])
     ap.add_argument("--build", action="store_true", help="build the profiling library (no GPU needed)")
     ap.add_argument("--calls", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=20)
@@ -90,7 +114,7 @@ def main():
         if not args.config:
             return 0
     if not args.config:
-        ap.error("name a config (decode1 or nvfp4) or --build")
+        ap.error("name a config (decode1, nvfp4 or decode16) or --build")
     if not os.path.exists(STAMPS_LIB):
         sys.exit(f"{STAMPS_LIB} is missing: run `python stamps.py --build` first")
     import numpy as np
