@@ -2,10 +2,11 @@
 // heads (G = H / Hkv query heads share a KV head), bf16 K/V in pages of page_size
 // tokens ([page_size, Hkv, D] each, token j in physical page page_table[j / page_size]).
 //
-//  * Block (b, g) takes keys [512 b, 512 b + 512) of KV head g; each of its 4 waves 128
+//  * Block (b, g) takes keys [256 b, 256 b + 256) of KV head g; each of its 4 waves 64
 //    keys, as pairs of 16-key tiles (a tile is one MFMA tile, inside one page). K and V
 //    of a tile stream once for all G query heads; the next pair's loads are in flight
-//    while the current one is reduced.
+//    while the current one is reduced. At 32 Ki keys the grid holds twice the blocks
+//    that are resident at once, so a CU whose blocks end early starts the next ones.
 //  * Scores S^T = K . Q^T on bf16 MFMA (v_mfma_f32_16x16x32_bf16; products exact, fp32
 //    accumulate): keys are the M side, so K loads need head_dim contiguous per lane
 //    (the layout in memory) and each lane ends with 4 keys of one head, which keeps the
@@ -29,10 +30,10 @@
 namespace oom {
 
 constexpr int AW = 4;           // waves per block
-constexpr int AKW = 128;        // keys per wave
+constexpr int AKW = 64;         // keys per wave
 constexpr int AKB = AW * AKW;   // keys per block
 constexpr int AG = 8;           // query heads per KV head (at most)
-constexpr int A_MAXB = 4096;    // blocks a KV head (2 Mi keys): the merge's weights sit in LDS
+constexpr int A_MAXB = 8192;    // blocks a KV head (2 Mi keys): the merge's weights sit in LDS
 constexpr int A_BUF_FLAGS = 0x00020000;
 constexpr int A_OOB = 0x7ffffff0;
 constexpr int A_BUF_SC1 = 16;
@@ -345,34 +346,54 @@ __global__ void __launch_bounds__(AW * 64) attn_decode_kernel(AttnArgs a) {
 // trips (stores acknowledged, a ticket, the partials' loads) on the last block's path,
 // which cost more than a kernel boundary.
 template <int D, int ODT>
-__global__ void __launch_bounds__(64) attn_merge_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(128) attn_merge_kernel(AttnArgs a) {
     static_assert(D == 128, "two columns a lane");
     constexpr int PSZ = 2 * AG + AG * D, CH = 64;  // partials a lane loads at once
     __shared__ float wts[A_MAXB];
-    const int lane = threadIdx.x, g = blockIdx.x, h = blockIdx.y, n = a.bph, c0 = 2 * lane;
+    __shared__ float part_m[2], part_l[2], part_a[2][D];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = blockIdx.x, h = blockIdx.y, n = a.bph;
+    const int c0 = 2 * lane;
     const float* hp = a.part + (size_t)g * n * PSZ;
     float M = -INFINITY, L = 0.0f, A0 = 0.0f, A1 = 0.0f;
-    if (n <= CH) {
-        // up to 64 partials (32 Ki keys): every load of the merge in flight at once
-        const bool ok = lane < n;
-        const float mq = ok ? hp[(size_t)lane * PSZ + h] : -INFINITY;
-        const float lq = ok ? hp[(size_t)lane * PSZ + AG + h] : 0.0f;
+    if (n <= 2 * CH) {
+        // up to 128 partials (32 Ki keys): wave w merges partials 64 w .. 64 w + 63 with
+        // every load in flight at once, then the two waves' (max, sum, acc) meet in LDS
+        const int q = CH * wave + lane;
+        const bool ok = q < n;
+        const float mq = ok ? hp[(size_t)q * PSZ + h] : -INFINITY;
+        const float lq = ok ? hp[(size_t)q * PSZ + AG + h] : 0.0f;
         float2 v[CH];
 #pragma unroll
         for (int j = 0; j < CH; j++)
-            v[j] = j < n ? *reinterpret_cast<const float2*>(hp + (size_t)j * PSZ + 2 * AG + h * D + c0)
-                         : make_float2(0.0f, 0.0f);
-        M = wave_max(mq);  // finite: every block holds a visible key
-        const float w = mq == -INFINITY ? 0.0f : expf(mq - M);
-        L = wave_sum(lq * w);
-        wts[lane] = w;
+            v[j] = CH * wave + j < n ? *reinterpret_cast<const float2*>(hp + (size_t)(CH * wave + j) * PSZ + 2 * AG +
+                                                                        h * D + c0)
+                                     : make_float2(0.0f, 0.0f);
+        float Mw = wave_max(mq);  // -inf only for a wave with no partial
+        const float w = mq == -INFINITY ? 0.0f : expf(mq - Mw);
+        const float Lw = wave_sum(lq * w);
+        wts[q] = w;
         wave_lds_order();
 #pragma unroll
         for (int j = 0; j < CH; j++) {  // past n: zero columns and weights
-            A0 = fmaf(v[j].x, wts[j], A0);
-            A1 = fmaf(v[j].y, wts[j], A1);
+            A0 = fmaf(v[j].x, wts[CH * wave + j], A0);
+            A1 = fmaf(v[j].y, wts[CH * wave + j], A1);
         }
+        if (lane == 0) {
+            part_m[wave] = Mw;
+            part_l[wave] = Lw;
+        }
+        part_a[wave][c0] = A0;
+        part_a[wave][c0 + 1] = A1;
+        __syncthreads();
+        if (wave == 1) return;
+        M = fmaxf(part_m[0], part_m[1]);  // finite: every block holds a visible key
+        const float f0 = part_m[0] == -INFINITY ? 0.0f : expf(part_m[0] - M);
+        const float f1 = part_m[1] == -INFINITY ? 0.0f : expf(part_m[1] - M);
+        L = fmaf(part_l[1], f1, part_l[0] * f0);
+        A0 = fmaf(part_a[1][c0], f1, part_a[0][c0] * f0);
+        A1 = fmaf(part_a[1][c0 + 1], f1, part_a[0][c0 + 1] * f0);
     } else {
+        if (wave == 1) return;
         for (int q = lane; q < n; q += 64) M = fmaxf(M, hp[(size_t)q * PSZ + h]);
         M = wave_max(M);
         for (int q0 = 0; q0 < n; q0 += 64) {
@@ -428,7 +449,7 @@ static int launch_attn_t(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_decode_kernel<D, QDT, ODT>), dim3(a.bph, a.Hkv), dim3(AW * 64), 0, st, a);
     if (a.bph > 1) {
         if (int rc = launched("oom_attn_decode_paged")) return rc;
-        hipLaunchKernelGGL((attn_merge_kernel<D, ODT>), dim3(a.Hkv, a.G), dim3(64), 0, st, a);
+        hipLaunchKernelGGL((attn_merge_kernel<D, ODT>), dim3(a.Hkv, a.G), dim3(128), 0, st, a);
     }
     return launched("oom_attn_decode_paged");
 }
