@@ -8,10 +8,12 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 (2 x 2.42 GB) alternate between steps so weights stream from HBM, not from the
 256 MB Infinity Cache.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--rounds R]
                     [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|turbo|prefill|nvfp4-prefill|gemv|copy]
 
-Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
+After W untimed warm-up steps, R rounds (default 5) of K back-to-back steps are timed with
+HIP events on the launch stream; `value` is the median round, and `timing` holds every
+round's figure and their spread. Prints one JSON line (rank 0): metric, value (us/token), roofline of the step's
 kernels against 8 TB/s HBM, and the reference CPU path (oracle restatement) timed on
 this host's cores over a bounded sample.
 """
@@ -33,6 +35,27 @@ METRIC = "MoE FP8 decode layer µs/token + achieved HBM GB/s (% of MI355X peak),
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def time_rounds(step, first, args, stream, torch, per_step=1):
+    """Median milliseconds per step over args.rounds rounds of args.steps back-to-back
+    calls step(first + r * args.steps + i): each round between two events on `stream` (the
+    launch stream), the device synchronised before and after. Returns (median, timing
+    record: rounds, per-round ms per step, spread = (max - min) / median). per_step divides
+    each round's figure further (calls a step makes)."""
+    per = []
+    for r in range(args.rounds):
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(args.steps):
+            step(first + r * args.steps + i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        per.append(a.elapsed_time(b) / (args.steps * per_step))
+    med = sorted(per)[len(per) // 2] if len(per) % 2 else sum(sorted(per)[len(per) // 2 - 1:len(per) // 2 + 1]) / 2
+    return med, {"rounds": len(per), "steps_per_round": args.steps, "round_ms": [round(v, 6) for v in per],
+                 "spread": (max(per) - min(per)) / med}
 
 
 def quantize_blocks_dev(w, torch):
@@ -172,7 +195,7 @@ def bench_decode(args, T, zipf, config):
     sets = [make_expert_set(E, geo, stride, 1234 + s, torch) for s in range(2)]
     addrs = [torch.tensor([b.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
              for b in sets]
-    n = args.warmup + args.steps
+    n = args.warmup + args.rounds * args.steps
     g = torch.Generator(device="cuda")
     g.manual_seed(99)
     logits = torch.randn((n, T, E), generator=g, device="cuda")
@@ -191,14 +214,7 @@ def bench_decode(args, T, zipf, config):
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(args.warmup, n):
-        step(i)
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms, timing = time_rounds(step, args.warmup, args, stream, torch)
     # algorithmic bytes: each distinct routed expert's weights and scales once, x and out
     idn = ids[args.warmup:].cpu().numpy()
     distinct = np.array([len(np.unique(s)) for s in idn])
@@ -213,6 +229,7 @@ def bench_decode(args, T, zipf, config):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "timing": timing,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -315,20 +332,14 @@ def bench_gemv(args):
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for i in range(args.steps):
-        step(i)
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / (args.steps * copies)  # per call
+    ms, timing = time_rounds(step, 0, args, stream, torch, per_step=copies)  # per call
     bytes_call = N * K + N * 4 + K * 2 + N * 2
     gbs = bytes_call / (ms * 1e-3) / 1e9
     res = {
         "metric": "FP8 weight-only GEMV us/call + achieved HBM GB/s (% of MI355X peak), 1 GPU",
         "value": ms * 1e3, "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms * copies, "calls_per_step": copies, "higher_is_better": False, "scaling": "weak",
+        "ms_per_step": ms * copies, "calls_per_step": copies, "timing": timing, "higher_is_better": False,
+        "scaling": "weak",
         "vs_baseline": None, "dtype": "fp8-e4m3 weights, bf16 x and y, fp32 accumulate", "data": "synthetic",
         "config": {"workload": "FP8 GEMV, batch 1: W 4096x4096 e4m3 from N(0,0.02) with per-row absmax fp32 scales, "
                                "x 1x4096 bf16 N(0,1), bf16 y; 48 weight copies rotate past the MALL",
@@ -410,20 +421,13 @@ def bench_attn(args):
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for i in range(args.steps):
-        step(i)
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / args.steps
+    ms, timing = time_rounds(step, 0, args, stream, torch)
     bytes_step = 2 * L * Hkv * D * 2 + L // P * 4 + 2 * H * D * 2
     gbs = bytes_step / (ms * 1e-3) / 1e9
     res = {
         "metric": "GQA paged decode attention us/step + achieved HBM GB/s (% of MI355X peak), 1 GPU",
         "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": ms, "timing": timing, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 K/V/q, fp32 softmax and accumulate, bf16 out", "data": "synthetic",
         "config": {"workload": "GQA decode attention, batch 1: 64 q heads, 8 KV heads, head_dim 128, 32768 keys, "
                                "bf16 KV in 16-token pages in random page order; 3 caches rotate past the MALL",
@@ -491,20 +495,13 @@ def bench_turbo(args):
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for i in range(args.steps):
-        step(i)
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / args.steps
+    ms, timing = time_rounds(step, 0, args, stream, torch)
     bytes_step = L * Hkv * (krb + vrb) + L + 2 * H * D * 4
     gbs = bytes_step / (ms * 1e-3) / 1e9
     res = {
         "metric": "Turbo k8v6 decode attention us/step + achieved HBM GB/s (% of MI355X peak), 1 GPU",
         "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": ms, "timing": timing, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "k8v6 Lloyd-Max codes with fp16 scales, f32 q/softmax/accumulate/out", "data": "synthetic",
         "config": {"workload": "decode attention, batch 1: 24 q heads over 2 KV heads, head_dim 256, 32768 keys, "
                                "Turbo k8v6 rows of N(0,1) vectors, all keys visible; 12 caches rotate past the MALL",
@@ -591,7 +588,7 @@ def bench_layer(args, T, config):
     g.manual_seed(98)
     rws = [(torch.randn((E, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16) for _ in range(2)]
     gws = [(torch.randn((1, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16) for _ in range(2)]
-    n = args.warmup + args.steps
+    n = args.warmup + args.rounds * args.steps
     xs = torch.randn((n, T, H), generator=g, device="cuda").to(torch.bfloat16)
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
     ids = torch.empty((n, T, k), dtype=torch.int32, device="cuda")
@@ -606,14 +603,7 @@ def bench_layer(args, T, config):
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(args.warmup, n):
-        step(i)
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms, timing = time_rounds(step, args.warmup, args, stream, torch)
     # algorithmic bytes: each distinct routed expert once, the shared expert, the router
     # and gate weights, x and out
     idn = ids[args.warmup:].cpu().numpy()
@@ -630,6 +620,7 @@ def bench_layer(args, T, config):
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "timing": timing,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -743,14 +734,7 @@ def bench_nvfp4_prefill(args):
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(args.steps):
-        step()
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / args.steps
+    ms, timing = time_rounds(lambda i: step(), 0, args, stream, torch)
     per_expert = 3 * H * I // 2 + 3 * H * I // 16 + 12
     bytes_step = n_e * per_expert + T * H * 4 + T * H * 2
     terms = 3 if exact else 1
@@ -760,7 +744,7 @@ def bench_nvfp4_prefill(args):
     res = {
         "metric": "MoE NVFP4 prefill (tiled, bf16 matrix cores) us/step + roofline fraction, 1 GPU",
         "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": ms, "timing": timing, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "nvfp4 weights decoded exactly to bf16, f32 activations as " +
                  ("three exact bf16 terms" if exact else "bf16") + ", fp32 accumulate",
         "data": "synthetic",
@@ -828,7 +812,7 @@ def bench_nvfp4(args):
     sets = [make_nvfp4_set(E, geo, stride, 2468 + s, torch) for s in range(2)]
     addrs = [torch.tensor([b.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
              for b in sets]
-    n = args.warmup + args.steps
+    n = args.warmup + args.rounds * args.steps
     g = torch.Generator(device="cuda")
     g.manual_seed(97)
     logits = torch.randn((n, T, E), generator=g, device="cuda").contiguous()
@@ -844,14 +828,7 @@ def bench_nvfp4(args):
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(args.warmup, n):
-        step(i)
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms, timing = time_rounds(step, args.warmup, args, stream, torch)
     idn = ids[args.warmup:].cpu().numpy()
     distinct = float(np.mean([len(np.unique(s_)) for s_ in idn]))
     per_expert = 3 * H * I // 2 + 3 * H * I // 16 + 12  # codes, scale bytes, the three scale_2 floats
@@ -860,7 +837,7 @@ def bench_nvfp4(args):
     res = {
         "metric": "MoE NVFP4 decode step us/token + achieved HBM GB/s (% of MI355X peak), 1 GPU",
         "value": ms * 1e3 / T, "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": ms, "timing": timing, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "nvfp4 (e2m1 + e4m3 group-16 scales) weights, bf16 activations, fp32 accumulate",
         "data": "synthetic",
         "config": {"workload": "MoE FFN decode step over nvfp4-modelopt-g16 records, batch 1: 512 experts top-10, "
@@ -920,7 +897,7 @@ def bench_prefill(args):
     addrs = torch.tensor([rec.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
     g = torch.Generator(device="cuda")
     g.manual_seed(17)
-    n = args.warmup + args.steps
+    n = args.warmup + args.rounds * args.steps
     bias = torch.from_numpy(zipf_bias(E, 1.1, 7)).cuda()
     logits = (torch.randn((n, T, E), generator=g, device="cuda") + bias).contiguous()
     x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
@@ -938,14 +915,7 @@ def bench_prefill(args):
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for i in range(args.warmup, n):
-        step(i)
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / args.steps
+    ms, timing = time_rounds(step, args.warmup, args, stream, torch)
     idn = ids[args.warmup:].cpu().numpy()
     distinct = float(np.mean([len(np.unique(s_)) for s_ in idn]))
     per_expert = 3 * H * I + 3 * (H // 128) * (I // 128) * 4
@@ -960,7 +930,7 @@ def bench_prefill(args):
     res = {
         "metric": "MoE FP8 prefill step us/step + achieved HBM GB/s and FP8 MFMA TFLOP/s (% of MI355X peak), 1 GPU",
         "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": ms, "timing": timing, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8-e4m3 weights; e4m3 activations (gate/up), h as " + ("two bf16 terms" if terms == 2 else "bf16")
                  + " (down); fp32 accumulate, bf16 out",
         "data": "synthetic",
@@ -1024,7 +994,7 @@ def bench_offload(args):
     stride = hip.record_stride(geo)
     steps = min(args.steps, 50)
     warmup = min(args.warmup, 5)
-    n = warmup + steps
+    n = warmup + args.rounds * steps
     log(f"bench: offload decode T={T} E={E} k={k} H={H} I={I}; {E * stride / 1e9:.2f} GB of records in pinned host memory")
     dev_set = make_expert_set(E, geo, stride, 1234, torch)
     host = hip.PinnedHost(E * stride)
@@ -1071,15 +1041,20 @@ def bench_offload(args):
             computed[i].record(stream)
 
     run(0, warmup)
-    torch.cuda.synchronize()
-    q.sync()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    run(warmup, n)
-    end.record(stream)
-    torch.cuda.synchronize()
-    q.sync()
-    ms = start.elapsed_time(end) / steps
+    per = []
+    for r in range(args.rounds):
+        torch.cuda.synchronize()
+        q.sync()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        run(warmup + r * steps, warmup + (r + 1) * steps)
+        end.record(stream)
+        torch.cuda.synchronize()
+        q.sync()
+        per.append(start.elapsed_time(end) / steps)
+    ms = sorted(per)[len(per) // 2]
+    timing = {"rounds": len(per), "steps_per_round": steps, "round_ms": [round(v, 6) for v in per],
+              "spread": (max(per) - min(per)) / ms}
     h2d = k * stride / (ms * 1e-3) / 1e9
     for ev in copied + computed:
         ev.close()
@@ -1088,7 +1063,7 @@ def bench_offload(args):
     return {
         "metric": "MoE FP8 decode step with host-tier experts: us/token + host-to-device GB/s, 1 GPU",
         "value": ms * 1e3 / T, "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": warmup,
-        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": ms, "timing": timing, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8-e4m3 weights, bf16 activations, fp32 accumulate", "data": "synthetic",
         "config": {"workload": "MoE FFN decode step, batch 1: 128 experts top-8, hidden 4096, inter 1536, all "
                                "records in pinned host memory; the 8 routed records copy to device slots each step "
@@ -1105,6 +1080,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--rounds", type=int, default=5,
+                    help="timed rounds of --steps launches each; the value is the median round")
     ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "offload", "attn",
                                                             "turbo", "prefill", "nvfp4-prefill", "gemv", "copy"])
     ap.add_argument("--prefill-precision", default="exact", choices=["exact", "bf16"],

@@ -29,14 +29,25 @@ __global__ void __launch_bounds__(256) fill_zero(uint4* p, size_t words, uint8_t
 }
 
 // The device's status word: a kernel whose bounded wait gives up stores 1 here (its
-// outputs are invalid); oom_status reads and clears it. One 256-byte line per device
+// outputs are invalid); oom_status exchanges it for 0 and reads the old value back through
+// the line's second word. One 256-byte line per device
 // (each device holds its own copy of a __device__ variable, at its own address).
 static __device__ __align__(256) uint32_t status_line[64];
+
+// Word 0 of the status line exchanged for 0 (one atomic step), the old value stored to
+// word 1 for the host to copy.
+__global__ void __launch_bounds__(64) status_take(uint32_t* line) {
+    if (threadIdx.x == 0) {
+        const uint32_t v = __hip_atomic_exchange(line, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(line + 1, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
 
 constexpr int MAX_DEVICES = 64;
 static std::mutex g_dev_mu;
 static uint32_t* g_status_ptr[MAX_DEVICES] = {};
 static std::atomic<uint32_t> g_wait_limit{DEFAULT_WAIT_LIMIT};
+static std::mutex g_status_mu;
 
 // The address of the current device's status word, looked up once per device with that
 // device current (nullptr if the runtime refuses).
@@ -71,15 +82,17 @@ extern "C" int oom_status(void* stream) {
     uint32_t* p = status_word();
     if (!p) return fail(OOM_ERR_LAUNCH, "oom_status: the device status word has no address");
     hipStream_t st = as_stream(stream);
+    std::lock_guard<std::mutex> lock(g_status_mu);  // one reader of word 1 at a time
+    // read and clear in one atomic exchange, so a give-up set by a kernel of another
+    // stream between a read and a separate clear cannot be lost; the value read goes to
+    // the line's second word, which the host then copies
+    hipLaunchKernelGGL(status_take, dim3(1), dim3(64), 0, st, p);
+    if (int rc = launched("oom_status")) return rc;
     uint32_t v = 0;
-    if (hipMemcpyAsync(&v, p, sizeof(v), hipMemcpyDeviceToHost, st) != hipSuccess ||
+    if (hipMemcpyAsync(&v, p + 1, sizeof(v), hipMemcpyDeviceToHost, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess)
         return fail(OOM_ERR_LAUNCH, std::string("oom_status: ") + hipGetErrorString(hipGetLastError()));
     if (v == 0) return OOM_OK;
-    // clear the word with the fill kernel (no memset node), ordered after the read
-    hipLaunchKernelGGL(fill_zero, dim3(1), dim3(256), 0, st, reinterpret_cast<uint4*>(p), (size_t)1,
-                       reinterpret_cast<uint8_t*>(p), 0);
-    if (int rc = launched("oom_status")) return rc;
     return fail(OOM_ERR_KERNEL,
                 "a bounded wait inside a kernel gave up (grid not resident at once, or a wait limit set by "
                 "oom_set_wait_limit): the outputs of that call are invalid");

@@ -1,6 +1,10 @@
-// The grid barrier's protocol, written once over an atomics policy so that the device
-// code (stream.hpp) and a CPU model of it (tests/barrier_model.cpp, std::thread per block)
-// run the same steps.
+// The grid barrier's protocol over an atomics policy, run by a CPU model of it
+// (tests/barrier_model.cpp, std::thread per block). The device form (grid_barrier_words
+// and grid_barrier_exit in stream.hpp) takes the same steps with the same group and target
+// helpers below, written lane-parallel: lane q < BAR_GROUPS of the block's first wave loads
+// group q's counter and the wave ballots the lanes' conditions (the model loops over the
+// groups in one thread), with a short sleep between polls, one meeting per area (use = 0)
+// and an exit add of 1 (meetings = 1).
 //
 // A barrier area holds BAR_GROUPS arrival counters and BAR_GROUPS exit counters, each on
 // a 256-byte line of its own, that only ever grow. Block b belongs to group b % G
@@ -46,6 +50,13 @@ OOM_BARRIER_FN uint32_t bar_group_size(uint32_t q, uint32_t nblocks) {
     return q < G ? (nblocks - q + G - 1) / G : 0u;
 }
 
+// The group of block `block` and what group q's arrival counter must reach for the
+// meeting `use` (0, 1, ...) of an area whose bases are `base`.
+OOM_BARRIER_FN uint32_t bar_group_of(uint32_t block, uint32_t nblocks) { return block % bar_groups(nblocks); }
+OOM_BARRIER_FN uint32_t bar_target(uint32_t base, uint32_t use, uint32_t q, uint32_t nblocks) {
+    return base + (use + 1) * bar_group_size(q, nblocks);
+}
+
 // Ops: static load (relaxed, device-coherent), add (relaxed, no value returned),
 // wait_mem (this agent's earlier memory operations complete) and pause (a short sleep
 // between polls). The CPU model runs these per block; the device runs the same steps
@@ -59,11 +70,11 @@ template <class Ops>
 OOM_BARRIER_FN bool barrier_arrive_wait(uint32_t* bar, const uint32_t (&base)[BAR_GROUPS], uint32_t use,
                                         uint32_t block, uint32_t nblocks, uint32_t spin_limit) {
     Ops::wait_mem();  // the bases (and this block's stores) are complete before the arrival
-    Ops::add(bar + (block % bar_groups(nblocks)) * BAR_STRIDE, 1u);
+    Ops::add(bar + bar_group_of(block, nblocks) * BAR_STRIDE, 1u);
     for (uint32_t spins = 0;;) {
         bool met = true;
         for (int q = 0; q < BAR_GROUPS; q++)
-            met &= (int32_t)(Ops::load(bar + q * BAR_STRIDE) - (base[q] + (use + 1) * bar_group_size(q, nblocks))) >= 0;
+            met &= (int32_t)(Ops::load(bar + q * BAR_STRIDE) - bar_target(base[q], use, (uint32_t)q, nblocks)) >= 0;
         if (met) return true;
         Ops::pause();
         if (++spins > spin_limit) return false;
@@ -72,7 +83,7 @@ OOM_BARRIER_FN bool barrier_arrive_wait(uint32_t* bar, const uint32_t (&base)[BA
 
 template <class Ops>
 OOM_BARRIER_FN void barrier_exit(uint32_t* bar, uint32_t block, uint32_t nblocks, uint32_t meetings) {
-    Ops::add(bar + BAR_EXIT + (block % bar_groups(nblocks)) * BAR_STRIDE, meetings);
+    Ops::add(bar + BAR_EXIT + bar_group_of(block, nblocks) * BAR_STRIDE, meetings);
 }
 
 }  // namespace oom

@@ -333,7 +333,7 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     if constexpr (SH) {
         if (tid == E) L.recs[E] = a.shared_rec[0];
     }
-    L.mask[tid] = 0u;
+    if (tid < 256) L.mask[tid] = 0u;  // (512 threads, 256 masks)
     // activations: thread tid takes columns 8 (tid + NT c) .. + 8 of every token row (zeros
     // past T and H); the loads stay in flight through the routing below and reach LDS after it
     static_assert(B_HMAX / 8 / NT == 1, "one pass of activation loads");

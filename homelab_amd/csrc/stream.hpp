@@ -29,8 +29,9 @@ constexpr size_t WS_TICKETS = WS_BAR2 + BAR_WORDS * 4;            // MAX_TILES l
 constexpr size_t WS_HEADER = (WS_TICKETS + (size_t)MAX_TILES * TICKET_STRIDE * 4 + 4095) & ~size_t(4095);
 
 // ---- phase timestamps (a profiling build only) -----------------------------------------
-// Built with -DOOM_STAMPS (stamps.py at the repository root builds that library apart from
-// liboom_hip.so), the one-launch decode kernels record the device's 100 MHz real-time clock
+// Built with -DOOM_STAMPS (a profiling library made apart from liboom_hip.so:
+// homelab_amd.build.build(build_dir=..., lib=..., defines=("OOM_STAMPS",))), the one-launch
+// decode kernels record the device's 100 MHz real-time clock
 // per wave at their phase boundaries: wave w of block b writes point p to
 // stamps[(b * waves + w) * STAMP_POINTS + p] (stamps: the buffer last handed to
 // oom_debug_set_stamps; none: nothing is written). The default build compiles none of it.
@@ -182,7 +183,7 @@ __device__ __forceinline__ uint32_t grid_barrier_base(uint32_t* bar) {
 // (every block of the grid, exactly once per call, on every path).
 __device__ __forceinline__ void grid_barrier_exit(uint32_t* bar) {
     if (threadIdx.x == 0)
-        (void)__hip_atomic_fetch_add(bar + BAR_EXIT + (blockIdx.x % bar_groups(gridDim.x)) * BAR_STRIDE, 1u,
+        (void)__hip_atomic_fetch_add(bar + BAR_EXIT + bar_group_of(blockIdx.x, gridDim.x) * BAR_STRIDE, 1u,
                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -201,9 +202,9 @@ __device__ __forceinline__ void grid_barrier_words(uint32_t* bar, uint32_t base,
         const int lane = threadIdx.x;
         wait_mem();  // the bases have been read before this block arrives
         if (lane == 0)
-            (void)__hip_atomic_fetch_add(bar + (blockIdx.x % bar_groups(gridDim.x)) * BAR_STRIDE, 1u,
+            (void)__hip_atomic_fetch_add(bar + bar_group_of(blockIdx.x, gridDim.x) * BAR_STRIDE, 1u,
                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t need = lane < BAR_GROUPS ? base + bar_group_size((uint32_t)lane, gridDim.x) : 0u;
+        const uint32_t need = lane < BAR_GROUPS ? bar_target(base, 0u, (uint32_t)lane, gridDim.x) : 0u;
         uint32_t* mine = bar + (lane < BAR_GROUPS ? lane : 0) * BAR_STRIDE;
         for (uint32_t spins = 0;;) {
             const bool met = lane >= BAR_GROUPS ||

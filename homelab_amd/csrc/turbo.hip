@@ -8,10 +8,14 @@
 // level[idx] * scale with the Lloyd-Max levels of a unit Gaussian (the table of
 // oom_kv_codebooks, levels for b bits starting at 2^b - 4).
 //
-// The row codec (rotate, append, read) is one block of D threads per row, with the
-// butterfly order, the block RMS and the nearest-level search of
-// crates/oominf-cuda/kernels/attention.cu:9-131, so codes and scales are bit-exact against
-// the oracle. The decode attention (attention.cu:584-686, flash_decode in
+// The row codec (rotate, append, read) keeps a row in registers across D / 4 lanes of one
+// wave (four coordinates a lane, 256 / D rows a wave): the butterflies run in the lane and
+// across lanes by DPP and permlane moves, the block RMS by an 8-lane exchange, and the
+// codes are packed by OR-ing the lanes' nibbles. The arithmetic is the format's, fixed by
+// crates/oominf-cuda/kernels/attention.cu:9-131 (stage order, 1/sqrt(D) after the
+// butterflies, the 32-way xor pairing of the RMS sum, fp16 scales rounded to nearest even,
+// nearest level by bisection with ties to the lower level), so codes and scales are
+// bit-exact against the oracle. The decode attention (attention.cu:584-686, flash_decode in
 // crates/oominf-cuda/src/attention.rs:365-447) lists the visible keys (mask_compact,
 // attention.cu:363-374), splits the list evenly over P partials (each a 32-lane half of a
 // wave, lane l owning coordinates l, l + 32, ...: the reference's per-warp layout), keeps
@@ -28,7 +32,7 @@
 
 namespace oom {
 
-constexpr int TQ_MAXD = 256;          // coordinates a row (one block of D threads)
+constexpr int TQ_MAXD = 256;          // coordinates a row
 constexpr int TQ_LEVELS = 508;        // levels for 2..8 bits: 4 + 8 + ... + 256
 constexpr int TQ_MASK_THREADS = 1024; // mask_compact's block
 constexpr int TQ_G = 12;              // query heads a KV head (the decode kernel's instance)
@@ -40,118 +44,199 @@ __host__ __device__ inline int kv_row_bytes(int D, int bits) {
 }
 __host__ __device__ inline int codebook_offset(int bits) { return (1 << bits) - 4; }
 
-// The fixed random sign of coordinate i in the rotation (Knuth's multiplicative hash,
-// top bit).
+// The rotation's sign of coordinate i: the top bit of Knuth's multiplicative hash of i
+// (the cache format fixes it, so it is computed, not stored).
 __device__ __forceinline__ float kv_sign(int i) { return (((unsigned)i * 2654435761u) >> 31) ? -1.0f : 1.0f; }
 
-// Unnormalised Walsh-Hadamard transform of s[0 .. D) in LDS by the block's D threads:
-// stages h = 1, 2, 4, ..., thread i < D with (i & h) == 0 forming (s[i] + s[i + h],
-// s[i] - s[i + h]). Synchronises before each stage and after the last.
-__device__ void tq_wht(float* s, int D) {
-    for (int h = 1; h < D; h <<= 1) {
-        __syncthreads();
-        const int i = threadIdx.x;
-        if (i < D && (i & h) == 0) {
-            const float a = s[i], b = s[i + h];
-            s[i] = a + b;
-            s[i + h] = a - b;
+// ---- rows, one wave per 256 / D rows ------------------------------------------------
+// A row of D coordinates (D = 32, 64, 128 or 256) sits in D / 4 consecutive lanes of a
+// wave: lane l of the row (l = lane % (D / 4)) holds coordinates 4 l .. 4 l + 3 in
+// registers, one 16-byte load of an fp32 row, and a 32-coordinate block of the row is 8
+// neighbouring lanes. Every lane stays active through the cross-lane steps (DPP and
+// permlane read whole rows of lanes); only memory operations are predicated. No multiply
+// and add fuse here (fp contract off): the format's arithmetic rounds each product (a
+// decoded level times its scale, a square) before it enters a butterfly or a sum.
+constexpr int TR_WAVES = 4;  // waves a block of the row kernels
+
+// Walsh-Hadamard butterflies over the row in the format's stage order h = 1, 2, ..., D / 2,
+// each pair (i, i + h) becoming (s_i + s_{i+h}, s_i - s_{i+h}): stages 1 and 2 inside the
+// lane, stage 4 o with the lane l ^ o (the lane whose bit o is clear keeps the sum, the
+// other the lower coordinate's value minus its own).
+template <int D>
+__device__ __forceinline__ void row_wht(float (&x)[4], int lane) {
+#pragma clang fp contract(off)
+    const float a0 = x[0] + x[1], a1 = x[0] - x[1], a2 = x[2] + x[3], a3 = x[2] - x[3];
+    x[0] = a0 + a2;
+    x[2] = a0 - a2;
+    x[1] = a1 + a3;
+    x[3] = a1 - a3;
+#pragma unroll
+    for (int o = 1; 4 * o < D; o <<= 1) {
+        const bool upper = (lane & o) != 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float p = lane_xor_n(x[i], o, lane);
+            x[i] = upper ? p - x[i] : x[i] + p;
         }
     }
-    __syncthreads();
 }
 
-// Sum of v over the 32 lanes of this lane's half-wave by the xor butterfly 16, 8, 4, 2,
-// 1 (every lane ends with the same bits).
-__device__ __forceinline__ float half_xor_sum(float v) {
+// The sum of a 32-coordinate block's values v (this lane's four of them) with the pairing
+// of a 32-way xor butterfly over the coordinates, partner offsets 16, 8, 4, 2, 1 in that
+// order: offsets 16, 8 and 4 are the lanes l ^ 4, l ^ 2, l ^ 1 of the block's 8, offsets 2
+// and 1 the lane's own coordinates. Every lane of the block ends with the same bits.
+__device__ __forceinline__ float block_xor_sum(float (&v)[4], int lane) {
+#pragma clang fp contract(off)
 #pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 32);
+    for (int i = 0; i < 4; i++) v[i] = v[i] + lane_xor<4>(v[i], lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = v[i] + lane_xor<2>(v[i], lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = v[i] + lane_xor<1>(v[i], lane);
+    const float p0 = v[0] + v[2], p1 = v[1] + v[3];
+    return p0 + p1;
+}
+
+// OR of a 32-bit value over the 8 lanes of a block (every lane ends with it).
+__device__ __forceinline__ uint32_t block_or(uint32_t v, int lane) {
+    v |= __float_as_uint(lane_xor<1>(__uint_as_float(v), lane));
+    v |= __float_as_uint(lane_xor<2>(__uint_as_float(v), lane));
+    v |= __float_as_uint(lane_xor<4>(__uint_as_float(v), lane));
     return v;
 }
 
-// Coordinate d of a cache row (rotated space for Turbo rows); lv is the row's codebook.
-__device__ __forceinline__ float kv_value(const uint8_t* row, int d, int D, int bits, const float* lv) {
-    if (!bits) return reinterpret_cast<const float*>(row)[d];
-    const int b = d >> 5, lane = d & 31;
-    const float sc = __half2float(reinterpret_cast<const __half*>(row)[b]);
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(row + kv_scale_bytes(D)) + b * bits;
-    int idx = 0;
-    for (int j = 0; j < bits; j++) idx |= ((w[j] >> lane) & 1) << j;
-    return lv[idx] * sc;
+// The row this lane serves (rows past n: memory operations skipped) and its lane in the row.
+template <int D>
+__device__ __forceinline__ int64_t row_of(int lane, int& l) {
+    constexpr int LPR = D / 4;
+    l = lane % LPR;
+    return ((int64_t)blockIdx.x * TR_WAVES + (threadIdx.x >> 6)) * (64 / LPR) + lane / LPR;
 }
 
 // Rotates rows of D coordinates in place: forward y = H (s . x) / sqrt(D), inverse
-// x = s . (H y) / sqrt(D) (H symmetric, H H = D I). Grid: one block of D threads a row.
-__global__ void __launch_bounds__(TQ_MAXD) kv_rotate_kernel(float* __restrict__ x, int D, int inverse) {
-    __shared__ float s[TQ_MAXD];
-    float* r = x + (size_t)blockIdx.x * D;
-    const int i = threadIdx.x;
+// x = s . (H y) / sqrt(D) (H symmetric, H H = D I).
+template <int D>
+__global__ void __launch_bounds__(64 * TR_WAVES) kv_rotate_kernel(float* __restrict__ x, int64_t rows, int inverse) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    int l;
+    const int64_t r = row_of<D>(lane, l);
+    const bool ok = r < rows;
+    float* p = x + r * D + 4 * l;  // four fp32 accesses a lane: the ABI asks 4-byte alignment only
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = ok ? p[i] : 0.0f;
     const float norm = 1.0f / sqrtf((float)D);
-    s[i] = inverse ? r[i] : r[i] * kv_sign(i);
-    tq_wht(s, D);
-    r[i] = inverse ? s[i] * kv_sign(i) * norm : s[i] * norm;
+    if (!inverse) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] *= kv_sign(4 * l + i);
+    }
+    row_wht<D>(v, lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = inverse ? v[i] * kv_sign(4 * l + i) * norm : v[i] * norm;
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) p[i] = v[i];
+    }
 }
 
-// Appends rows (src [n, D]) at cache row row0, rotated and quantised for bits 2..8 (fp32
-// copies for bits 0). Grid: one block of D threads a row.
-__global__ void __launch_bounds__(TQ_MAXD) kv_append_kernel(const float* __restrict__ src, uint8_t* __restrict__ cache,
-                                                           int64_t row0, int D, int bits,
-                                                           const float* __restrict__ levels) {
-    __shared__ float s[TQ_MAXD];
+// Appends rows (src [n, D] fp32) as Turbo rows of `bits` at cache row row0: rotated
+// (y = H (s . x) / sqrt(D)), per block of 32 the fp16 RMS scale (round to nearest even),
+// each coordinate the nearest codebook level of y / scale (bisection of the ascending
+// levels, then the closer neighbour, ties to the lower level), and the codes as `bits`
+// bit-plane words per block. lv_all: the 508-level table of oom_kv_codebooks.
+template <int D>
+__global__ void __launch_bounds__(64 * TR_WAVES) kv_append_kernel(const float* __restrict__ src,
+                                                                 uint8_t* __restrict__ cache, int64_t row0,
+                                                                 int64_t rows, int bits,
+                                                                 const float* __restrict__ lv_all) {
+#pragma clang fp contract(off)
     __shared__ float lv[256];
-    const size_t r = blockIdx.x;
-    const int i = threadIdx.x;
-    const float* x = src + r * D;
-    uint8_t* row = cache + ((size_t)row0 + r) * kv_row_bytes(D, bits);
-    if (!bits) {
-        reinterpret_cast<float*>(row)[i] = x[i];
-        return;
+    const int lane = threadIdx.x & 63, n = 1 << bits;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) lv[t] = lv_all[codebook_offset(bits) + t];
+    int l;
+    const int64_t r = row_of<D>(lane, l);
+    const bool ok = r < rows;
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = ok ? src[r * D + 4 * l + i] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] *= kv_sign(4 * l + i);
+    row_wht<D>(y, lane);
+    float sq[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        y[i] = y[i] / sqrtf((float)D);
+        sq[i] = y[i] * y[i];
     }
-    for (int t = i; t < (1 << bits); t += blockDim.x) lv[t] = levels[codebook_offset(bits) + t];
-    s[i] = x[i] * kv_sign(i);
-    tq_wht(s, D);  // (its first synchronisation also publishes lv)
-    const float y = s[i] / sqrtf((float)D);
-    const float ss = half_xor_sum(y * y);
+    const float ss = block_xor_sum(sq, lane);
     const __half hs = __float2half(sqrtf(ss / 32.0f));  // round to nearest even
     const float sc = __half2float(hs);
-    const float u = sc > 0.0f ? y / sc : 0.0f;
-    // nearest level: bisection of the ascending codebook, then the closer neighbour
-    // (ties to the lower level)
-    int lo = 0, hi = (1 << bits) - 1;
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (lv[mid] <= u) lo = mid;
-        else hi = mid;
+    __syncthreads();  // the levels are in LDS
+    int idx[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float u = sc > 0.0f ? y[i] / sc : 0.0f;
+        int lo = 0, hi = n - 1;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (lv[mid] <= u) lo = mid;
+            else hi = mid;
+        }
+        idx[i] = fabsf(u - lv[lo]) <= fabsf(u - lv[hi]) ? lo : hi;
     }
-    const int idx = fabsf(u - lv[lo]) <= fabsf(u - lv[hi]) ? lo : hi;
-    const int lane = i & 31, b = i >> 5;
-    if (lane == 0) reinterpret_cast<__half*>(row)[b] = hs;
-    uint32_t* w = reinterpret_cast<uint32_t*>(row + kv_scale_bytes(D)) + b * bits;
-    const uint64_t sh = (threadIdx.x & 32) ? 32 : 0;  // this lane's half of the wave
+    // word j of the block: bit t = 4 (l % 8) + i is bit j of coordinate t's code; the 8
+    // lanes OR their nibbles together and lane l % 8 == j keeps word j
+    const int lb = l & 7, b = l >> 3;
+    uint32_t mine = 0;
     for (int j = 0; j < bits; j++) {
-        const uint32_t m = (uint32_t)(__ballot((idx >> j) & 1) >> sh);
-        if (lane == j) w[j] = m;
+        uint32_t nib = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) nib |= (uint32_t)((idx[i] >> j) & 1) << i;
+        const uint32_t w = block_or(nib << (4 * lb), lane);
+        mine = lb == j ? w : mine;
+    }
+    if (ok) {
+        uint8_t* row = cache + (row0 + r) * kv_row_bytes(D, bits);
+        if (lb == 0) reinterpret_cast<__half*>(row)[b] = hs;
+        if (lb < bits) reinterpret_cast<uint32_t*>(row + kv_scale_bytes(D))[b * bits + lb] = mine;
     }
 }
 
-// Reads rows back as fp32 [n, D], decoded and un-rotated for bits 2..8. Grid: one block
-// of D threads a row.
-__global__ void __launch_bounds__(TQ_MAXD) kv_read_kernel(const uint8_t* __restrict__ cache, float* __restrict__ dst,
-                                                         int D, int bits, const float* __restrict__ levels) {
-    __shared__ float s[TQ_MAXD];
+// Reads Turbo rows of `bits` back as fp32 [n, D]: each coordinate level[code] * scale of its
+// block, then un-rotated: x = s . (H y) / sqrt(D).
+template <int D>
+__global__ void __launch_bounds__(64 * TR_WAVES) kv_read_kernel(const uint8_t* __restrict__ cache,
+                                                               float* __restrict__ dst, int64_t rows, int bits,
+                                                               const float* __restrict__ lv_all) {
+#pragma clang fp contract(off)
     __shared__ float lv[256];
-    const size_t r = blockIdx.x;
-    const int i = threadIdx.x;
-    const uint8_t* row = cache + r * kv_row_bytes(D, bits);
-    float* out = dst + r * D;
-    if (!bits) {
-        out[i] = reinterpret_cast<const float*>(row)[i];
-        return;
+    const int lane = threadIdx.x & 63, n = 1 << bits;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) lv[t] = lv_all[codebook_offset(bits) + t];
+    int l;
+    const int64_t r = row_of<D>(lane, l);
+    const bool ok = r < rows;
+    const int lb = l & 7, b = l >> 3;
+    const uint8_t* row = cache + (ok ? r : 0) * kv_row_bytes(D, bits);
+    const float sc = ok ? __half2float(reinterpret_cast<const __half*>(row)[b]) : 0.0f;
+    const uint32_t* wd = reinterpret_cast<const uint32_t*>(row + kv_scale_bytes(D)) + b * bits;
+    int idx[4] = {0, 0, 0, 0};
+    for (int j = 0; j < bits; j++) {
+        const uint32_t w = ok ? wd[j] : 0u;
+#pragma unroll
+        for (int i = 0; i < 4; i++) idx[i] |= (int)((w >> (4 * lb + i)) & 1u) << j;
     }
-    for (int t = i; t < (1 << bits); t += blockDim.x) lv[t] = levels[codebook_offset(bits) + t];
-    __syncthreads();
-    s[i] = kv_value(row, i, D, bits, lv);
-    tq_wht(s, D);
-    out[i] = s[i] * kv_sign(i) / sqrtf((float)D);
+    __syncthreads();  // the levels are in LDS
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = lv[idx[i]] * sc;
+    row_wht<D>(v, lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = v[i] * kv_sign(4 * l + i) / sqrtf((float)D);
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[r * D + 4 * l + i] = v[i];
+    }
 }
 
 // Inclusive prefix sum of v over the block (blockDim a multiple of 64, at most 1024):
@@ -781,21 +866,22 @@ __global__ void __launch_bounds__(TC_THREADS) attn_turbo_combine_kernel(TurboArg
         for (int s = 0; s < SL; s++) y += acc[s][d];
         acc[0][d] = y / den;
     }
+    __syncthreads();
     if constexpr (ROT) {
-        // the block's first D threads run the butterflies (tq_wht synchronises the block)
-        float* s = acc[0];
-        for (int hs = 1; hs < D; hs <<= 1) {
-            __syncthreads();
-            if (tid < D && (tid & hs) == 0) {
-                const float x0 = s[tid], x1 = s[tid + hs];
-                s[tid] = x0 + x1;
-                s[tid + hs] = x0 - x1;
-            }
+        // rotated back by the first wave: lane l takes coordinates 4 l .. 4 l + 3 through the
+        // butterflies, then signs and the 1 / sqrt(D) = 1 / 16
+        static_assert(D == 256, "one wave holds the head's 256 coordinates");
+        if (wave == 0) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = acc[0][4 * lane + i];
+            row_wht<D>(v, lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = v[i] * kv_sign(4 * lane + i) * (1.0f / 16.0f);
+#pragma unroll
+            for (int i = 0; i < 4; i++) a.out[(size_t)h * D + 4 * lane + i] = v[i];
         }
-        __syncthreads();
-        if (tid < D) a.out[(size_t)h * D + tid] = s[tid] * kv_sign(tid) * (1.0f / 16.0f);
     } else {
-        __syncthreads();
         if (tid < D) a.out[(size_t)h * D + tid] = acc[0][tid];
     }
 }
@@ -860,8 +946,8 @@ static const std::vector<float>& codebooks() {
     return table;
 }
 
-// Rows of d coordinates stored at `bits` (0: fp32): one block of d threads a row, and a
-// power-of-two d for the rotation (kv_row_shape, crates/oominf-cuda/src/attention.rs:351-356).
+// Rows of d coordinates stored at `bits` (0: fp32): d a multiple of 32 up to 256, and a
+// power of two for the rotation (kv_row_shape, crates/oominf-cuda/src/attention.rs:351-356).
 static bool kv_row_shape(int d, int bits) {
     return d >= 32 && d % 32 == 0 && d <= TQ_MAXD && (bits == 0 || ((d & (d - 1)) == 0 && bits >= 2 && bits <= 8));
 }
@@ -909,12 +995,32 @@ extern "C" size_t oom_kv_row_bytes(int d, int bits) {
     return (size_t)oom::kv_row_bytes(d, bits);
 }
 
+namespace oom {
+
+// Blocks of the row kernels: TR_WAVES waves a block, 256 / d rows a wave.
+static unsigned row_blocks(int64_t rows, int d) {
+    const int64_t per = (int64_t)TR_WAVES * (256 / d);
+    return (unsigned)((rows + per - 1) / per);
+}
+
+#define OOM_ROW_LAUNCH(KERNEL, d, ...)                                                                     \
+    switch (d) {                                                                                           \
+        case 32: hipLaunchKernelGGL(KERNEL<32>, dim3(grid), dim3(64 * TR_WAVES), 0, st, __VA_ARGS__); break;   \
+        case 64: hipLaunchKernelGGL(KERNEL<64>, dim3(grid), dim3(64 * TR_WAVES), 0, st, __VA_ARGS__); break;   \
+        case 128: hipLaunchKernelGGL(KERNEL<128>, dim3(grid), dim3(64 * TR_WAVES), 0, st, __VA_ARGS__); break; \
+        default: hipLaunchKernelGGL(KERNEL<256>, dim3(grid), dim3(64 * TR_WAVES), 0, st, __VA_ARGS__); break;  \
+    }
+
+}  // namespace oom
+
 extern "C" int oom_kv_rotate(float* x, int rows, int d, int inverse, void* stream) {
     using namespace oom;
     OOM_REQUIRE(kv_row_shape(d, 4) && rows >= 0, "oom_kv_rotate: d must be a power of two, 32..256");
     if (rows == 0) return OOM_OK;
     OOM_REQUIRE(x, "oom_kv_rotate: null buffer");
-    hipLaunchKernelGGL(kv_rotate_kernel, dim3((unsigned)rows), dim3(d), 0, as_stream(stream), x, d, inverse ? 1 : 0);
+    const unsigned grid = row_blocks(rows, d);
+    hipStream_t st = as_stream(stream);
+    OOM_ROW_LAUNCH(kv_rotate_kernel, d, x, (int64_t)rows, inverse ? 1 : 0)
     return launched("oom_kv_rotate");
 }
 
@@ -927,8 +1033,16 @@ extern "C" int oom_kv_append(const float* src, uint8_t* cache, int64_t start, in
     if (rows == 0) return OOM_OK;
     OOM_REQUIRE(rows < (1ll << 31), "oom_kv_append: too many rows");
     OOM_REQUIRE(src && cache && (bits == 0 || levels), "oom_kv_append: null buffer");
-    hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)rows), dim3(d), 0, as_stream(stream), src, cache,
-                       start * kv_heads, d, bits, levels);
+    hipStream_t st = as_stream(stream);
+    if (!bits) {
+        // fp32 rows are the values as they are: one contiguous copy
+        if (hipMemcpyAsync(cache + start * kv_heads * (int64_t)d * 4, src, (size_t)rows * d * 4,
+                           hipMemcpyDeviceToDevice, st) != hipSuccess)
+            return launched("oom_kv_append");
+        return OOM_OK;
+    }
+    const unsigned grid = row_blocks(rows, d);
+    OOM_ROW_LAUNCH(kv_append_kernel, d, src, cache, start * kv_heads, rows, bits, levels)
     return launched("oom_kv_append");
 }
 
@@ -941,10 +1055,18 @@ extern "C" int oom_kv_read(const uint8_t* cache, float* dst, int len, int kv_hea
     if (rows == 0) return OOM_OK;
     OOM_REQUIRE(rows < (1ll << 31), "oom_kv_read: too many rows");
     OOM_REQUIRE(cache && dst && (bits == 0 || levels), "oom_kv_read: null buffer");
-    hipLaunchKernelGGL(kv_read_kernel, dim3((unsigned)rows), dim3(d), 0, as_stream(stream), cache, dst, d, bits,
-                       levels);
+    hipStream_t st = as_stream(stream);
+    if (!bits) {
+        if (hipMemcpyAsync(dst, cache, (size_t)rows * d * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
+            return launched("oom_kv_read");
+        return OOM_OK;
+    }
+    const unsigned grid = row_blocks(rows, d);
+    OOM_ROW_LAUNCH(kv_read_kernel, d, cache, dst, rows, bits, levels)
     return launched("oom_kv_read");
 }
+
+#undef OOM_ROW_LAUNCH
 
 extern "C" int oom_mask_compact(const uint8_t* mask, int32_t* sel, int n, void* stream) {
     using namespace oom;

@@ -117,14 +117,15 @@ def geometry(schema: dict):
 
 
 def e4m3_rne(x) -> np.ndarray:
-    """e4m3fn codes of f32 values: round to nearest even, saturating at +-448 (0x7e), sign
-    kept for zero (crates/oominf-core/src/fp8.rs:5-27). Normal codes are (e + 7) << 3 |
+    """e4m3fn codes of f32 values: round to nearest even, saturating at +-448 (0x7e), NaN to
+    sign | 0x7e, sign kept for zero (crates/oominf-core/src/fp8.rs:5-27). Normal codes are (e + 7) << 3 |
     (m - 8) for |x| = m 2^(e - 3), 8 <= m < 16; subnormals (|x| < 2^-6) are m for
     |x| = m 2^-9 -- both (e + 6) 8 + m with e = -6 below 2^-6, which also carries a
     mantissa that rounds up to 16 into the next exponent."""
     x = np.asarray(x, dtype=np.float32)
     sign = np.signbit(x).astype(np.uint8) << 7
-    a = np.minimum(np.abs(x).astype(np.float64), 448.0)
+    a = np.abs(x).astype(np.float64)
+    a = np.minimum(np.where(np.isnan(a), 448.0, a), 448.0)  # NaN saturates like +-inf: sign | 0x7e
     _, ex = np.frexp(a)
     e = np.where(a < 2.0 ** -6, -6, ex.astype(np.int64) - 1)
     m = np.rint(a / np.exp2((e - 3).astype(np.float64)))  # exact scaling; half to even
@@ -145,7 +146,8 @@ def quantize_blocks(w_bits) -> tuple[np.ndarray, np.ndarray]:
     nbr, nbc = (n + BLOCK - 1) // BLOCK, (k + BLOCK - 1) // BLOCK
     pad = np.zeros((nbr * BLOCK, nbc * BLOCK), dtype=np.float32)
     pad[:n, :k] = np.abs(w)
-    amax = pad.reshape(nbr, BLOCK, nbc, BLOCK).max(axis=(1, 3))
+    # NaN-ignoring maximum from 0, as f32::max folds (an all-NaN block gets scale 1)
+    amax = np.fmax.reduce(pad.reshape(nbr, BLOCK, nbc, BLOCK), axis=(1, 3), initial=np.float32(0.0))
     s = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
     full = np.repeat(np.repeat(s, BLOCK, axis=0), BLOCK, axis=1)[:n, :k]
     q = e4m3_rne(w / full)

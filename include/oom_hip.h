@@ -74,8 +74,12 @@ const char* oom_last_error(void);
  * errors, which surface at its next synchronising call as an Err (its error contract:
  * crates/oominf-cuda/src/lib.rs:157-160), that failure is reported at a sync point:
  * oom_status waits for `stream`, then returns OOM_ERR_KERNEL if any kernel of this
- * library on the current device gave up a wait since the last oom_status (and clears
- * the word), else OOM_OK. oom_stream_sync reports it the same way. */
+ * library on the current device gave up a wait since the last oom_status, else OOM_OK;
+ * it reads and clears the word in one atomic exchange. oom_stream_sync reports it the
+ * same way. The word is per device, not per stream: a give-up in a kernel on any stream
+ * of the device is reported by the next oom_status (or oom_stream_sync) on that device,
+ * whichever stream it names, and only once; a backend that drives several streams of one
+ * device checks it once per step. */
 int oom_status(void* stream);
 
 /* Polls of each bounded wait before it gives up, for later launches of this process

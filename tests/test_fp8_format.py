@@ -43,7 +43,7 @@ def test_e4m3_matches_oracle_on_ties_subnormals_and_saturation():
     pos = np.array([oracle.e4m3_to_f32(c) for c in range(0x7f)], dtype=np.float64)
     mids = (pos[:-1] + pos[1:]) / 2  # exact ties between neighbouring codes
     x = np.concatenate([mids, -mids, pos, [0.0, -0.0, 448.0, 449.0, 464.0, 500.0, 1e6, -1e6, 2.0 ** -10, 2.0 ** -11,
-                                          3 * 2.0 ** -11, -(2.0 ** -12)],
+                                          3 * 2.0 ** -11, -(2.0 ** -12), np.nan, -np.nan, np.inf, -np.inf],
                         rng.standard_normal(5000) * 40, rng.standard_normal(2000) * 0.01]).astype(np.float32)
     want = np.array([oracle.e4m3_from_f32(float(v)) for v in x], dtype=np.uint8)
     np.testing.assert_array_equal(ff.e4m3_rne(x), want)
@@ -60,6 +60,9 @@ def random_bf16(shape, seed, scale=0.02):
 def test_quantize_blocks_matches_oracle(n, k):
     w = random_bf16((n, k), n * 7 + k)
     w[: min(n, 128), : min(k, 128)] = 0  # an all-zero block takes scale 1
+    w[-1, -1] = 0x7fc0  # a NaN: ignored by the block maximum, coded as 0x7e
+    if n > 128 and k > 128:
+        w[128:, 128:256] = 0xffc0  # an all-NaN block: scale 1, every code sign | 0x7e
     q, s = ff.quantize_blocks(w)
     wq, ws = oracle.quantize(w, oracle.SCALE_128X128)
     np.testing.assert_array_equal(q, wq)

@@ -223,7 +223,8 @@ def test_experts_stage_by_stage(hip, H, I, E, T, k):
                                         (64, 512, 10, 1.1),   # the released model's E, ballot ranks, one round
                                         (128, 512, 10, 1.1),  # ... past 1024 slots: two rounds
                                         (3, 8192, 32, None),  # the largest E and k: the counting fallback
-                                        (40, 8192, 32, 1.1)])  # ... over two rounds of 1024 slots
+                                        (40, 8192, 32, 1.1),  # ... over two rounds of 1024 slots
+                                        (2048, 128, 8, 1.1)])  # the prefill's plan: 16,384 slots, 16 rounds
 def test_device_plan_matches_host_plan(hip, T, E, k, zipf):
     import torch
 

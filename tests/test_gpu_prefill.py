@@ -259,7 +259,9 @@ def test_prefill_small(hip, T, E, k, H, I, prec):
 def test_prefill_full_shape_sampled_tokens(hip, prec):
     """2048 tokens, 128 experts (all routed), top-8 with a Zipf(1.1) bias, hidden 4096,
     inter 1536. A token's output depends only on its own row, routing and the experts
-    it picks, so the oracle checks a sample of 12 tokens of the full step."""
+    it picks, so the oracle checks a sample of the full step: 12 fixed tokens, the last
+    two tokens of each of the two heaviest experts' runs (their last, partial 128-row
+    M-tiles) and the tokens of the lightest experts' runs (one or two assignments)."""
     import torch
 
     T, E, k, H, I = 2048, 128, 8, 4096, 1536
@@ -282,6 +284,18 @@ def test_prefill_full_shape_sampled_tokens(hip, prec):
     addrs = torch.tensor([buf.data_ptr() + e * stride for e in range(E)], dtype=torch.int64, device="cuda")
     logits = synth.decode_logits(31, T, E, 1.1)
     xb = synth.activations_bf16(31, T, H)
-    sample = np.array([0, 1, 2, 100, 511, 777, 1024, 1500, 1800, 2045, 2046, 2047])
+    fixed = [0, 1, 2, 100, 511, 777, 1024, 1500, 1800, 2045, 2046, 2047]
+    ids, _ = oracle.router_topk(logits, k)
+    experts, off, tok, _ = oracle.moe_plan(ids, E)
+    count = np.diff(off)
+    heavy = np.argsort(-count, kind="stable")[:2]
+    tail = [int(t) for i in heavy for t in tok[off[i + 1] - 2:off[i + 1]]]
+    assert all(count[i] % 128 for i in heavy), "the heaviest experts' last M-tiles are full: pick another seed"
+    light = np.nonzero(count <= 2)[0]
+    assert light.size, "no expert with one or two assignments: pick another seed"
+    singles = [int(t) for i in light[:6] for t in tok[off[i]:off[i + 1]]]
+    sample = np.array(sorted(set(fixed + tail + singles)))
+    print(f"sample: {sample.size} tokens (heaviest experts {count[heavy].tolist()} assignments, "
+          f"{light.size} experts with <= 2)", flush=True)
     prefill_check(hip, geo, (buf, addrs), logits, xb, k, sample,
                   precision=hip.EXPERT_EXACT if prec == "exact" else hip.EXPERT_BF16)

@@ -56,7 +56,7 @@ def test_rotate_bit_exact(hip, d):
 
 
 @pytest.mark.parametrize("bits", [0, 2, 3, 4, 5, 6, 7, 8])
-@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 def test_append_and_read_bit_exact(hip, levels, bits, d):
     import torch
 
@@ -113,6 +113,7 @@ CASES = [
     (24, 2, 32768, 8, 6, "qsa"),    # a long context, about 4k keys selected
     (24, 2, 1, 8, 6, "all"),
     (12, 1, 333, 4, 3, "qsa"),
+    (12, 1, 65536, 4, 4, "qsa"),    # one KV head over 64k keys: 256 partials, the combine's second load batch
     (24, 2, 777, 0, 0, "all"),      # an fp32 cache
 ]
 
