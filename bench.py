@@ -369,8 +369,8 @@ def cpu_baseline_attn(q, k, v, table, kv_len, H, Hkv, D, scale, budget_s):
     import oracle
 
     G = H // Hkv
-    heads = [(np.ascontiguousarray(q[g * G:(g + 1) * G]), np.ascontiguousarray(k[:, :, g:g + 1]),
-              np.ascontiguousarray(v[:, :, g:g + 1])) for g in range(Hkv)]
+    heads = [(np.ascontiguousarray(q[g * G:(g + 1) * G]), np.ascontiguousarray(k[:, g:g + 1]),
+              np.ascontiguousarray(v[:, g:g + 1])) for g in range(Hkv)]
     threads = max(1, min(Hkv, usable_cores()))
 
     def one(g):
@@ -405,8 +405,8 @@ def bench_attn(args):
     # three caches rotate between steps so K/V stream from HBM, not from the MALL
     caches = []
     for _ in range(3):
-        k = torch.randn((n_pages, P, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
-        v = torch.randn((n_pages, P, Hkv, D), generator=g, device="cuda").to(torch.bfloat16)
+        k = torch.randn((n_pages, Hkv, P, D), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((n_pages, Hkv, P, D), generator=g, device="cuda").to(torch.bfloat16)
         table = torch.randperm(n_pages, generator=g, device="cuda").to(torch.int32)
         caches.append((k, v, table))
     q = torch.randn((H, D), generator=g, device="cuda").to(torch.bfloat16)

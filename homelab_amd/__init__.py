@@ -330,9 +330,9 @@ def attn_decode_workspace_size(kv_len: int, heads: int, kv_heads: int, d: int) -
 
 
 def attn_decode_paged(q, k_pages, v_pages, page_table, kv_len: int, scale: float, out, ws, stream=None) -> None:
-    """q [heads, d]; k_pages / v_pages bf16 [n_pages, page_size, kv_heads, d]; page_table i32."""
+    """q [heads, d]; k_pages / v_pages bf16 [n_pages, kv_heads, page_size, d]; page_table i32."""
     heads, d = q.shape
-    n_pages, page_size, kv_heads, _ = k_pages.shape
+    n_pages, kv_heads, page_size, _ = k_pages.shape
     check(lib().oom_attn_decode_paged(_ptr(q), _dtype_code(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table),
                                       n_pages, page_size, kv_len, heads, kv_heads, d, scale, _ptr(out),
                                       _dtype_code(out), _ptr(ws), ws.numel() * ws.element_size(), _stream(stream)))

@@ -1,10 +1,13 @@
 // Paged GQA decode attention on gfx950: one query token, H query heads over Hkv KV
 // heads (G = H / Hkv query heads share a KV head), bf16 K/V in pages of page_size
-// tokens ([page_size, Hkv, D] each, token j in physical page page_table[j / page_size]).
+// tokens ([Hkv, page_size, D] each: one KV head's keys of a page are page_size x D
+// contiguous, 4 KiB at 16 keys of 128 dims), token j in physical page
+// page_table[j / page_size] at slot j % page_size.
 //
 //  * Block (b, g) takes keys [256 b, 256 b + 256) of KV head g; each of its 4 waves 64
-//    keys, as pairs of 16-key tiles (a tile is one MFMA tile, inside one page). K and V
-//    of a tile stream once for all G query heads; the next pair's loads are in flight
+//    keys, as pairs of 16-key tiles (a tile is one MFMA tile, inside one page: one
+//    contiguous 4 KiB run of K and one of V). K and V of a tile stream once for all G
+//    query heads; the next pair's loads are in flight
 //    while the current one is reduced. At 32 Ki keys the grid holds twice the blocks
 //    that are resident at once, so a CU whose blocks end early starts the next ones.
 //  * Scores S^T = K . Q^T on bf16 MFMA (v_mfma_f32_16x16x32_bf16; products exact, fp32
@@ -57,7 +60,7 @@ __device__ __forceinline__ uint4 a_ld16(__amdgpu_buffer_rsrc_t r, int off) {
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// Buffer resource over the KV-head slice of one page (empty if the page index is bad).
+// Buffer resource over one page, all its KV heads (empty if the page index is bad).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint16_t* base, int page, int n_pages,
                                                            int page_bytes) {
     const bool ok = page >= 0 && page < n_pages;
@@ -66,17 +69,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint16_t* base
 }
 
 // Loads of one 16-key tile (inside one page), keys past kv_len and tiles whose page
-// index is out of range reading zeros. K in the MFMA A layout of the scores: lane l holds
-// key l % 16, head_dim 32 s + 8 (l / 16) .. + 8. V: lane l holds head_dim 8 (l % 16) .. + 8
-// of key 4 q + l / 16 (q < 4).
+// index is out of range reading zeros. Key slot s of KV head g sits at row g * page_size
+// + s of the page (D * 2 bytes a row). K in the MFMA A layout of the scores: lane l holds
+// key l % 16, head_dim 32 s + 8 (l / 16) .. + 8 (the four instructions of a tile cover its
+// 4 KiB run). V: lane l holds head_dim 8 (l % 16) .. + 8 of key 4 q + l / 16 (q < 4): an
+// instruction reads 1 KiB contiguous.
 template <int D>
 __device__ __forceinline__ void k_load(const AttnArgs& a, int g, int key0, int page, int lane, uint4 (&k)[D / 32]) {
-    const int ps = a.page_size, page_bytes = ps * a.Hkv * D * 2, row_bytes = a.Hkv * D * 2;
+    const int ps = a.page_size, page_bytes = ps * a.Hkv * D * 2, row_bytes = D * 2;
     if (key0 >= a.kv_len) page = -1;
     const __amdgpu_buffer_rsrc_t kr = page_rsrc(a.kp, page, a.n_pages, page_bytes);
-    const int slot0 = key0 % ps;
-    const int kbase = key0 + (lane & 15) < a.kv_len ? (slot0 + (lane & 15)) * row_bytes + g * D * 2 + 16 * (lane >> 4)
-                                                    : A_OOB;
+    const int row0 = g * ps + key0 % ps;
+    const int kbase = key0 + (lane & 15) < a.kv_len ? (row0 + (lane & 15)) * row_bytes + 16 * (lane >> 4) : A_OOB;
 #pragma unroll
     for (int s = 0; s < D / 32; s++) k[s] = a_ld16(kr, kbase == A_OOB ? A_OOB : kbase + 64 * s);
 }
@@ -84,14 +88,14 @@ __device__ __forceinline__ void k_load(const AttnArgs& a, int g, int key0, int p
 template <int D>
 __device__ __forceinline__ void v_load(const AttnArgs& a, int g, int key0, int page, int lane, uint4 (&v)[4]) {
     static_assert(D == 128, "V loads: 16 lanes of 8 head_dim columns a key");
-    const int ps = a.page_size, page_bytes = ps * a.Hkv * D * 2, row_bytes = a.Hkv * D * 2;
+    const int ps = a.page_size, page_bytes = ps * a.Hkv * D * 2, row_bytes = D * 2;
     if (key0 >= a.kv_len) page = -1;
     const __amdgpu_buffer_rsrc_t vr = page_rsrc(a.vp, page, a.n_pages, page_bytes);
-    const int slot0 = key0 % ps;
+    const int row0 = g * ps + key0 % ps;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int kk = 4 * q + (lane >> 4);
-        v[q] = a_ld16(vr, key0 + kk < a.kv_len ? (slot0 + kk) * row_bytes + g * D * 2 + (lane & 15) * 16 : A_OOB);
+        v[q] = a_ld16(vr, key0 + kk < a.kv_len ? (row0 + kk) * row_bytes + (lane & 15) * 16 : A_OOB);
     }
 }
 

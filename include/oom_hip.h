@@ -308,7 +308,7 @@ int oom_moe_swiglu_range(const float* g, const float* u, float* h, int64_t start
 
 /* Paged GQA decode attention for one query token: out[h, :] = sum_j softmax_j(q_h . k_j
  * * scale) v_j over the kv_len keys, query head h reading KV head h / (heads / kv_heads).
- * q [heads, d] in q_dtype; k_pages and v_pages bf16 [n_pages, page_size, kv_heads, d]
+ * q [heads, d] in q_dtype; k_pages and v_pages bf16 [n_pages, kv_heads, page_size, d]
  * (16-byte aligned); key j lives in physical page page_table[j / page_size] (i32, one
  * entry per page of the sequence; an entry outside [0, n_pages) reads zeros) at slot
  * j % page_size. d = 128, heads / kv_heads <= 8, page_size a multiple of 16. fp32 dot

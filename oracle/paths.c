@@ -480,7 +480,8 @@ void oracle_attn_decode_paged(const uint16_t* q, const uint16_t* k_pages, const 
                     s[jj] = -INFINITY;
                     continue;
                 }
-                size_t row = ((size_t)page_table[j / page_size] * page_size + (size_t)(j % page_size)) * Hkv + kvh;
+                /* pages [n_pages, Hkv, page_size, D]: KV head kvh's slot j % page_size */
+                size_t row = ((size_t)page_table[j / page_size] * Hkv + kvh) * page_size + (size_t)(j % page_size);
                 const uint16_t* kr = k_pages + row * D;
                 const uint16_t* vr = v_pages + row * D;
                 float dot = 0.0f;

@@ -171,14 +171,14 @@ def f64_moe_nvfp4(ids_w, x: np.ndarray, recs, geo: oracle.Nvfp4Record) -> np.nda
 
 
 def paged_attention_case(seed, H, Hkv, D, kv_len, page=16, spare_pages=3):
-    """q bf16 [H, D]; K and V bf16 [n_pages, page, Hkv, D] with a few pages more than the
+    """q bf16 [H, D]; K and V bf16 [n_pages, Hkv, page, D] with a few pages more than the
     sequence uses; the page table maps logical page i to a seeded random physical page."""
     n_used = (kv_len + page - 1) // page
     n_pages = n_used + spare_pages
     table = oracle.permutation(n_pages, seed)[:n_used].astype(np.int32)
     q = oracle.gaussian_bf16((H, D), oracle.seed(seed, 1))
-    k = oracle.gaussian_bf16((n_pages, page, Hkv, D), oracle.seed(seed, 2))
-    v = oracle.gaussian_bf16((n_pages, page, Hkv, D), oracle.seed(seed, 3))
+    k = oracle.gaussian_bf16((n_pages, Hkv, page, D), oracle.seed(seed, 2))
+    v = oracle.gaussian_bf16((n_pages, Hkv, page, D), oracle.seed(seed, 3))
     return q, k, v, table
 
 
@@ -191,8 +191,8 @@ def f64_attention(qf, k, v, table, page, kv_len, H, Hkv, D, scale):
     phys = table[j // page]
     out = np.zeros((H, D))
     for h in range(H):
-        K = kf[phys, j % page, h // G]
-        V = vf[phys, j % page, h // G]
+        K = kf[phys, h // G, j % page]
+        V = vf[phys, h // G, j % page]
         s = K @ np.asarray(qf[h], dtype=np.float64) * scale
         p = np.exp(s - s.max())
         out[h] = p @ V / p.sum()

@@ -57,8 +57,8 @@ CASES = [
     (4, 4, 128, 300, 16, "f32"),      # one query head per KV head
     (24, 4, 128, 2100, 16, "bf16"),   # six query heads per KV head
     (8, 2, 128, 4097, 64, "f32"),
-    (8, 1, 128, 32769, 16, "f32"),    # 33 blocks: merge groups of 32 and 1, then a second level
-    (16, 2, 128, 70000, 16, "bf16"),  # 69 blocks: three groups, two levels
+    (8, 1, 128, 32769, 16, "f32"),    # 129 partials a KV head: the merge's loop past its one-round 128
+    (16, 2, 128, 70000, 16, "bf16"),  # 274 partials a KV head, three rounds of the merge's loop
 ]
 
 
@@ -95,7 +95,7 @@ def test_attention_convex_and_page_order(hip):
     vf = oracle.bf16_to_f32(v)
     j = np.arange(kv_len)
     for h in range(H):
-        rows = vf[table[j // 16], j % 16, h // 8]
+        rows = vf[table[j // 16], h // 8, j % 16]
         assert np.all(got[h] <= rows.max(0) + 1e-5) and np.all(got[h] >= rows.min(0) - 1e-5)
     # the same logical cache under another physical page order reads the same bits
     perm = np.random.default_rng(5).permutation(k.shape[0]).astype(np.int32)

@@ -250,8 +250,8 @@ def paged_case(seed, H, Hkv, D, kv_len, page=16):
     n_pages = (kv_len + page - 1) // page
     perm = oracle.permutation(n_pages, seed)
     q = oracle.gaussian_bf16((H, D), oracle.seed(seed, 1))
-    k = oracle.gaussian_bf16((n_pages, page, Hkv, D), oracle.seed(seed, 2))
-    v = oracle.gaussian_bf16((n_pages, page, Hkv, D), oracle.seed(seed, 3))
+    k = oracle.gaussian_bf16((n_pages, Hkv, page, D), oracle.seed(seed, 2))
+    v = oracle.gaussian_bf16((n_pages, Hkv, page, D), oracle.seed(seed, 3))
     return q, k, v, perm
 
 
@@ -264,8 +264,8 @@ def f64_attention(q, k, v, perm, page, kv_len, H, Hkv, D, scale):
     phys = perm[j // page]
     out = np.zeros((H, D))
     for h in range(H):
-        K = kf[phys, j % page, h // G]
-        V = vf[phys, j % page, h // G]
+        K = kf[phys, h // G, j % page]
+        V = vf[phys, h // G, j % page]
         s = K @ qf[h] * scale
         p = np.exp(s - s.max())
         out[h] = p @ V / p.sum()
@@ -290,7 +290,7 @@ def test_attention_is_a_convex_combination_and_ignores_page_order():
     # a convex combination of the visible V rows stays inside their range
     phys = perm[np.arange(kv_len) // 16]
     for h in range(H):
-        rows = vf[phys, np.arange(kv_len) % 16, h // 4]
+        rows = vf[phys, h // 4, np.arange(kv_len) % 16]
         assert np.all(out[h] <= rows.max(0) + 1e-5) and np.all(out[h] >= rows.min(0) - 1e-5)
     # the same logical cache stored in another page order reads identically
     perm2 = oracle.permutation(len(perm), 99)
@@ -301,10 +301,10 @@ def test_attention_is_a_convex_combination_and_ignores_page_order():
     out2 = oracle.attn_decode_paged(q, k2, v2, perm2, 16, kv_len, H, Hkv, D, 0.125)
     np.testing.assert_array_equal(out, out2)
     # identical keys give uniform weights: the output is the mean of V
-    k3 = np.repeat(k[:1, :1], k.shape[0], 0).repeat(16, 1)
+    k3 = np.broadcast_to(k[:1, :1, :1], k.shape).copy()
     out3 = oracle.attn_decode_paged(q, k3, v, perm, 16, kv_len, H, Hkv, D, 0.125)
     for h in range(H):
-        rows = vf[phys, np.arange(kv_len) % 16, h // 4].astype(np.float64)
+        rows = vf[phys, h // 4, np.arange(kv_len) % 16].astype(np.float64)
         np.testing.assert_allclose(out3[h], rows.mean(0), atol=2e-6)
 
 
