@@ -9,7 +9,7 @@ oom_moe_decode_fp8 with inputs resident in HBM. Two full sets of 128 experts
 256 MB Infinity Cache.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--rounds R]
-                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|turbo|prefill|nvfp4-prefill|gemv|copy]
+                    [--config decode1|decode16|layer1|layer16|nvfp4|offload|attn|turbo|prefill|nvfp4-prefill|gemv|copy|bf16]
 
 After W untimed warm-up steps, R rounds (default 5) of K back-to-back steps are timed with
 HIP events on the launch stream; `value` is the median round, and `timing` holds every
@@ -796,6 +796,70 @@ def bench_nvfp4_prefill(args):
     return res
 
 
+def bench_bf16(args):
+    """The routed experts over bf16 records (the format's unquantised `bf16` layout) at the
+    FP8 decode shape: 128 experts, 8 picked per step, hidden 4096, inter 1536, batch 1, bf16
+    x; a step is oom_moe_gate_up_bf16, oom_moe_down_bf16 and oom_moe_combine_slots over a
+    plan built beforehand for every step (seeded picks, different experts each step). Two
+    sets of 128 records (2 x 4.8 GB) alternate so weights stream from HBM."""
+    import numpy as np
+    import torch
+
+    import homelab_amd as hip
+
+    T, E, k, H, I = 1, 128, 8, 4096, 1536
+    geo = hip.bf16_geometry(H, I)
+    stride = (geo.down_weight + H * I * 2 + 4095) // 4096 * 4096
+    log(f"bench: bf16-record experts T={T} E={E} k={k} H={H} I={I}; building 2 sets of {E * stride / 1e9:.2f} GB")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(123)
+    sets = []
+    for s_ in range(2):
+        buf = torch.empty((E, stride), dtype=torch.uint8, device="cuda")
+        for e in range(E):
+            for off_, n in [(geo.gate_weight, I * H), (geo.up_weight, I * H), (geo.down_weight, H * I)]:
+                w = (torch.randn(n, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+                buf[e, off_:off_ + 2 * n] = w.view(torch.uint8)
+        sets.append(buf)
+    n = args.warmup + args.rounds * args.steps
+    rng = np.random.default_rng(5)
+    picks = np.stack([np.sort(rng.choice(E, size=k, replace=False)) for _ in range(n)])
+    recs = torch.tensor([[sets[i % 2].data_ptr() + int(e) * stride for e in picks[i]] for i in range(n)],
+                        dtype=torch.int64, device="cuda")
+    off = torch.arange(k + 1, dtype=torch.int32, device="cuda")
+    tok = torch.zeros(k, dtype=torch.int32, device="cuda")
+    slot = torch.arange(k, dtype=torch.int32, device="cuda").reshape(1, k)
+    wts = torch.full((1, k), 1.0 / k, dtype=torch.float32, device="cuda")
+    x = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+    h = torch.empty((k, I), dtype=torch.float32, device="cuda")
+    y = torch.empty((k, H), dtype=torch.float32, device="cuda")
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        hip.moe_gate_up_bf16(recs[i], off, tok, k, x, h, geo, stream)
+        hip.moe_down_bf16(recs[i], off, k, h, y, geo, stream)
+        hip.moe_combine_slots(y, slot, wts, out, stream)
+
+    for i in range(args.warmup):
+        step(i)
+    ms, timing = time_rounds(step, args.warmup, args, stream, torch)
+    bytes_step = k * 3 * H * I * 2 + 2 * T * H * 2
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    return {
+        "metric": "bf16-record routed experts us/token + achieved HBM GB/s (% of MI355X peak), 1 GPU",
+        "value": ms * 1e3 / T, "unit": "us/token", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "timing": timing, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 weights and x, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "routed experts over bf16 records, batch 1: 8 of 128 experts a step, hidden 4096, "
+                               "inter 1536, bf16 N(0,0.02) weights; 2 record sets alternate past the MALL",
+                   "batch": T, "experts": E, "picked": k, "hidden": H, "inter": I},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": measured_traffic("bf16"), "kernel": "moe_gate_up_bf16_kernel + moe_down_bf16_kernel",
+                     "algorithmic_bytes_per_step": float(bytes_step)},
+    }
+
+
 def bench_nvfp4(args):
     """One routed MoE decode step over NVFP4 (nvfp4-modelopt-g16) records at the released
     model's routed geometry: 512 experts, top-10, hidden 2560, inter 640, batch 1, fresh
@@ -1083,7 +1147,7 @@ def main():
     ap.add_argument("--rounds", type=int, default=5,
                     help="timed rounds of --steps launches each; the value is the median round")
     ap.add_argument("--config", default="decode1", choices=["decode1", "decode16", "layer1", "layer16", "nvfp4", "offload", "attn",
-                                                            "turbo", "prefill", "nvfp4-prefill", "gemv", "copy"])
+                                                            "turbo", "prefill", "nvfp4-prefill", "gemv", "copy", "bf16"])
     ap.add_argument("--prefill-precision", default="exact", choices=["exact", "bf16"],
                     help="activation precision of the prefill's down projection (the reference's ExpertPrecision)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -1127,6 +1191,8 @@ def run_config(args, torch):
         res = bench_offload(args)
     elif args.config == "nvfp4":
         res = bench_nvfp4(args)
+    elif args.config == "bf16":
+        res = bench_bf16(args)
     elif args.config in ("layer1", "layer16"):
         res = bench_layer(args, 1 if args.config == "layer1" else 16, args.config)
     else:

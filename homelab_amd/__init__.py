@@ -51,6 +51,8 @@ SIGNATURES = {
     "oom_moe_layer_decode_fp8": (I32, [P, I32, P, P, I32, I32, I32, P, P, P, P, P, P, P, I32, P, SZ, P]),
     "oom_moe_gate_up_fp8": (I32, [P, P, P, I32, P, I32, P, P, P]),
     "oom_moe_down_fp8": (I32, [P, P, I32, P, P, P, P]),
+    "oom_moe_gate_up_bf16": (I32, [P, P, P, I32, P, I32, P, P, P]),
+    "oom_moe_down_bf16": (I32, [P, P, I32, P, P, P, P]),
     "oom_moe_combine_slots": (I32, [P, P, P, P, I32, I32, I32, I32, P]),
     "oom_moe_plan_size": (SZ, [I32, I32, I32]),
     "oom_moe_plan": (I32, [P, I32, I32, I32, P, P, P, P]),
@@ -176,6 +178,22 @@ def record_stride(geo: Fp8Record) -> int:
     return (end + 4095) // 4096 * 4096
 
 
+class Bf16Record(ctypes.Structure):
+    """OomBf16Record of include/oom_hip.h: part offsets of a bf16 expert record."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in ("hidden", "inter", "gate_weight", "up_weight", "down_weight")]
+
+
+def bf16_geometry(hidden: int, inter: int) -> Bf16Record:
+    """The bf16 record layout (gate.weight, up.weight, down.weight; parts 256-byte aligned)."""
+    def al(v):
+        return (v + 255) // 256 * 256
+    gw = 0
+    uw = al(gw + inter * hidden * 2)
+    dw = al(uw + inter * hidden * 2)
+    return Bf16Record(hidden, inter, gw, uw, dw)
+
+
 class Nvfp4Record(ctypes.Structure):
     """OomNvfp4Record of include/oom_hip.h: part offsets of an NVFP4 expert record and the
     float indices of its three weight_scale_2 scalars."""
@@ -239,6 +257,16 @@ def moe_gate_up_fp8(recs, off, assign_tok, n_experts: int, x, h, geo: Fp8Record,
 def moe_down_fp8(recs, off, n_experts: int, h, y, geo: Fp8Record, stream=None) -> None:
     check(lib().oom_moe_down_fp8(_ptr(recs), _ptr(off), n_experts, _ptr(h), _ptr(y), ctypes.byref(geo),
                                  _stream(stream)))
+
+
+def moe_gate_up_bf16(recs, off, assign_tok, n_experts: int, x, h, geo: Bf16Record, stream=None) -> None:
+    check(lib().oom_moe_gate_up_bf16(_ptr(recs), _ptr(off), _ptr(assign_tok), n_experts, _ptr(x), _dtype_code(x),
+                                     _ptr(h), ctypes.byref(geo), _stream(stream)))
+
+
+def moe_down_bf16(recs, off, n_experts: int, h, y, geo: Bf16Record, stream=None) -> None:
+    check(lib().oom_moe_down_bf16(_ptr(recs), _ptr(off), n_experts, _ptr(h), _ptr(y), ctypes.byref(geo),
+                                  _stream(stream)))
 
 
 def moe_combine_slots(y, slot_assign, w, out, stream=None) -> None:

@@ -230,9 +230,9 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint64_t* __restric
 }
 
 // out[t, c] = sum_s w[t, s] * y[slot_assign[t, s], c] in slot order
-// (crates/oominf-cuda/kernels/moe.cu:153-164).
-// out[t, c] = sum_s w[t, s] * y[slot[t, s], c] in slot order. Block (token t, column
-// chunk of 1024): each thread 4 consecutive columns with 16-byte loads of y.
+// (crates/oominf-cuda/kernels/moe.cu:153-164). Block (token t, column chunk of 1024): each
+// thread 4 consecutive columns; the slots go 8 at a time, their indices and weights first,
+// then the 8 rows' 16-byte loads together, then the multiply-adds in slot order.
 template <int ODT>
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ slot,
                                                           const float* __restrict__ w, void* __restrict__ out, int T,
@@ -241,17 +241,32 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
     if (c0 >= H) return;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const bool vec = c0 + 4 <= H && (H & 3) == 0;
-    for (int s = 0; s < k; s++) {
-        const float ws = w[t * k + s];
-        const float* row = y + (size_t)slot[t * k + s] * H;
+    for (int s0 = 0; s0 < k; s0 += 8) {
+        int sl[8];
+        float ws[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const bool ok = s0 + i < k;
+            sl[i] = ok ? slot[t * k + s0 + i] : 0;
+            ws[i] = ok ? w[t * k + s0 + i] : 0.0f;
+        }
         if (vec) {
-            const float4 v = *reinterpret_cast<const float4*>(row + c0);
-            acc[0] = fmaf(ws, v.x, acc[0]);
-            acc[1] = fmaf(ws, v.y, acc[1]);
-            acc[2] = fmaf(ws, v.z, acc[2]);
-            acc[3] = fmaf(ws, v.w, acc[3]);
+            float4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                v[i] = s0 + i < k ? *reinterpret_cast<const float4*>(y + (size_t)sl[i] * H + c0)
+                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (s0 + i >= k) break;
+                acc[0] = fmaf(ws[i], v[i].x, acc[0]);
+                acc[1] = fmaf(ws[i], v[i].y, acc[1]);
+                acc[2] = fmaf(ws[i], v[i].z, acc[2]);
+                acc[3] = fmaf(ws[i], v[i].w, acc[3]);
+            }
         } else {
-            for (int j = 0; j < 4 && c0 + j < H; j++) acc[j] = fmaf(ws, row[c0 + j], acc[j]);
+            for (int i = 0; i < 8 && s0 + i < k; i++)
+                for (int j = 0; j < 4 && c0 + j < H; j++) acc[j] = fmaf(ws[i], y[(size_t)sl[i] * H + c0 + j], acc[j]);
         }
     }
     for (int j = 0; j < 4 && c0 + j < H; j++) store_out<ODT>(out, (size_t)t * H + c0 + j, acc[j]);

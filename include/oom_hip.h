@@ -64,6 +64,18 @@ typedef struct OomFp8Record {
     int64_t down_scale;
 } OomFp8Record;
 
+/* Byte layout of a bf16 expert record (layout tag "bf16", docs/dev/format.md:72-73:
+ * unquantised weights as released): byte offsets of gate.weight and up.weight (bf16
+ * [inter, hidden]) and down.weight (bf16 [hidden, inter]), row-major, each 16-byte
+ * aligned. The reference's Bf16Record (crates/oominf-core/src/backend.rs:800-807). */
+typedef struct OomBf16Record {
+    int64_t hidden;
+    int64_t inter;
+    int64_t gate_weight;
+    int64_t up_weight;
+    int64_t down_weight;
+} OomBf16Record;
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* oom_last_error(void);
 
@@ -148,6 +160,18 @@ int oom_moe_gate_up_fp8(const uint64_t* recs, const int32_t* off, const int32_t*
  * crates/oominf-cuda/src/experts.rs:174-209). */
 int oom_moe_down_fp8(const uint64_t* recs, const int32_t* off, int n_experts, const float* h, float* y,
                      const OomFp8Record* geo, void* stream);
+
+/* The routed experts' gate/up + SwiGLU and down projection over bf16 records read in
+ * place, for decode-sized steps: the arguments and results of oom_moe_gate_up_fp8 and
+ * oom_moe_down_fp8 with the weights bf16 (widened exactly to fp32), fp32 products and
+ * accumulation, x in x_dtype (f32 or bf16). hidden and inter multiples of 8 up to 4096.
+ * Replace Experts::moe_gate_up_bf16 and Experts::moe_down_bf16
+ * (crates/oominf-core/src/backend.rs:837-858; crates/oominf-cuda/kernels/moe.cu:343-443),
+ * called by run_group for Geometry::Bf16 (crates/oominf-models-qwen/src/moe.rs:741-744). */
+int oom_moe_gate_up_bf16(const uint64_t* recs, const int32_t* off, const int32_t* assign_tok, int n_experts,
+                         const void* x, int x_dtype, float* h, const OomBf16Record* geo, void* stream);
+int oom_moe_down_bf16(const uint64_t* recs, const int32_t* off, int n_experts, const float* h, float* y,
+                      const OomBf16Record* geo, void* stream);
 
 /* out[t, c] = sum_s w[t, s] * y[slot_assign[t, s], c], summed in slot order.
  * y f32 [A, H]; w f32 [T, k]; out [T, H] in out_dtype.

@@ -54,6 +54,27 @@ def record_geometry(hidden: int, inter: int) -> Fp8Record:
     return Fp8Record(hidden, inter, gw, gs, uw, us, dw, ds)
 
 
+class Bf16Record(ctypes.Structure):
+    """OomBf16Record of include/oom_hip.h: byte offsets of a bf16 expert record's parts."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in ("hidden", "inter", "gate_weight", "up_weight", "down_weight")]
+
+
+def bf16_geometry(hidden: int, inter: int) -> Bf16Record:
+    """The bf16 record layout (docs/dev/format.md:72-73): gate.weight, up.weight bf16
+    [inter, hidden], down.weight bf16 [hidden, inter], each part 256-byte aligned."""
+    def al(v):
+        return (v + 255) // 256 * 256
+    gw = 0
+    uw = al(gw + inter * hidden * 2)
+    dw = al(uw + inter * hidden * 2)
+    return Bf16Record(hidden, inter, gw, uw, dw)
+
+
+def bf16_stride(geo: Bf16Record) -> int:
+    return (geo.down_weight + geo.hidden * geo.inter * 2 + 4095) // 4096 * 4096
+
+
 class Nvfp4Record(ctypes.Structure):
     """OomNvfp4Record of include/oom_hip.h: byte offsets of an NVFP4 expert record's parts
     and the float indices of the three weight_scale_2 scalars."""
@@ -134,6 +155,8 @@ def lib() -> ctypes.CDLL:
             "oracle_e2m1_to_f32": (F, [ctypes.c_uint8]),
             "oracle_nvfp4_rows": (None, [P, P, F, I64, I64, P, I32, P]),
             "oracle_moe_gate_up_nvfp4": (None, [P, P, P, I32, P, P, P]),
+            "oracle_moe_gate_up_bf16": (None, [P, P, P, I32, P, P, P]),
+            "oracle_moe_down_bf16": (None, [P, P, I32, P, P, P]),
             "oracle_moe_down_nvfp4": (None, [P, P, I32, P, P, P]),
             "oracle_moe_decode_nvfp4": (I32, [P, P, P, I32, I32, I32, P, P, P, P]),
             "oracle_grouped_gemm_fp8": (None, [P, P, P, I32, P, P, I32, P, I64, I64, I64, I64]),
@@ -415,6 +438,25 @@ def nvfp4_rows(packed: np.ndarray, scales: np.ndarray, s2: float, x: np.ndarray)
     T = x.shape[0]
     y = np.empty((T, rows), dtype=np.float32)
     lib().oracle_nvfp4_rows(_p(packed), _p(scales), s2, rows, 2 * half, _p(x), T, _p(y))
+    return y
+
+
+def moe_gate_up_bf16(recs, off, assign_tok, x: np.ndarray, geo: Bf16Record) -> np.ndarray:
+    """h f32 [A, inter] over bf16 records (uint8 arrays), x f32 [*, hidden]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    h = np.empty((int(off[-1]), geo.inter), dtype=np.float32)
+    lib().oracle_moe_gate_up_bf16(_p(_ptrs(recs)), _p(np.ascontiguousarray(off, dtype=np.int32)),
+                                  _p(np.ascontiguousarray(assign_tok, dtype=np.int32)), len(recs), _p(x), _p(h),
+                                  ctypes.byref(geo))
+    return h
+
+
+def moe_down_bf16(recs, off, h: np.ndarray, geo: Bf16Record) -> np.ndarray:
+    """y f32 [A, hidden] over bf16 records, h f32 [A, inter]."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    y = np.empty((int(off[-1]), geo.hidden), dtype=np.float32)
+    lib().oracle_moe_down_bf16(_p(_ptrs(recs)), _p(np.ascontiguousarray(off, dtype=np.int32)), len(recs), _p(h), _p(y),
+                               ctypes.byref(geo))
     return y
 
 

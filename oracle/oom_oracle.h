@@ -147,6 +147,13 @@ float oracle_e2m1_to_f32(uint8_t code);
 void oracle_nvfp4_rows(const uint8_t* packed, const uint8_t* scales, float s2, int64_t rows, int64_t cols,
                        const float* x, int T, float* y);
 /* gate/up + SwiGLU and down over NVFP4 records (moe.cu:52-151 semantics). */
+/* bf16 records (layout tag bf16; bf16rec.c): the reference's moe_gate_up_bf16 and
+ * moe_down_bf16 (crates/oominf-cuda/kernels/moe.cu:343-443). */
+void oracle_moe_gate_up_bf16(const uint8_t* const* recs, const int32_t* off, const int32_t* assign_tok, int n_e,
+                             const float* x, float* h, const OomBf16Record* geo);
+void oracle_moe_down_bf16(const uint8_t* const* recs, const int32_t* off, int n_e, const float* h, float* y,
+                          const OomBf16Record* geo);
+
 void oracle_moe_gate_up_nvfp4(const uint8_t* const* recs, const int32_t* off, const int32_t* assign_tok, int n_e,
                               const float* x, float* h, const OomNvfp4Record* geo);
 void oracle_moe_down_nvfp4(const uint8_t* const* recs, const int32_t* off, int n_e, const float* h, float* y,
