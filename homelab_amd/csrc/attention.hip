@@ -343,88 +343,90 @@ __global__ void __launch_bounds__(AW * 64) attn_decode_kernel(AttnArgs a) {
     *reinterpret_cast<float4*>(mine + 2 * AG + h * D + c0) = make_float4(A[0], A[1], A[2], A[3]);
 }
 
-// The merge of a KV head's block partials, one block of 64 per (KV head g, query head h):
-// the global max over the partials, each partial's weight exp(M_b - M) (in LDS), the sum,
-// and lane l's columns 2 l, 2 l + 1 of sum_b w_b acc_b in block order; out = acc / sum. A
-// second kernel, not a merge inside the first: a merge there puts three device-scope round
-// trips (stores acknowledged, a ticket, the partials' loads) on the last block's path,
-// which cost more than a kernel boundary.
+// The merge of a KV head's block partials: the global max over the partials, each partial's
+// weight exp(M_b - M) (in LDS), the sum, and sum_b w_b acc_b in block order; out = acc / sum.
+// A second kernel, not a merge inside the first: a merge there puts three device-scope round
+// trips (stores acknowledged, a ticket, the partials' loads) on the last block's path, which
+// cost more than a kernel boundary.
+//  * Up to 128 partials (32 Ki keys): block (g, h, q) of two waves merges columns 32 q .. 32 q
+//    + 31 of head h, so 4 blocks share a head and the grid spreads the partials' loads over 4
+//    times as many CUs. Wave w takes partials 64 w .. 64 w + 63: lane l computes partial
+//    64 w + l's weight, then loads column 32 q + l % 32 of partials 64 w + 2 j + l / 32
+//    (j < 32), every load in flight at once; the two lane halves, then the two waves, add up.
+//  * More partials: one wave walks them in rounds of 64 (q = 0 blocks only).
 template <int D, int ODT>
 __global__ void __launch_bounds__(128) attn_merge_kernel(AttnArgs a) {
-    static_assert(D == 128, "two columns a lane");
-    constexpr int PSZ = 2 * AG + AG * D, CH = 64;  // partials a lane loads at once
+    static_assert(D == 128, "four quarters of 32 columns");
+    constexpr int PSZ = 2 * AG + AG * D, CH = 64;  // partials a wave covers at once
     __shared__ float wts[A_MAXB];
-    __shared__ float part_m[2], part_l[2], part_a[2][D];
+    __shared__ float part_m[2], part_l[2], part_a[2][32];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = blockIdx.x, h = blockIdx.y, n = a.bph;
-    const int c0 = 2 * lane;
     const float* hp = a.part + (size_t)g * n * PSZ;
-    float M = -INFINITY, L = 0.0f, A0 = 0.0f, A1 = 0.0f;
     if (n <= 2 * CH) {
-        // up to 128 partials (32 Ki keys): wave w merges partials 64 w .. 64 w + 63 with
-        // every load in flight at once, then the two waves' (max, sum, acc) meet in LDS
-        const int q = CH * wave + lane;
-        const bool ok = q < n;
-        const float mq = ok ? hp[(size_t)q * PSZ + h] : -INFINITY;
-        const float lq = ok ? hp[(size_t)q * PSZ + AG + h] : 0.0f;
-        float2 v[CH];
+        const int q = blockIdx.z, col = 32 * q + (lane & 31), par = lane >> 5;
+        const int p = CH * wave + lane;
+        const bool ok = p < n;
+        const float mq = ok ? hp[(size_t)p * PSZ + h] : -INFINITY;
+        const float lq = ok ? hp[(size_t)p * PSZ + AG + h] : 0.0f;
+        float v[CH / 2];
 #pragma unroll
-        for (int j = 0; j < CH; j++)
-            v[j] = CH * wave + j < n ? *reinterpret_cast<const float2*>(hp + (size_t)(CH * wave + j) * PSZ + 2 * AG +
-                                                                        h * D + c0)
-                                     : make_float2(0.0f, 0.0f);
-        float Mw = wave_max(mq);  // -inf only for a wave with no partial
+        for (int j = 0; j < CH / 2; j++) {
+            const int pj = CH * wave + 2 * j + par;
+            v[j] = pj < n ? hp[(size_t)pj * PSZ + 2 * AG + h * D + col] : 0.0f;
+        }
+        const float Mw = wave_max(mq);  // -inf only for a wave with no partial
         const float w = mq == -INFINITY ? 0.0f : expf(mq - Mw);
         const float Lw = wave_sum(lq * w);
-        wts[q] = w;
+        wts[p] = w;
         wave_lds_order();
+        float A = 0.0f;
 #pragma unroll
-        for (int j = 0; j < CH; j++) {  // past n: zero columns and weights
-            A0 = fmaf(v[j].x, wts[CH * wave + j], A0);
-            A1 = fmaf(v[j].y, wts[CH * wave + j], A1);
-        }
+        for (int j = 0; j < CH / 2; j++) A = fmaf(v[j], wts[CH * wave + 2 * j + par], A);  // past n: zeros
+        A += lane_xor<32>(A, lane);  // the two lane halves (even and odd partials)
         if (lane == 0) {
             part_m[wave] = Mw;
             part_l[wave] = Lw;
         }
-        part_a[wave][c0] = A0;
-        part_a[wave][c0 + 1] = A1;
+        if (lane < 32) part_a[wave][lane] = A;
         __syncthreads();
-        if (wave == 1) return;
-        M = fmaxf(part_m[0], part_m[1]);  // finite: every block holds a visible key
+        if (wave == 1 || lane >= 32) return;
+        const float M = fmaxf(part_m[0], part_m[1]);  // finite: every block holds a visible key
         const float f0 = part_m[0] == -INFINITY ? 0.0f : expf(part_m[0] - M);
         const float f1 = part_m[1] == -INFINITY ? 0.0f : expf(part_m[1] - M);
-        L = fmaf(part_l[1], f1, part_l[0] * f0);
-        A0 = fmaf(part_a[1][c0], f1, part_a[0][c0] * f0);
-        A1 = fmaf(part_a[1][c0 + 1], f1, part_a[0][c0 + 1] * f0);
-    } else {
-        if (wave == 1) return;
-        for (int q = lane; q < n; q += 64) M = fmaxf(M, hp[(size_t)q * PSZ + h]);
-        M = wave_max(M);
-        for (int q0 = 0; q0 < n; q0 += 64) {
-            const int q = q0 + lane;
-            float w = 0.0f, lq = 0.0f;
-            if (q < n) {
-                const float mq = hp[(size_t)q * PSZ + h];
-                w = mq == -INFINITY ? 0.0f : expf(mq - M);
-                lq = hp[(size_t)q * PSZ + AG + h];
-                wts[q] = w;
-            }
-            L += wave_sum(lq * w);
+        const float L = fmaf(part_l[1], f1, part_l[0] * f0);
+        const float A1 = fmaf(part_a[1][lane], f1, part_a[0][lane] * f0);
+        store_out<ODT>(a.out, (size_t)(g * a.G + h) * D + col, A1 / L);
+        return;
+    }
+    if (wave == 1 || blockIdx.z != 0) return;
+    const int c0 = 2 * lane;
+    float M = -INFINITY, L = 0.0f, A0 = 0.0f, A1 = 0.0f;
+    for (int p = lane; p < n; p += 64) M = fmaxf(M, hp[(size_t)p * PSZ + h]);
+    M = wave_max(M);
+    for (int p0 = 0; p0 < n; p0 += 64) {
+        const int p = p0 + lane;
+        float w = 0.0f, lq = 0.0f;
+        if (p < n) {
+            const float mq = hp[(size_t)p * PSZ + h];
+            w = mq == -INFINITY ? 0.0f : expf(mq - M);
+            lq = hp[(size_t)p * PSZ + AG + h];
+            wts[p] = w;
         }
-        wave_lds_order();
-        for (int q0 = 0; q0 < n; q0 += CH) {
-            float2 v[CH];
+        L += wave_sum(lq * w);
+    }
+    wave_lds_order();
+    for (int p0 = 0; p0 < n; p0 += CH) {
+        float2 v[CH];
 #pragma unroll
-            for (int j = 0; j < CH; j++)
-                v[j] = q0 + j < n ? *reinterpret_cast<const float2*>(hp + (size_t)(q0 + j) * PSZ + 2 * AG + h * D + c0)
-                                  : make_float2(0.0f, 0.0f);
+        for (int j = 0; j < CH; j++)
+            v[j] = p0 + j < n ? *reinterpret_cast<const float2*>(hp + (size_t)(p0 + j) * PSZ + 2 * AG + h * D + c0)
+                              : make_float2(0.0f, 0.0f);
 #pragma unroll
-            for (int j = 0; j < CH; j++) {
-                if (q0 + j >= n) break;
-                const float w = wts[q0 + j];
-                A0 = fmaf(v[j].x, w, A0);
-                A1 = fmaf(v[j].y, w, A1);
-            }
+        for (int j = 0; j < CH; j++) {
+            if (p0 + j >= n) break;
+            const float w = wts[p0 + j];
+            A0 = fmaf(v[j].x, w, A0);
+            A1 = fmaf(v[j].y, w, A1);
         }
     }
     const size_t oi = (size_t)(g * a.G + h) * D + c0;
@@ -453,7 +455,7 @@ static int launch_attn_t(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_decode_kernel<D, QDT, ODT>), dim3(a.bph, a.Hkv), dim3(AW * 64), 0, st, a);
     if (a.bph > 1) {
         if (int rc = launched("oom_attn_decode_paged")) return rc;
-        hipLaunchKernelGGL((attn_merge_kernel<D, ODT>), dim3(a.Hkv, a.G), dim3(128), 0, st, a);
+        hipLaunchKernelGGL((attn_merge_kernel<D, ODT>), dim3(a.Hkv, a.G, a.bph <= 128 ? 4 : 1), dim3(128), 0, st, a);
     }
     return launched("oom_attn_decode_paged");
 }
