@@ -55,7 +55,35 @@ struct GArgs {
     float* y;               // [A, N] fp32 (plain and down passes)
     uint16_t* hh;           // [A, N] bf16 hi term of h (gate/up pass) / of the activations (down pass)
     uint16_t* hl;           // [A, N] bf16 lo term
+#ifdef OOM_STAMPS
+    uint64_t* stamps;       // per block: start, end, (expert, first assignment, N offset, assignments), where
+#endif
 };
+
+// A profiling build (-DOOM_STAMPS) records each block's start and end on the 100 MHz clock,
+// its tile and the XCC / HW_ID it ran on: 4 words per linear block id.
+#ifdef OOM_STAMPS
+uint64_t* stamps_buffer();
+__device__ __forceinline__ void g_stamp(uint64_t* st, int L, int p, uint64_t v) {
+    if (st && threadIdx.x == 0) st[4 * (size_t)L + p] = v;
+}
+#define G_STAMP_START(G, L, I, M0, N0, CNT)                                                                  \
+    do {                                                                                                     \
+        g_stamp((G).stamps, L, 0, wall_clock64());                                                           \
+        g_stamp((G).stamps, L, 2, ((uint64_t)(I) << 48) | ((uint64_t)(M0) << 32) | ((uint64_t)(N0) << 16) |  \
+                                      (uint64_t)(CNT));                                                      \
+        g_stamp((G).stamps, L, 3, ((uint64_t)(uint32_t)__builtin_amdgcn_s_getreg(20 | (15 << 11)) << 32) |   \
+                                      (uint32_t)__builtin_amdgcn_s_getreg(4 | (31 << 11)));                  \
+    } while (0)
+#define G_STAMP_END(G, L) g_stamp((G).stamps, L, 1, wall_clock64())
+#else
+#define G_STAMP_START(G, L, I, M0, N0, CNT) \
+    do {                                    \
+    } while (0)
+#define G_STAMP_END(G, L) \
+    do {                  \
+    } while (0)
+#endif
 
 // e4m3fn code of v, round to nearest even, saturating at +-448 (the quantiser's rule,
 // crates/oominf-core/src/fp8.rs:5-27), with the gfx950 OCP-FP8 conversion.
@@ -240,7 +268,7 @@ __device__ __forceinline__ void g_barrier() {
 template <int NB>
 struct GSrc {
     __amdgpu_buffer_rsrc_t xr, wr, xsr, sr;
-    int xo[2], wo[NB][2];  // step-0 byte offsets
+    int xo[2], wo[NB][2];  // step-0 byte offsets (xo < 0: a row past the expert, loads zeros)
     int xso, so;           // step-0 byte offsets of this lane's scales (G_OOB: none)
 };
 
@@ -253,7 +281,7 @@ __device__ __forceinline__ void g_issue(const GSrc<NB>& s, int kb, int nkb, uint
     const bool ok = kb < nkb;
     const int k0 = kb * GBK;
 #pragma unroll
-    for (int j = 0; j < 2; j++) dma16(s.xr, sb + (2 * wave + j) * 1024, ok ? s.xo[j] + k0 : G_OOB);
+    for (int j = 0; j < 2; j++) dma16(s.xr, sb + (2 * wave + j) * 1024, ok && s.xo[j] >= 0 ? s.xo[j] + k0 : G_OOB);
 #pragma unroll
     for (int m = 0; m < NB; m++)
 #pragma unroll
@@ -369,12 +397,16 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     }
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
+    const int Lb = (int)(blockIdx.x + blockIdx.y * gridDim.x);
+    (void)Lb;
+    G_STAMP_START(g, Lb, i, m0, n0, a1 - a0);
     const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
     const int nkb = (int)(g.K / GBK);
     const bool xgrp = g.x_group != 0;
     // ---- this thread's sources: load j of the A (and each B) tile covers positions
     // (2 wave + j) 64 + lane, i.e. chunk c of tile row r (rows past the expert's range
-    // repeat its first assignment) ----
+    // load zeros from past the resource: no memory traffic, and their products are not
+    // stored) ----
     GSrc<NB> src;
     src.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.xq), (short)0, 0x7fff0000, G_BUF_FLAGS);
     const int wbytes = (int)(max(g.w_off, NB == 2 ? g.w2_off : g.w_off) + g.N * g.K);  // end of the weight parts
@@ -383,9 +415,8 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     for (int j = 0; j < 2; j++) {
         int r, c;
         pos_chunk((2 * wave + j) * 64 + lane, r, c);
-        int a = a0 + m0 + r;
-        if (a >= a1) a = a0;
-        src.xo[j] = (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c;
+        const int a = a0 + m0 + r;
+        src.xo[j] = a < a1 ? (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c : -1;
 #pragma unroll
         for (int m = 0; m < NB; m++)
             src.wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r) * g.K) + 16 * c;
@@ -484,6 +515,7 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
                 }
             }
     }
+    G_STAMP_END(g, Lb);
 }
 
 // ---- down pass over h as one or two bf16 terms ----------------------------------------
@@ -525,7 +557,7 @@ constexpr int dw_lps() { return 2 * TERMS + 2 + 1; }
 
 struct DWSrc {
     __amdgpu_buffer_rsrc_t hr, wr, sr;
-    int ho[2], wo[2];
+    int ho[2], wo[2];  // step-0 byte offsets (ho < 0: a row past the expert, loads zeros)
     int hl_off;
     int so;
 };
@@ -538,7 +570,8 @@ __device__ __forceinline__ void dw_issue(const DWSrc& s, int kb, int nkb, uint8_
     for (int t = 0; t < TERMS; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
-            dma16(s.hr, sb + t * D_HT + (2 * wave + j) * 1024, ok ? s.ho[j] + t * s.hl_off + k0 : G_OOB);
+            dma16(s.hr, sb + t * D_HT + (2 * wave + j) * 1024,
+                  ok && s.ho[j] >= 0 ? s.ho[j] + t * s.hl_off + k0 : G_OOB);
 #pragma unroll
     for (int j = 0; j < 2; j++)
         dma16(s.wr, sb + TERMS * D_HT + (2 * wave + j) * 1024, ok ? s.wo[j] + kb * GBK2 : G_OOB);
@@ -605,7 +638,7 @@ __device__ __forceinline__ void dw_reads(const uint8_t* sb, int wm, int wn, int 
 }
 
 // act: this wave's 16-row M subtiles that hold assignments (1 or 2; a subtile past the
-// expert's last assignment only repeats its first one, and its products are not stored).
+// expert's last assignment holds zeros, and its products are not stored).
 template <int TERMS>
 __device__ __forceinline__ void dw_step(const uint8_t* sb, int wm, int wn, int wave, int lane, bool fold, int act,
                                         gf32x4 (&blk)[2][8], float (&acc)[2][8][4]) {
@@ -670,6 +703,7 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
     const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBNW;
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
+    G_STAMP_START(g, L, i, m0, n0, a1 - a0);
     const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
     const int nkb = (int)(g.K / GBK2);
     DWSrc src;
@@ -681,9 +715,8 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
     for (int j = 0; j < 2; j++) {
         int r, c;
         pos_chunk((2 * wave + j) * 64 + lane, r, c);
-        int a = a0 + m0 + r;
-        if (a >= a1) a = a0;
-        src.ho[j] = (int)(a * g.K * 2) + 16 * c;
+        const int a = a0 + m0 + r;
+        src.ho[j] = a < a1 ? (int)(a * g.K * 2) + 16 * c : -1;  // past the expert: zeros
         // weights: position (2 wave + j) 64 + lane = row p / 4, chunk (p % 4) ^ ((row >> 2) & 3)
         const int p = (2 * wave + j) * 64 + lane, wr = p >> 2, wc = (p & 3) ^ ((wr >> 2) & 3);
         src.wo[j] = (int)(g.w_off + (int64_t)(n0 + wr) * g.K) + 16 * wc;
@@ -735,6 +768,7 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
                 if (n < g.N) g.y[(int64_t)a * g.N + n] = acc[ms][ns][e];
             }
         }
+    G_STAMP_END(g, L);
 }
 
 // ---- host side -----------------------------------------------------------------------
@@ -909,6 +943,9 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     a.s2_off = geo->up_scale;
     a.hh = hh;
     a.hl = precision == OOM_EXPERT_EXACT ? hl : nullptr;
+#ifdef OOM_STAMPS
+    a.stamps = stamps_buffer();
+#endif
     // 8 spare rows of blocks: the XCD-run order needs the grid to cover 8 ceil(W / 8) slots
     if (int rc = launch_grouped(a, 1, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles + 8, 1), st)) return rc;
     GArgs d{};
@@ -923,6 +960,10 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     d.hh = hh;
     d.hl = hl;
     d.y = y;
+#ifdef OOM_STAMPS
+    // the down pass's blocks after the gate/up grid's
+    d.stamps = a.stamps ? a.stamps + 4 * (size_t)(geo->inter / GBN) * (w.max_tiles + 8) : nullptr;
+#endif
     const int terms = precision == OOM_EXPERT_EXACT ? 2 : 1;
     if (int rc = launch_grouped_down(d, terms, dim3((unsigned)cdiv(geo->hidden, GBNW), (unsigned)w.max_tiles + 8, 1),
                                      st))
