@@ -4,12 +4,13 @@
 // contiguous, 4 KiB at 16 keys of 128 dims), token j in physical page
 // page_table[j / page_size] at slot j % page_size.
 //
-//  * Block (b, g) takes keys [256 b, 256 b + 256) of KV head g; each of its 4 waves 64
+//  * Block (b, g) takes keys [1024 b, 1024 b + 1024) of KV head g; each of its 4 waves 256
 //    keys, as pairs of 16-key tiles (a tile is one MFMA tile, inside one page: one
 //    contiguous 4 KiB run of K and one of V). K and V of a tile stream once for all G
-//    query heads; the next pair's loads are in flight
-//    while the current one is reduced. At 32 Ki keys the grid holds twice the blocks
-//    that are resident at once, so a CU whose blocks end early starts the next ones.
+//    query heads; the next pair's loads are in flight while the current one is reduced.
+//    At 32 Ki keys and 8 KV heads that is 256 blocks, one a CU, and 32 partials a KV head
+//    for the merge (measured against 64 keys a wave: 29.4 against 31.8 us a step; 128:
+//    30.5; 512 keys a wave, or 8-wave blocks, or two and three pairs in flight: slower).
 //  * Scores S^T = K . Q^T on bf16 MFMA (v_mfma_f32_16x16x32_bf16; products exact, fp32
 //    accumulate): keys are the M side, so K loads need head_dim contiguous per lane
 //    (the layout in memory) and each lane ends with 4 keys of one head, which keeps the
@@ -33,10 +34,10 @@
 namespace oom {
 
 constexpr int AW = 4;           // waves per block
-constexpr int AKW = 64;         // keys per wave
+constexpr int AKW = 256;        // keys per wave
 constexpr int AKB = AW * AKW;   // keys per block
 constexpr int AG = 8;           // query heads per KV head (at most)
-constexpr int A_MAXB = 8192;    // blocks a KV head (2 Mi keys): the merge's weights sit in LDS
+constexpr int A_MAXB = 8192;    // blocks a KV head (8 Mi keys): the merge's weights sit in LDS
 constexpr int A_BUF_FLAGS = 0x00020000;
 constexpr int A_OOB = 0x7ffffff0;
 constexpr int A_BUF_SC1 = 16;
@@ -477,7 +478,7 @@ extern "C" int oom_attn_decode_paged(const void* q, int q_dtype, const uint16_t*
                 "oom_attn_decode_paged: heads must be a multiple of kv_heads, at most 8 query heads per KV head");
     OOM_REQUIRE(page_size >= 16 && page_size % 16 == 0, "oom_attn_decode_paged: page_size must be a multiple of 16");
     OOM_REQUIRE(kv_len >= 1 && n_pages >= 1, "oom_attn_decode_paged: kv_len and n_pages must be >= 1");
-    OOM_REQUIRE(kv_len <= A_MAXB * AKB, "oom_attn_decode_paged: kv_len above 2 Mi keys");
+    OOM_REQUIRE(kv_len <= A_MAXB * AKB, "oom_attn_decode_paged: kv_len above 8 Mi keys");
     OOM_REQUIRE((int64_t)page_size * kv_heads * d * 2 < (1ll << 31), "oom_attn_decode_paged: page too large");
     OOM_REQUIRE(q_dtype == OOM_F32 || q_dtype == OOM_BF16, "oom_attn_decode_paged: q_dtype");
     OOM_REQUIRE(out_dtype == OOM_F32 || out_dtype == OOM_BF16, "oom_attn_decode_paged: out_dtype");

@@ -57,8 +57,10 @@ CASES = [
     (4, 4, 128, 300, 16, "f32"),      # one query head per KV head
     (24, 4, 128, 2100, 16, "bf16"),   # six query heads per KV head
     (8, 2, 128, 4097, 64, "f32"),
-    (8, 1, 128, 32769, 16, "f32"),    # 129 partials a KV head: the merge's loop past its one-round 128
-    (16, 2, 128, 70000, 16, "bf16"),  # 274 partials a KV head, three rounds of the merge's loop
+    (8, 1, 128, 32769, 16, "f32"),    # 33 partials a KV head (1024 keys a block)
+    (16, 2, 128, 70000, 16, "bf16"),  # 69 partials a KV head
+    (8, 1, 128, 131073, 16, "f32"),   # 129 partials: the merge's loop past its one-round 128
+    (8, 1, 128, 280000, 16, "bf16"),  # 274 partials, three rounds of the merge's loop
 ]
 
 
