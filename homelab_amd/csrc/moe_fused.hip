@@ -344,17 +344,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rec_rsrc(const PlanLds& pl, in
                                              BUF_FLAGS);
 }
 
-// Gate/up item `it` (expert it / I, row it % I): one gate row and one up row, 1024
-// columns per chunk, and their 128 x 128-block scales; an item past NG reads zeros.
+// Gate/up item `it` (plan slot item_slot(it), row it % I): one gate row and one up row,
+// 1024 columns per chunk, and their 128 x 128-block scales; an item past NG reads zeros.
+// With a shared expert (plan slot k) its rows come first (items 0 .. I - 1: they need no
+// routing, so they stream while the token is routed), then routed slot s at (s + 1) I.
 struct Gate1 {
     uint4 g[4], u[4];
     float sg[4], su[4];
 };
 
-__device__ __forceinline__ void gate1_load(const FusedArgs& a, const PlanLds& pl, int it, int NG, int lane, Gate1& w) {
+__device__ __forceinline__ int item_slot(const FusedArgs& a, int it, bool shared_first) {
+    const int I = (int)a.I;
+    return shared_first ? (it < I ? a.k : it / I - 1) : it / I;
+}
+
+__device__ __forceinline__ void gate1_load(const FusedArgs& a, const PlanLds& pl, int it, int NG, int lane, Gate1& w,
+                                           bool shared_first = false) {
     const int H = (int)a.H, I = (int)a.I, nkb = (H + 127) >> 7;
     const bool valid = it < NG;
-    const int i = valid ? it / I : 0, j = valid ? it % I : 0;
+    const int i = valid ? item_slot(a, it, shared_first) : 0, j = valid ? it % I : 0;
     const __amdgpu_buffer_rsrc_t r = rec_rsrc(pl, i, valid ? a.rec_bytes : 0);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -371,7 +379,7 @@ __device__ __forceinline__ void gate1_load(const FusedArgs& a, const PlanLds& pl
 // h[a(it), j(it)] = silu(x . gate row) * (x . up row).
 template <int XDT>
 __device__ __forceinline__ void gate1_compute(const FusedArgs& a, const PlanLds& pl, int it, int NG, const Gate1& w,
-                                              const XRow<XDT>& xr, int lane) {
+                                              const XRow<XDT>& xr, int lane, bool shared_first = false) {
     float acc[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -396,7 +404,7 @@ __device__ __forceinline__ void gate1_compute(const FusedArgs& a, const PlanLds&
     const float tot = wave_sum_multi<2>(acc, lane);
     const float up = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 32));
     if (lane == 0 && it < NG) {
-        const int I = (int)a.I, i = it / I, j = it % I;
+        const int I = (int)a.I, i = item_slot(a, it, shared_first), j = it % I;
         st_dev(&a.h[(size_t)pl.off[i] * I + j], siluf(tot) * up);
     }
 }
@@ -622,9 +630,33 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
     if (tid >= RT0 && tid - RT0 < E) pl.recs[tid - RT0] = a.all_recs[tid - RT0];
     if constexpr (SH) {
         if (tid == RT0 + E) pl.recs[E] = a.shared_rec[0];
+        if (tid == 64) {
+            // plan slot k, the shared expert (record E of the table, h row k), and the
+            // claim counter: set before routing, so the shared rows can stream meanwhile
+            pl.experts[k] = E;
+            pl.off[k] = k;
+            pl.off[k + 1] = k + 1;
+            pl.claims = 0u;
+        }
     }
     XRow<XDT> xr;
     if constexpr (TG == 1) xrow_load<XDT>(a.x, (int)a.H, lane, xr);
+    // one token with a shared expert: the waves other than the router's claim their first
+    // item now, and one of the shared expert's rows starts streaming before routing ends
+    // (LDS-only block syncs here and after routing: a __syncthreads would wait for those
+    // loads)
+    int it_pre = 0;
+    Gate1 w0, w1;  // one-token phase 1: the wave's current and next gate/up item
+    if constexpr (SH) {
+        lds_barrier();  // the record table and the shared slot's plan entries
+        if (wave != 0) {
+            uint32_t c = 0;
+            if (lane == 0) c = __hip_atomic_fetch_add(&pl.claims, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            c = __builtin_amdgcn_readfirstlane(c);
+            it_pre = (int)(blockIdx.x * FW1 + c % FW1 + (c / FW1) * gridDim.x * FW1);
+            if (it_pre < (int)a.I) gate1_load(a, pl, it_pre, (int)a.I, lane, w0, true);
+        }
+    }
     // ---- routing and plan: slots sorted by (expert, slot), experts in id order ----
     if (T == 1) {
         // one token: wave 0 routes it and plans in place, one block-wide sync
@@ -639,12 +671,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             if (lane == 0) {
                 pl.n_e = k;
                 pl.off[k] = k;
-                pl.claims = 0u;
-                if constexpr (SH) {
-                    // plan slot k: the shared expert (record E of the table), h row k
-                    pl.experts[k] = E;
-                    pl.off[k + 1] = k + 1;
-                }
+                if constexpr (!SH) pl.claims = 0u;  // with a shared expert: set before routing
             }
         }
         if constexpr (SH) {
@@ -696,7 +723,8 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             }
         }
     }
-    __syncthreads();
+    if constexpr (SH) lds_barrier();
+    else __syncthreads();
     if constexpr (TG == 1) OOM_STAMP(a.stamps, WB, 1);  // routed and planned
     if (blockIdx.x == 0)
         for (int s = tid; s < A; s += blockDim.x) {
@@ -709,7 +737,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
     if constexpr (TG == 1) {
         // ---- phase 1, one token: item it = (expert it / I, row it % I); the next item's
         // loads are in flight while the current one is reduced ----
-        const int NG = (n_e + (SH ? 1 : 0)) * (int)a.I;  // the shared expert's rows last
+        const int NG = (n_e + (SH ? 1 : 0)) * (int)a.I;  // the shared expert's rows first
         // Block b owns items b WB + c % WB + (c / WB) NW (c = 0, 1, ...); its waves claim
         // them in that order from a counter in LDS, so a wave that gets fewer issue slots
         // (the second wave of a SIMD) takes fewer items than its partner.
@@ -719,9 +747,15 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             c = __builtin_amdgcn_readfirstlane(c);
             return (int)(blockIdx.x * WB + c % WB + (c / WB) * NW);
         };
-        Gate1 w0, w1;
-        int it0 = claim();
-        gate1_load(a, pl, it0, NG, lane, w0);
+        int it0;
+        if constexpr (SH) {
+            // the router's wave claims now; a wave whose first item is a routed row loads it now
+            it0 = wave == 0 ? claim() : it_pre;
+            if (wave == 0 || it_pre >= (int)a.I) gate1_load(a, pl, it0, NG, lane, w0, true);
+        } else {
+            it0 = claim();
+            gate1_load(a, pl, it0, NG, lane, w0);
+        }
         // this block's first 16-row output tile of the wave's expert slot (one slot per
         // wave) streams behind the wave's first gate/up item: block b takes tiles b,
         // b + G, ... for all (<= 8) experts
@@ -730,12 +764,12 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
         down1_load<DCH>(a, pl, s0, tb0, s0 < n_e && tb0 < tiles1, lane, d0);
         while (it0 < NG) {
             const int it1 = claim();
-            gate1_load(a, pl, it1, NG, lane, w1);
-            gate1_compute<XDT>(a, pl, it0, NG, w0, xr, lane);
+            gate1_load(a, pl, it1, NG, lane, w1, SH);
+            gate1_compute<XDT>(a, pl, it0, NG, w0, xr, lane, SH);
             if (it1 >= NG) break;
             it0 = claim();
-            gate1_load(a, pl, it0, NG, lane, w0);
-            gate1_compute<XDT>(a, pl, it1, NG, w1, xr, lane);
+            gate1_load(a, pl, it0, NG, lane, w0, SH);
+            gate1_compute<XDT>(a, pl, it1, NG, w1, xr, lane, SH);
         }
         OOM_STAMP(a.stamps, WB, 2);  // gate/up items done, down weights in flight or in
         wait_mem();  // this wave's h stores (and loads) are complete before its block arrives
