@@ -15,6 +15,8 @@
 //    32 x 64); per K step of 128 the block stages the activation rows (gathered by
 //    assignment) and the weight rows in LDS (rows padded to 144 bytes), and the next
 //    step's global loads are in flight while the current step runs on the matrix cores.
+//  * The prefill step's gate/up pass takes 256-assignment tiles instead
+//    (grouped_gate_up256_kernel, two LDS stages of 64 KiB).
 //  * Gate/up: both weight tiles share the activation tile; the epilogue forms
 //    h = silu(g) * u and writes hi = bf16(h) and, for the exact precision, lo =
 //    bf16(h - hi) (16 significant bits, relative error <= 2^-17): h is not quantised
@@ -179,7 +181,7 @@ __global__ void __launch_bounds__(256) quant_rows_vec_kernel(const void* __restr
 // ---- the tile table of a device plan: tile mt = (expert i, assignments from off[i] + m0).
 // One block of 1024 threads; experts in chunks of 1024 with a running carry.
 __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __restrict__ n_e_p,
-                                                             const int32_t* __restrict__ off,
+                                                             const int32_t* __restrict__ off, int tile_rows,
                                                              int32_t* __restrict__ tiles, int32_t* __restrict__ ntiles) {
     __shared__ int wsum[16];
     __shared__ int carry_s;
@@ -188,7 +190,7 @@ __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __re
     __syncthreads();
     for (int c0 = 0; c0 < n_e; c0 += (int)blockDim.x) {
         const int i = c0 + tid;
-        const int cnt = i < n_e ? (off[i + 1] - off[i] + GBM - 1) / GBM : 0;
+        const int cnt = i < n_e ? (off[i + 1] - off[i] + tile_rows - 1) / tile_rows : 0;
         // inclusive scan within the wave, then over the waves
         int incl = cnt;
 #pragma unroll
@@ -203,7 +205,7 @@ __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __re
         const int start = before + incl - cnt;
         for (int t = 0; t < cnt; t++) {
             tiles[2 * (start + t)] = i;
-            tiles[2 * (start + t) + 1] = t * GBM;
+            tiles[2 * (start + t) + 1] = t * tile_rows;
         }
         __syncthreads();
         if (tid == (int)blockDim.x - 1) carry_s = start + cnt;
@@ -518,6 +520,163 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     G_STAMP_END(g, Lb);
 }
 
+// ---- gate/up over 256-assignment tiles (the prefill step) -----------------------------
+//
+// A block takes 256 assignments x 128 gate rows and the same 128 up rows of one expert: a
+// K step moves 64 KiB into LDS (the activation tile 32 KiB, each weight tile 16 KiB) for
+// 256 x 256 x 128 multiply-adds, against 48 KiB for half of that in a 128-row tile, and an
+// expert's weight slab is staged once per 256 assignments instead of once per 128. Wave
+// (wm, wn) of the 8 takes rows 64 wm .. + 64 (4 M subtiles) and rows 64 wn .. + 64 of both
+// weight tiles (4 N subtiles each): 128 accumulators a lane. Two LDS stages: at step kb a
+// wave waits for its own loads of stage kb, the block synchronises (every wave's loads of
+// kb have landed, every wave is done reading the other buffer), stage kb + 1 is issued, and
+// step kb runs on the matrix cores while kb + 1 loads. Per-row activation scales only
+// (x_group 0, the prefill's quantiser). Tiles come from a table of 256-row tiles, in the
+// XCD runs of grouped_gemm_kernel.
+constexpr int GBM2 = 256;                                 // assignments per block tile
+constexpr int GU2_SB = GBM2 * GBK + 2 * GBN * GBK;        // stage operands: A, gate, up tiles
+constexpr int GU2_STOT = GU2_SB + GTHREADS * 4;           // + the weight scales, 64 words a wave
+
+struct GU2Src {
+    __amdgpu_buffer_rsrc_t xr, wr, sr;
+    int xo[4], wo[2][2];  // step-0 byte offsets (xo < 0: a row past the expert, loads zeros)
+    int so;               // step-0 byte offset of this lane's weight block scale (G_OOB: none)
+};
+
+__device__ __forceinline__ void gu2_issue(const GU2Src& s, int kb, int nkb, uint8_t* sb, int wave) {
+    const bool ok = kb < nkb;
+    const int k0 = kb * GBK;
+#pragma unroll
+    for (int j = 0; j < 4; j++) dma16(s.xr, sb + (4 * wave + j) * 1024, ok && s.xo[j] >= 0 ? s.xo[j] + k0 : G_OOB);
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            dma16(s.wr, sb + GBM2 * GBK + m * GBN * GBK + (2 * wave + j) * 1024, ok ? s.wo[m][j] + k0 : G_OOB);
+    dma4(s.sr, reinterpret_cast<float*>(sb + GU2_SB) + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * kb : G_OOB);
+}
+
+// One K step: acc[m][ms][ns] += ws(m) * (block sum of M subtile ms and N subtile ns of
+// weight matrix m). A wave with any assignment runs all 4 M subtiles (rows past the expert
+// hold zeros and are not stored): per-subtile branches cost more registers than the
+// matrix work they save on partial tiles.
+__device__ __forceinline__ void gu2_step(const uint8_t* sb, int wm, int wn, int wave, int lane,
+                                         float (&acc)[2][4][4][4]) {
+    const float* scw = reinterpret_cast<const float*>(sb + GU2_SB) + 64 * wave;
+    const float ws[2] = {scw[0], scw[1]};
+    gi32x8 aop[4];
+#pragma unroll
+    for (int ms = 0; ms < 4; ms++) aop[ms] = gop(sb, 64 * wm + 16 * ms + (lane & 15), lane);
+    // the 8 B operands (gate subtiles, then up) one read ahead of their products: holding
+    // all of them beside the 128 accumulators spills
+    const uint8_t* bt = sb + GBM2 * GBK;
+    const int brow = 64 * wn + (lane & 15);
+    gi32x8 bcur = gop(bt, brow, lane);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const int m = q >> 2, ns = q & 3;
+        gi32x8 bnext = bcur;
+        if (q < 7) bnext = gop(bt + ((q + 1) >> 2) * GBN * GBK, brow + 16 * ((q + 1) & 3), lane);
+#pragma unroll
+        for (int ms = 0; ms < 4; ms++) {
+            const gf32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            const gf32x4 blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop[ms], bcur, z, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = fmaf(blk[e], ws[m], acc[m][ms][ns][e]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        bcur = bnext;
+    }
+}
+
+__global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
+    // each stage its own LDS object, so the compiler's waits for direct-to-LDS loads cover
+    // only the loads into the buffer a read touches
+    __shared__ __align__(16) uint8_t sb0[GU2_STOT], sb1[GU2_STOT];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int NT = (int)gridDim.x, MT = *g.ntiles, W = NT * MT;
+    const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), C = (W + 7) / 8;
+    if ((L >> 3) >= C) return;
+    const int w = (L & 7) * C + (L >> 3);
+    if (w >= W) return;
+    const int nt = w / MT, mt = w - nt * MT;
+    const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBN;
+    const int a0 = g.off[i], a1 = g.off[i + 1];
+    if (a0 + m0 >= a1) return;
+    G_STAMP_START(g, L, i, m0, n0, a1 - a0);
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
+    const int nkb = (int)(g.K / GBK);
+    GU2Src src;
+    src.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.xq), (short)0, 0x7fff0000, G_BUF_FLAGS);
+    src.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0,
+                                               (int)(max(g.w_off, g.w2_off) + g.N * g.K), G_BUF_FLAGS);
+    src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
+    // load j of the A tile covers positions (4 wave + j) 64 + lane, of each weight tile
+    // (2 wave + j) 64 + lane: chunk c of tile row r
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int r, c;
+        pos_chunk((4 * wave + j) * 64 + lane, r, c);
+        const int a = a0 + m0 + r;
+        src.xo[j] = a < a1 ? (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int r, c;
+        pos_chunk((2 * wave + j) * 64 + lane, r, c);
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+            src.wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r) * g.K) + 16 * c;
+    }
+    src.so = lane < 2 ? (int)((lane == 0 ? g.s_off : g.s2_off) + (int64_t)(n0 / 128) * nkb * 4) : G_OOB;
+    const bool act = __builtin_amdgcn_readfirstlane(a1 - (a0 + m0) - 64 * wm > 0);  // the wave holds assignments
+    float acc[2][4][4][4];
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int ms = 0; ms < 4; ms++)
+#pragma unroll
+            for (int ns = 0; ns < 4; ns++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = 0.0f;
+#define GU2_STEP(SB, NSB)                                               \
+    {                                                                   \
+        wait_vm<0>();                                                   \
+        g_barrier();                                                    \
+        gu2_issue(src, kb + 1, nkb, NSB, wave);                         \
+        if (act) gu2_step(SB, wm, wn, wave, lane, acc);                 \
+        if (++kb == nkb) break;                                         \
+    }
+    int kb = 0;
+    gu2_issue(src, 0, nkb, sb0, wave);
+    for (;;) {
+        GU2_STEP(sb0, sb1)
+        GU2_STEP(sb1, sb0)
+    }
+#undef GU2_STEP
+    wait_vm<0>();  // the zero-filled stage past the end has landed before the block ends
+    // h = silu(xs g) * (xs u) as two bf16 terms: hi = bf16(h), lo = bf16(h - hi)
+#pragma unroll
+    for (int ms = 0; ms < 4; ms++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int a = a0 + m0 + 64 * wm + 16 * ms + 4 * (lane >> 4) + e;
+            if (a >= a1) continue;
+            const float xsr = g.xs[g.rows ? g.rows[a] : a];
+#pragma unroll
+            for (int ns = 0; ns < 4; ns++) {
+                const float h = siluf(acc[0][ms][ns][e] * xsr) * (acc[1][ms][ns][e] * xsr);
+                const uint16_t hi = f32_to_bf16(h);
+                const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
+                g.hh[(int64_t)a * g.N + n] = hi;
+                if (g.hl) g.hl[(int64_t)a * g.N + n] = f32_to_bf16(h - bf16_to_f32(hi));
+            }
+        }
+    G_STAMP_END(g, L);
+}
+
 // ---- down pass over h as one or two bf16 terms ----------------------------------------
 //
 // y[a, r] = sum_kb ws(r, kb) * sum_{c in kb} (hi[a, c] (+ lo[a, c])) * e4m3(W[r, c]) for the
@@ -779,6 +938,11 @@ int launch_grouped(const GArgs& a, int mode, dim3 grid, hipStream_t st) {
     return launched("grouped_gemm_fp8");
 }
 
+int launch_grouped_gate_up256(const GArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL(grouped_gate_up256_kernel, grid, dim3(GTHREADS), 0, st, a);
+    return launched("grouped_gate_up_fp8");
+}
+
 int launch_grouped_down(const GArgs& a, int terms, dim3 grid, hipStream_t st) {
     if (terms == 2) hipLaunchKernelGGL(grouped_down_wide_kernel<2>, grid, dim3(GTHREADS), 0, st, a);
     else hipLaunchKernelGGL(grouped_down_wide_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
@@ -801,8 +965,9 @@ int launch_quant_rows(const void* x, int xdt, int64_t rows, int64_t cols, uint8_
     return launched("quantize_rows_fp8");
 }
 
-int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, int32_t* tiles, int32_t* ntiles, hipStream_t st) {
-    hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(1024), 0, st, n_e, off, tiles, ntiles);
+int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, int tile_rows, int32_t* tiles, int32_t* ntiles,
+                         hipStream_t st) {
+    hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(1024), 0, st, n_e, off, tile_rows, tiles, ntiles);
     return launched("grouped_tiles");
 }
 
@@ -815,11 +980,13 @@ int launch_combine(const float* y, const int32_t* slot, const float* w, void* ou
                    hipStream_t st);
 int check_geo(const OomFp8Record* g, const char* who);
 
-// Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | hh | hl | y (hh and hl:
-// the bf16 hi and lo terms of h [A, inter]; hl is written for the exact precision only).
+// Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | tiles2 | hh | hl | y
+// (tiles: the 128-row tile table of the down pass, tiles2: the 256-row one of gate/up; hh
+// and hl: the bf16 hi and lo terms of h [A, inter]; hl is written for the exact precision
+// only).
 struct PrefillWs {
-    size_t plan, recs, xq, xs, tiles, hh, hl, y, total;
-    int max_tiles;
+    size_t plan, recs, xq, xs, tiles, tiles2, hh, hl, y, total;
+    int max_tiles, max_tiles2;
 };
 
 static size_t p_al256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -828,12 +995,14 @@ static PrefillWs prefill_ws(int T, int E, int k, const OomFp8Record& g) {
     PrefillWs w;
     const size_t A = (size_t)T * k, H = (size_t)g.hidden, I = (size_t)g.inter;
     w.max_tiles = (int)(cdiv((int64_t)A, GBM) + std::min<int64_t>(E, (int64_t)A));
+    w.max_tiles2 = (int)(cdiv((int64_t)A, GBM2) + std::min<int64_t>(E, (int64_t)A));
     w.plan = 0;
     w.recs = p_al256(PlanView::size(E, (int)A) * sizeof(int32_t));
     w.xq = w.recs + p_al256((size_t)std::min<size_t>(E, A) * sizeof(uint64_t));
     w.xs = w.xq + p_al256((size_t)T * H);
     w.tiles = w.xs + p_al256((size_t)T * sizeof(float));
-    w.hh = w.tiles + p_al256((2 * (size_t)w.max_tiles + 1) * sizeof(int32_t));
+    w.tiles2 = w.tiles + p_al256((2 * (size_t)w.max_tiles + 1) * sizeof(int32_t));
+    w.hh = w.tiles2 + p_al256((2 * (size_t)w.max_tiles2 + 1) * sizeof(int32_t));
     w.hl = w.hh + p_al256(A * I * sizeof(uint16_t));
     w.y = w.hl + p_al256(A * I * sizeof(uint16_t));
     w.total = w.y + p_al256(A * H * sizeof(float));
@@ -916,6 +1085,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     float* xs = reinterpret_cast<float*>(base + w.xs);
     int32_t* tiles = reinterpret_cast<int32_t*>(base + w.tiles);
     int32_t* ntiles = tiles + 2 * w.max_tiles;
+    int32_t* tiles2 = reinterpret_cast<int32_t*>(base + w.tiles2);
+    int32_t* ntiles2 = tiles2 + 2 * w.max_tiles2;
     uint16_t* hh = reinterpret_cast<uint16_t*>(base + w.hh);
     uint16_t* hl = reinterpret_cast<uint16_t*>(base + w.hl);
     float* y = reinterpret_cast<float*>(base + w.y);
@@ -925,13 +1096,14 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     if (int rc = oom_router_topk(logits, ids, weights, T, E, k, stream)) return rc;
     if (int rc = oom_moe_plan(ids, T, E, k, all_recs, plan, recs, stream)) return rc;
     if (int rc = launch_quant_rows(x, x_dtype, T, geo->hidden, xq, xs, st)) return rc;
-    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), tiles, ntiles, st)) return rc;
+    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM, tiles, ntiles, st)) return rc;
+    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM2, tiles2, ntiles2, st)) return rc;
     GArgs a{};
     a.recs = recs;
     a.off = pv.off();
     a.rows = pv.assign_tok();
-    a.tiles = tiles;
-    a.ntiles = ntiles;
+    a.tiles = tiles2;
+    a.ntiles = ntiles2;
     a.xq = xq;
     a.xs = xs;
     a.x_group = 0;
@@ -947,7 +1119,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     a.stamps = stamps_buffer();
 #endif
     // 8 spare rows of blocks: the XCD-run order needs the grid to cover 8 ceil(W / 8) slots
-    if (int rc = launch_grouped(a, 1, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles + 8, 1), st)) return rc;
+    if (int rc = launch_grouped_gate_up256(a, dim3((unsigned)(geo->inter / GBN), (unsigned)w.max_tiles2 + 8, 1), st))
+        return rc;
     GArgs d{};
     d.recs = recs;
     d.off = pv.off();
@@ -962,7 +1135,7 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     d.y = y;
 #ifdef OOM_STAMPS
     // the down pass's blocks after the gate/up grid's
-    d.stamps = a.stamps ? a.stamps + 4 * (size_t)(geo->inter / GBN) * (w.max_tiles + 8) : nullptr;
+    d.stamps = a.stamps ? a.stamps + 4 * (size_t)(geo->inter / GBN) * (w.max_tiles2 + 8) : nullptr;
 #endif
     const int terms = precision == OOM_EXPERT_EXACT ? 2 : 1;
     if (int rc = launch_grouped_down(d, terms, dim3((unsigned)cdiv(geo->hidden, GBNW), (unsigned)w.max_tiles + 8, 1),

@@ -126,12 +126,14 @@ def prefill_workspace(ws, T, E, k, H, I):
     def al(v):
         return (v + 255) // 256 * 256
     A = T * k
-    max_tiles = (A + 127) // 128 + min(E, A)
+    max_tiles = (A + 127) // 128 + min(E, A)     # 128-row tiles (down)
+    max_tiles2 = (A + 255) // 256 + min(E, A)    # 256-row tiles (gate/up)
     o_recs = al((2 + 2 * E + 2 * A) * 4)
     o_xq = o_recs + al(min(E, A) * 8)
     o_xs = o_xq + al(T * H)
     o_tiles = o_xs + al(T * 4)
-    o_hh = o_tiles + al((2 * max_tiles + 1) * 4)
+    o_tiles2 = o_tiles + al((2 * max_tiles + 1) * 4)
+    o_hh = o_tiles2 + al((2 * max_tiles2 + 1) * 4)
     o_hl = o_hh + al(A * I * 2)
     W = ws.cpu().numpy()
     plan = W[:(2 + 2 * E + 2 * A) * 4].view(np.int32)
