@@ -533,14 +533,24 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
 // step kb runs on the matrix cores while kb + 1 loads. Per-row activation scales only
 // (x_group 0, the prefill's quantiser). Tiles come from a table of 256-row tiles, in the
 // XCD runs of grouped_gemm_kernel.
+//
+// A tile of at most 32 assignments (a light expert, or a heavy expert's last rows) is a
+// stream of its weight slab: its step time is the latency of a stage, whatever the stage
+// holds. Its stages hold two K steps each (two 36 KiB halves: the 32-row activation tile
+// and both weight tiles of a K step), so 64 KiB of weights are in flight instead of 32.
 constexpr int GBM2 = 256;                                 // assignments per block tile
 constexpr int GU2_SB = GBM2 * GBK + 2 * GBN * GBK;        // stage operands: A, gate, up tiles
-constexpr int GU2_STOT = GU2_SB + GTHREADS * 4;           // + the weight scales, 64 words a wave
+constexpr int GU2_LROWS = 32;                             // assignments of a two-step (light) tile
+constexpr int GU2_LA = GU2_LROWS * GBK;                   // its activation tile, one K step
+constexpr int GU2_LHALF = GU2_LA + 2 * GBN * GBK;         // one K step of a light stage
+constexpr int GU2_SCALES = GU2_SB > 2 * GU2_LHALF ? GU2_SB : 2 * GU2_LHALF;  // the scale words
+constexpr int GU2_STOT = GU2_SCALES + GTHREADS * 4;       // + 64 words a wave
 
 struct GU2Src {
     __amdgpu_buffer_rsrc_t xr, wr, sr;
     int xo[4], wo[2][2];  // step-0 byte offsets (xo < 0: a row past the expert, loads zeros)
     int so;               // step-0 byte offset of this lane's weight block scale (G_OOB: none)
+    int lxo, lso;         // the light stages' activation chunk and scale (wave / 4: which K step)
 };
 
 __device__ __forceinline__ void gu2_issue(const GU2Src& s, int kb, int nkb, uint8_t* sb, int wave) {
@@ -553,23 +563,41 @@ __device__ __forceinline__ void gu2_issue(const GU2Src& s, int kb, int nkb, uint
 #pragma unroll
         for (int j = 0; j < 2; j++)
             dma16(s.wr, sb + GBM2 * GBK + m * GBN * GBK + (2 * wave + j) * 1024, ok ? s.wo[m][j] + k0 : G_OOB);
-    dma4(s.sr, reinterpret_cast<float*>(sb + GU2_SB) + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * kb : G_OOB);
+    dma4(s.sr, reinterpret_cast<float*>(sb + GU2_SCALES) + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * kb : G_OOB);
 }
 
-// One K step: acc[m][ms][ns] += ws(m) * (block sum of M subtile ms and N subtile ns of
-// weight matrix m). A wave with any assignment runs all 4 M subtiles (rows past the expert
-// hold zeros and are not stored): per-subtile branches cost more registers than the
-// matrix work they save on partial tiles.
-__device__ __forceinline__ void gu2_step(const uint8_t* sb, int wm, int wn, int wave, int lane,
-                                         float (&acc)[2][4][4][4]) {
-    const float* scw = reinterpret_cast<const float*>(sb + GU2_SB) + 64 * wave;
-    const float ws[2] = {scw[0], scw[1]};
-    gi32x8 aop[4];
+// A light stage: K steps kb and kb + 1 (kb even, K steps even in number). Waves 0-3 load
+// the first step's 32-row activation tile, waves 4-7 the second's; every wave loads its
+// chunks of both steps' weight tiles; lanes 0-3 the block scales (gate kb, up kb, gate
+// kb + 1, up kb + 1).
+__device__ __forceinline__ void gu2_issue_light(const GU2Src& s, int kb, int nkb, uint8_t* sb, int wave) {
+    const bool ok = kb < nkb;
+    const int k0 = kb * GBK;
+    dma16(s.xr, sb + (wave >> 2) * GU2_LHALF + (wave & 3) * 1024, ok && s.lxo >= 0 ? s.lxo + k0 : G_OOB);
 #pragma unroll
-    for (int ms = 0; ms < 4; ms++) aop[ms] = gop(sb, 64 * wm + 16 * ms + (lane & 15), lane);
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                dma16(s.wr, sb + h * GU2_LHALF + GU2_LA + m * GBN * GBK + (2 * wave + j) * 1024,
+                      ok ? s.wo[m][j] + k0 + h * GBK : G_OOB);
+    dma4(s.sr, reinterpret_cast<float*>(sb + GU2_SCALES) + 64 * wave, ok && s.lso != G_OOB ? s.lso + 4 * kb : G_OOB);
+}
+
+// One K step: acc[m][ms][ns] += ws[m] * (block sum of M subtile ms and N subtile ns of
+// weight matrix m), over the activation tile `at` and the weight tiles at `bt`. A wave with
+// any assignment runs MS M subtiles (rows past the expert hold zeros and are not stored):
+// per-subtile branches cost more registers than the matrix work they save.
+template <int MS>
+__device__ __forceinline__ void gu2_step(const uint8_t* at, const uint8_t* bt, const float* ws, int wm, int wn,
+                                         int lane, float (&acc)[2][4][4][4]) {
+    const float wsc[2] = {ws[0], ws[1]};
+    gi32x8 aop[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) aop[ms] = gop(at, 64 * wm + 16 * ms + (lane & 15), lane);
     // the 8 B operands (gate subtiles, then up) one read ahead of their products: holding
     // all of them beside the 128 accumulators spills
-    const uint8_t* bt = sb + GBM2 * GBK;
     const int brow = 64 * wn + (lane & 15);
     gi32x8 bcur = gop(bt, brow, lane);
 #pragma unroll
@@ -578,11 +606,11 @@ __device__ __forceinline__ void gu2_step(const uint8_t* sb, int wm, int wn, int 
         gi32x8 bnext = bcur;
         if (q < 7) bnext = gop(bt + ((q + 1) >> 2) * GBN * GBK, brow + 16 * ((q + 1) & 3), lane);
 #pragma unroll
-        for (int ms = 0; ms < 4; ms++) {
+        for (int ms = 0; ms < MS; ms++) {
             const gf32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
             const gf32x4 blk = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop[ms], bcur, z, 0, 0, 0, 127, 0, 127);
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = fmaf(blk[e], ws[m], acc[m][ms][ns][e]);
+            for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = fmaf(blk[e], wsc[m], acc[m][ms][ns][e]);
         }
         __builtin_amdgcn_sched_barrier(0);
         bcur = bnext;
@@ -631,6 +659,18 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
             src.wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r) * g.K) + 16 * c;
     }
     src.so = lane < 2 ? (int)((lane == 0 ? g.s_off : g.s2_off) + (int64_t)(n0 / 128) * nkb * 4) : G_OOB;
+    const bool light = a1 - (a0 + m0) <= GU2_LROWS && (nkb & 1) == 0;
+    {
+        // light stages: activation chunk (wave % 4) 64 + lane of K step kb + wave / 4, and
+        // lane 2 h + m's block scale of matrix m at K step kb + h
+        int r, c;
+        pos_chunk((wave & 3) * 64 + lane, r, c);
+        const int a = a0 + m0 + r;
+        src.lxo = a < a1 ? (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c + (wave >> 2) * GBK : -1;
+        src.lso = lane < 4 ? (int)(((lane & 1) == 0 ? g.s_off : g.s2_off) + (int64_t)(n0 / 128) * nkb * 4) +
+                                 4 * (lane >> 1)
+                           : G_OOB;
+    }
     const bool act = __builtin_amdgcn_readfirstlane(a1 - (a0 + m0) - 64 * wm > 0);  // the wave holds assignments
     float acc[2][4][4][4];
 #pragma unroll
@@ -641,21 +681,44 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
             for (int ns = 0; ns < 4; ns++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = 0.0f;
-#define GU2_STEP(SB, NSB)                                               \
-    {                                                                   \
-        wait_vm<0>();                                                   \
-        g_barrier();                                                    \
-        gu2_issue(src, kb + 1, nkb, NSB, wave);                         \
-        if (act) gu2_step(SB, wm, wn, wave, lane, acc);                 \
-        if (++kb == nkb) break;                                         \
+#define GU2_SW(B) (reinterpret_cast<const float*>((B) + GU2_SCALES) + 64 * wave)
+#define GU2_STEP(SB, NSB)                                                                 \
+    {                                                                                     \
+        wait_vm<0>();                                                                     \
+        g_barrier();                                                                      \
+        gu2_issue(src, kb + 1, nkb, NSB, wave);                                           \
+        if (act) gu2_step<4>(SB, SB + GBM2 * GBK, GU2_SW(SB), wm, wn, lane, acc);         \
+        if (++kb == nkb) break;                                                           \
+    }
+#define GU2_LSTEP(SB, NSB)                                                                                     \
+    {                                                                                                          \
+        wait_vm<0>();                                                                                          \
+        g_barrier();                                                                                           \
+        gu2_issue_light(src, kb + 2, nkb, NSB, wave);                                                          \
+        if (act) {                                                                                             \
+            gu2_step<2>(SB, SB + GU2_LA, GU2_SW(SB), wm, wn, lane, acc);                                       \
+            gu2_step<2>(SB + GU2_LHALF, SB + GU2_LHALF + GU2_LA, GU2_SW(SB) + 2, wm, wn, lane, acc);           \
+        }                                                                                                      \
+        kb += 2;                                                                                               \
+        if (kb == nkb) break;                                                                                  \
     }
     int kb = 0;
-    gu2_issue(src, 0, nkb, sb0, wave);
-    for (;;) {
-        GU2_STEP(sb0, sb1)
-        GU2_STEP(sb1, sb0)
+    if (light) {
+        gu2_issue_light(src, 0, nkb, sb0, wave);
+        for (;;) {
+            GU2_LSTEP(sb0, sb1)
+            GU2_LSTEP(sb1, sb0)
+        }
+    } else {
+        gu2_issue(src, 0, nkb, sb0, wave);
+        for (;;) {
+            GU2_STEP(sb0, sb1)
+            GU2_STEP(sb1, sb0)
+        }
     }
 #undef GU2_STEP
+#undef GU2_LSTEP
+#undef GU2_SW
     wait_vm<0>();  // the zero-filled stage past the end has landed before the block ends
     // h = silu(xs g) * (xs u) as two bf16 terms: hi = bf16(h), lo = bf16(h - hi)
 #pragma unroll

@@ -247,8 +247,12 @@ def prefill_check(hip, geo, recs, logits, xb, k, sample=None, precision=None):
 
 
 @pytest.mark.parametrize("prec", ["bf16", "exact"])
-@pytest.mark.parametrize("T,E,k,H,I", [(64, 16, 4, 512, 256), (7, 8, 2, 256, 128), (300, 32, 8, 1024, 384)])
+@pytest.mark.parametrize("T,E,k,H,I", [(64, 16, 4, 512, 256), (7, 8, 2, 256, 128), (300, 32, 8, 1024, 384),
+                                       (40, 8, 4, 384, 256)])
 def test_prefill_small(hip, T, E, k, H, I, prec):
+    """Small steps against the oracle. Hidden 384 (three K steps, an odd count) keeps the
+    gate/up pass's tiles of at most 32 assignments on single-step stages; the others take
+    two K steps a stage for them."""
     print(f"prefill T={T} E={E} k={k} H={H} I={I} precision={prec}", flush=True)
     geo = oracle.record_geometry(H, I)
     logits = synth.decode_logits(77 + T, T, E, 1.1)
