@@ -772,16 +772,28 @@ constexpr int GBNW = 256;                      // outputs per block tile
 constexpr int DW_WT = GBNW * GBK2;             // bytes of the weight tile
 template <int TERMS>
 constexpr int dw_sbytes() { return TERMS * D_HT + DW_WT; }
+// A tile of at most 32 assignments streams the weights: its stages hold two K steps (one
+// 128-column scale block), each half the 32-row h term tiles and the weight tile of one K
+// step, so four K steps of weights are in flight instead of two.
+constexpr int DL_ROWS = 32;
+constexpr int DL_HT = DL_ROWS * GBK2 * 2;      // bytes of one light h term tile
 template <int TERMS>
-constexpr int dw_stot() { return dw_sbytes<TERMS>() + GTHREADS * 4; }
+constexpr int dl_half() { return TERMS * DL_HT + DW_WT; }
+template <int TERMS>
+constexpr int dw_scales() { return dw_sbytes<TERMS>() > 2 * dl_half<TERMS>() ? dw_sbytes<TERMS>() : 2 * dl_half<TERMS>(); }
+template <int TERMS>
+constexpr int dw_stot() { return dw_scales<TERMS>() + GTHREADS * 4; }
 template <int TERMS>
 constexpr int dw_lps() { return 2 * TERMS + 2 + 1; }
+template <int TERMS>
+constexpr int dl_lps() { return (TERMS == 2 ? 2 : 1) + 4 + 1; }
 
 struct DWSrc {
     __amdgpu_buffer_rsrc_t hr, wr, sr;
     int ho[2], wo[2];  // step-0 byte offsets (ho < 0: a row past the expert, loads zeros)
     int hl_off;
     int so;
+    int lho;           // light stages: this wave's h chunk at K step 0 (< 0: past the expert)
 };
 
 template <int TERMS>
@@ -800,18 +812,78 @@ __device__ __forceinline__ void dw_issue(const DWSrc& s, int kb, int nkb, uint8_
     dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
 }
 
-// A: h term t, row half hf of M subtile ms (+2048 bytes; t: +D_HT); B: weight rows of N subtile ns
-// (+1024 bytes each, 8 of them); then this wave's weight block scale.
+// A light stage: K steps kb and kb + 1 (kb even). TERMS 2: wave w loads h term w / 4 of
+// both halves; TERMS 1: wave w loads the h tile of half w / 4. Every wave loads its chunks
+// of both halves' weight tiles, lane 0 the block scale.
 template <int TERMS>
-__device__ __forceinline__ void dw_reads(const uint8_t* sb, int wm, int wn, int wave, int lane,
-                                         uint4 (&ra)[2][TERMS][2], uint4 (&rb)[8], float& ws) {
-    typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
-    const uint32_t base = (uint32_t)(uintptr_t)(lds_cptr)sb;
-    const int g = lane >> 4, row = 32 * wm + (lane & 15), wrow = 128 * wn + (lane & 15);
-    const uint32_t a0 = base + 16 * chunk_pos(row, 2 * g), a1 = base + 16 * chunk_pos(row, 2 * g + 1);
-    const uint32_t bb = base + TERMS * D_HT + 16 * wchunk_pos(wrow, g);
-    const uint32_t sc = base + dw_sbytes<TERMS>() + 4 * 64 * wave;
+__device__ __forceinline__ void dw_issue_light(const DWSrc& s, int kb, int nkb, uint8_t* sb, float* scw, int wave) {
+    const bool ok = kb < nkb;
+    const int k0 = kb * GBK2 * 2;
     if constexpr (TERMS == 2) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            dma16(s.hr, sb + h * dl_half<TERMS>() + (wave >> 2) * DL_HT + (wave & 3) * 1024,
+                  ok && s.lho >= 0 ? s.lho + k0 + h * GBK2 * 2 : G_OOB);
+    } else {
+        dma16(s.hr, sb + (wave >> 2) * dl_half<TERMS>() + (wave & 3) * 1024, ok && s.lho >= 0 ? s.lho + k0 : G_OOB);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            dma16(s.wr, sb + h * dl_half<TERMS>() + TERMS * DL_HT + (2 * wave + j) * 1024,
+                  ok ? s.wo[j] + (kb + h) * GBK2 : G_OOB);
+    dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
+}
+
+// A: h term t, row half hf of M subtile ms (+2048 bytes; t: +the term tile's size); B: weight
+// rows of N subtile ns (+1024 bytes each: 8 of them, or the light layout's 2); then this
+// wave's weight block scale. ab: the term-0 h tile, bt: the wave's first weight row's chunks,
+// scw: the stage's scale words. row0: the wave's first h row; wrow0: its first weight row.
+template <int TERMS, bool LIGHT>
+__device__ __forceinline__ void dw_reads(const uint8_t* ab, const uint8_t* bt, const uint8_t* scw, int row0, int wrow0,
+                                         int wave, int lane, uint4 (&ra)[2][TERMS][2], uint4 (&rb)[8], float& ws) {
+    typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
+    const uint32_t base = (uint32_t)(uintptr_t)(lds_cptr)ab;
+    const int g = lane >> 4, row = row0 + (lane & 15), wrow = wrow0 + (lane & 15);
+    const uint32_t a0 = base + 16 * chunk_pos(row, 2 * g), a1 = base + 16 * chunk_pos(row, 2 * g + 1);
+    const uint32_t bb = (uint32_t)(uintptr_t)(lds_cptr)bt + 16 * wchunk_pos(wrow, g);
+    const uint32_t sc = (uint32_t)(uintptr_t)(lds_cptr)scw + 4 * 64 * wave;
+    if constexpr (TERMS == 2 && LIGHT) {
+        static_assert(DL_HT == 4096, "light term offsets");
+        asm volatile(
+            "ds_read_b128 %0, %11\n\t"
+            "ds_read_b128 %1, %12\n\t"
+            "ds_read_b128 %2, %11 offset:2048\n\t"
+            "ds_read_b128 %3, %12 offset:2048\n\t"
+            "ds_read_b128 %4, %11 offset:4096\n\t"
+            "ds_read_b128 %5, %12 offset:4096\n\t"
+            "ds_read_b128 %6, %11 offset:6144\n\t"
+            "ds_read_b128 %7, %12 offset:6144\n\t"
+            "ds_read_b128 %8, %13\n\t"
+            "ds_read_b128 %9, %13 offset:1024\n\t"
+            "ds_read_b32 %10, %14\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(ra[0][1][0]),
+              "=&v"(ra[0][1][1]), "=&v"(ra[1][1][0]), "=&v"(ra[1][1][1]), "=&v"(rb[0]), "=&v"(rb[1]), "=&v"(ws)
+            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
+            : "memory");
+    } else if constexpr (LIGHT) {
+        asm volatile(
+            "ds_read_b128 %0, %7\n\t"
+            "ds_read_b128 %1, %8\n\t"
+            "ds_read_b128 %2, %7 offset:2048\n\t"
+            "ds_read_b128 %3, %8 offset:2048\n\t"
+            "ds_read_b128 %4, %9\n\t"
+            "ds_read_b128 %5, %9 offset:1024\n\t"
+            "ds_read_b32 %6, %10\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(rb[0]), "=&v"(rb[1]),
+              "=&v"(ws)
+            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
+            : "memory");
+    } else if constexpr (TERMS == 2) {
+        static_assert(D_HT == 16384, "term offsets");
         asm volatile(
             "ds_read_b128 %0, %17\n\t"
             "ds_read_b128 %1, %18\n\t"
@@ -861,14 +933,18 @@ __device__ __forceinline__ void dw_reads(const uint8_t* sb, int wm, int wn, int 
 
 // act: this wave's 16-row M subtiles that hold assignments (1 or 2; a subtile past the
 // expert's last assignment holds zeros, and its products are not stored).
-template <int TERMS>
-__device__ __forceinline__ void dw_step(const uint8_t* sb, int wm, int wn, int wave, int lane, bool fold, int act,
-                                        gf32x4 (&blk)[2][8], float (&acc)[2][8][4]) {
+// LIGHT: the wave's 2 N subtiles (32 weight rows) over the tile's at most 32 h rows;
+// otherwise its 8 N subtiles (128 rows) over its 32 h rows.
+template <int TERMS, bool LIGHT>
+__device__ __forceinline__ void dw_step(const uint8_t* ab, const uint8_t* bt, const uint8_t* scw, int row0, int wrow0,
+                                        int wave, int lane, bool fold, int act, gf32x4 (&blk)[2][8],
+                                        float (&acc)[2][8][4]) {
+    constexpr int NS = LIGHT ? 2 : 8;
     uint4 ra[2][TERMS][2], rb[8];
     float ws;
-    dw_reads<TERMS>(sb, wm, wn, wave, lane, ra, rb, ws);
+    dw_reads<TERMS, LIGHT>(ab, bt, scw, row0, wrow0, wave, lane, ra, rb, ws);
 #pragma unroll
-    for (int ns = 0; ns < 8; ns++) {
+    for (int ns = 0; ns < NS; ns++) {
         const uint32_t ww[4] = {rb[ns].x, rb[ns].y, rb[ns].z, rb[ns].w};
         gbf16x8 b[2];
 #pragma unroll
@@ -896,7 +972,7 @@ __device__ __forceinline__ void dw_step(const uint8_t* sb, int wm, int wn, int w
 #pragma unroll
         for (int ms = 0; ms < 2; ms++)
 #pragma unroll
-            for (int ns = 0; ns < 8; ns++) {
+            for (int ns = 0; ns < NS; ns++) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[ms][ns][e] = fmaf(blk[ms][ns][e], ws, acc[ms][ns][e]);
                 blk[ms][ns] = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -904,24 +980,25 @@ __device__ __forceinline__ void dw_step(const uint8_t* sb, int wm, int wn, int w
     }
 }
 
-// Tiles from the device tile table in XCD runs, as grouped_gemm_kernel, but with the N-tile
-// fastest: the blocks an XCD runs together take the N-tiles of one M-tile, so that tile's h
-// planes come into the XCD's L2 once and serve all of them. (M-tile fastest re-fetched every
+// Tiles from the device tile table: each XCD takes whole M-tiles with the N-tile fastest, so
+// the blocks an XCD runs together take the N-tiles of one M-tile, and that tile's h planes
+// come into the XCD's L2 once and serve all of them. (M-tile fastest re-fetched every
 // M-tile's h from beyond the L2 for each N-tile: 3.2 GB a 2048-token step with two terms.)
 // Outputs past N (hidden not a multiple of 256) read zero weights and are not stored.
 template <int TERMS>
 __global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
-    constexpr int STOT = dw_stot<TERMS>(), SBYTES = dw_sbytes<TERMS>();
+    constexpr int STOT = dw_stot<TERMS>(), SCB = dw_scales<TERMS>();
     __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT], sb2[STOT];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int NT = (int)gridDim.x, MT = *g.ntiles, W = NT * MT;
-    const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), C = (W + 7) / 8;
-    if ((L >> 3) >= C) return;
-    const int w = (L & 7) * C + (L >> 3);
-    if (w >= W) return;
-    const int mt = w / NT, nt = w - mt * NT;
+    // block L runs on XCD L % 8 as its item q = L / 8: M-tile 8 (q / NT) + L % 8, N-tile
+    // q % NT (M-tiles dealt to the XCDs in turn, so each XCD gets its share of heavy and
+    // light tiles)
+    const int NT = (int)gridDim.x, MT = *g.ntiles;
+    const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), q = L >> 3;
+    const int mt = 8 * (q / NT) + (L & 7), nt = q % NT;
+    if (mt >= MT) return;
     const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBNW;
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
@@ -944,10 +1021,25 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
         src.wo[j] = (int)(g.w_off + (int64_t)(n0 + wr) * g.K) + 16 * wc;
     }
     src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
-    const int nw0 = n0 + 128 * wn;  // this wave's first output (its 128-row scale block)
-    const int left = a1 - (a0 + m0) - 32 * wm;  // assignments from this wave's first row on
+    // a light tile (at most 32 assignments; K steps come in pairs, K being a multiple of
+    // 128): wave w takes weight rows 32 w .. + 32 over all the tile's h rows; otherwise wave
+    // (wm, wn) takes h rows 32 wm .. + 32 and weight rows 128 wn .. + 128
+    const int rows = a1 - (a0 + m0);
+    const bool light = rows <= DL_ROWS;
+    const int row0 = light ? 0 : 32 * wm, wrow0 = light ? 32 * wave : 128 * wn;
+    const int nw0 = n0 + wrow0;  // this wave's first output (inside one 128-row scale block)
+    const int left = rows - row0;  // assignments from this wave's first row on
     const int act = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : left <= 16 ? 1 : 2);
     src.so = lane == 0 && nw0 < g.N ? (int)(g.s_off + (int64_t)(nw0 / 128) * (g.K / 128) * 4) : G_OOB;
+    // light stages: h chunk (wave % 4) 64 + lane of term wave / 4 (TERMS 2) or of K step
+    // wave / 4 (TERMS 1)
+    {
+        int r, c;
+        pos_chunk((wave & 3) * 64 + lane, r, c);
+        const int a = a0 + m0 + r;
+        src.lho = a < a1 ? (int)(a * g.K * 2) + 16 * c + (TERMS == 2 ? (wave >> 2) * src.hl_off : (wave >> 2) * GBK2 * 2)
+                         : -1;
+    }
     float acc[2][8][4];
     gf32x4 blk[2][8];
 #pragma unroll
@@ -958,36 +1050,64 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[ms][ns][e] = 0.0f;
         }
-#define DW_SW(B) reinterpret_cast<float*>((B) + SBYTES)
-#define DW_STEP(SB, NSB)                                                                                 \
-    {                                                                                                    \
-        wait_vm<dw_lps<TERMS>()>();                                                                      \
-        g_barrier();                                                                                     \
-        dw_issue<TERMS>(src, kb + 2, nkb, NSB, DW_SW(NSB), wave);                                        \
-        if (act > 0) dw_step<TERMS>(SB, wm, wn, wave, lane, (kb & 1) || kb + 1 == nkb, act, blk, acc);   \
-        if (++kb == nkb) break;                                                                          \
+#define DW_SW(B) reinterpret_cast<float*>((B) + SCB)
+#define DW_STEP(SB, NSB)                                                                                   \
+    {                                                                                                      \
+        wait_vm<dw_lps<TERMS>()>();                                                                        \
+        g_barrier();                                                                                       \
+        dw_issue<TERMS>(src, kb + 2, nkb, NSB, DW_SW(NSB), wave);                                          \
+        if (act > 0)                                                                                       \
+            dw_step<TERMS, false>(SB, SB + TERMS * D_HT, SB + SCB, row0, wrow0, wave, lane,                \
+                                  (kb & 1) || kb + 1 == nkb, act, blk, acc);                               \
+        if (++kb == nkb) break;                                                                            \
+    }
+#define DW_LSTEP(SB, NSB)                                                                                  \
+    {                                                                                                      \
+        wait_vm<dl_lps<TERMS>()>();                                                                        \
+        g_barrier();                                                                                       \
+        dw_issue_light<TERMS>(src, kb + 4, nkb, NSB, DW_SW(NSB), wave);                                    \
+        if (act > 0) {                                                                                     \
+            dw_step<TERMS, true>(SB, SB + TERMS * DL_HT, SB + SCB, row0, wrow0, wave, lane, false, act, blk, \
+                                 acc);                                                                     \
+            dw_step<TERMS, true>(SB + dl_half<TERMS>(), SB + dl_half<TERMS>() + TERMS * DL_HT, SB + SCB, row0, \
+                                 wrow0, wave, lane, true, act, blk, acc);                                  \
+        }                                                                                                  \
+        kb += 2;                                                                                           \
+        if (kb == nkb) break;                                                                              \
     }
     int kb = 0;
-    dw_issue<TERMS>(src, 0, nkb, sb0, DW_SW(sb0), wave);
-    dw_issue<TERMS>(src, 1, nkb, sb1, DW_SW(sb1), wave);
-    for (;;) {
-        DW_STEP(sb0, sb2)
-        DW_STEP(sb1, sb0)
-        DW_STEP(sb2, sb1)
+    if (light) {
+        dw_issue_light<TERMS>(src, 0, nkb, sb0, DW_SW(sb0), wave);
+        dw_issue_light<TERMS>(src, 2, nkb, sb1, DW_SW(sb1), wave);
+        for (;;) {
+            DW_LSTEP(sb0, sb2)
+            DW_LSTEP(sb1, sb0)
+            DW_LSTEP(sb2, sb1)
+        }
+    } else {
+        dw_issue<TERMS>(src, 0, nkb, sb0, DW_SW(sb0), wave);
+        dw_issue<TERMS>(src, 1, nkb, sb1, DW_SW(sb1), wave);
+        for (;;) {
+            DW_STEP(sb0, sb2)
+            DW_STEP(sb1, sb0)
+            DW_STEP(sb2, sb1)
+        }
     }
 #undef DW_SW
 #undef DW_STEP
+#undef DW_LSTEP
     wait_vm<0>();  // the zero-filled stages past the end have landed before the block ends
+    const int nsw = light ? 2 : 8;  // the wave's N subtiles
 #pragma unroll
     for (int ms = 0; ms < 2; ms++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int a = a0 + m0 + 32 * wm + 16 * ms + 4 * (lane >> 4) + e;
+            const int a = a0 + m0 + row0 + 16 * ms + 4 * (lane >> 4) + e;
             if (a >= a1) continue;
 #pragma unroll
             for (int ns = 0; ns < 8; ns++) {
                 const int64_t n = nw0 + 16 * ns + (lane & 15);
-                if (n < g.N) g.y[(int64_t)a * g.N + n] = acc[ms][ns][e];
+                if (ns < nsw && n < g.N) g.y[(int64_t)a * g.N + n] = acc[ms][ns][e];
             }
         }
     G_STAMP_END(g, L);
