@@ -179,18 +179,28 @@ __global__ void __launch_bounds__(256) quant_rows_vec_kernel(const void* __restr
 }
 
 // ---- the tile table of a device plan: tile mt = (expert i, assignments from off[i] + m0).
-// One block of 1024 threads; experts in chunks of 1024 with a running carry.
+// One block of 1024 threads; experts in chunks of 1024 with a running carry. With
+// light_rows > 0 the table lists the tiles of more than light_rows assignments first and
+// then the others (each expert's last tile when it holds at most light_rows), so the
+// blocks that take tiles in table order start the long ones first.
 __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __restrict__ n_e_p,
                                                              const int32_t* __restrict__ off, int tile_rows,
-                                                             int32_t* __restrict__ tiles, int32_t* __restrict__ ntiles) {
+                                                             int light_rows, int32_t* __restrict__ tiles,
+                                                             int32_t* __restrict__ ntiles) {
     __shared__ int wsum[16];
     __shared__ int carry_s;
     const int n_e = *n_e_p, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) carry_s = 0;
     __syncthreads();
+    for (int pass = 0; pass < (light_rows > 0 ? 2 : 1); pass++)
     for (int c0 = 0; c0 < n_e; c0 += (int)blockDim.x) {
         const int i = c0 + tid;
-        const int cnt = i < n_e ? (off[i + 1] - off[i] + tile_rows - 1) / tile_rows : 0;
+        const int n = i < n_e ? off[i + 1] - off[i] : 0, full = n / tile_rows, rem = n - full * tile_rows;
+        // pass 0: every tile, or (light_rows > 0) all but a last tile of at most light_rows;
+        // pass 1: that last tile
+        const bool last_light = light_rows > 0 && rem > 0 && rem <= light_rows;
+        const int cnt = pass == 0 ? full + (rem > 0 && !last_light ? 1 : 0) : (last_light ? 1 : 0);
+        const int t0 = pass == 0 ? 0 : full;
         // inclusive scan within the wave, then over the waves
         int incl = cnt;
 #pragma unroll
@@ -205,7 +215,7 @@ __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __re
         const int start = before + incl - cnt;
         for (int t = 0; t < cnt; t++) {
             tiles[2 * (start + t)] = i;
-            tiles[2 * (start + t) + 1] = t * tile_rows;
+            tiles[2 * (start + t) + 1] = (t0 + t) * tile_rows;
         }
         __syncthreads();
         if (tid == (int)blockDim.x - 1) carry_s = start + cnt;
@@ -531,8 +541,7 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
 // wave waits for its own loads of stage kb, the block synchronises (every wave's loads of
 // kb have landed, every wave is done reading the other buffer), stage kb + 1 is issued, and
 // step kb runs on the matrix cores while kb + 1 loads. Per-row activation scales only
-// (x_group 0, the prefill's quantiser). Tiles come from a table of 256-row tiles, in the
-// XCD runs of grouped_gemm_kernel.
+// (x_group 0, the prefill's quantiser). Tiles come from a table of 256-row tiles.
 //
 // A tile of at most 32 assignments (a light expert, or a heavy expert's last rows) is a
 // stream of its weight slab: its step time is the latency of a stage, whatever the stage
@@ -624,12 +633,13 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    const int NT = (int)gridDim.x, MT = *g.ntiles, W = NT * MT;
-    const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), C = (W + 7) / 8;
-    if ((L >> 3) >= C) return;
-    const int w = (L & 7) * C + (L >> 3);
-    if (w >= W) return;
-    const int nt = w / MT, mt = w - nt * MT;
+    // block L runs on XCD L % 8 as its item q = L / 8: tile 8 (q / NT) + L % 8, N-tile q % NT
+    // (tiles dealt to the XCDs in turn, so each XCD gets its share of heavy and light tiles;
+    // a tile's N-tiles run together and share its activation rows through that XCD's L2)
+    const int NT = (int)gridDim.x, MT = *g.ntiles;
+    const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), q = L >> 3;
+    const int mt = 8 * (q / NT) + (L & 7), nt = q % NT;
+    if (mt >= MT) return;
     const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBN;
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
@@ -1148,9 +1158,10 @@ int launch_quant_rows(const void* x, int xdt, int64_t rows, int64_t cols, uint8_
     return launched("quantize_rows_fp8");
 }
 
-int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, int tile_rows, int32_t* tiles, int32_t* ntiles,
-                         hipStream_t st) {
-    hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(1024), 0, st, n_e, off, tile_rows, tiles, ntiles);
+int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, int tile_rows, int light_rows, int32_t* tiles,
+                         int32_t* ntiles, hipStream_t st) {
+    hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(1024), 0, st, n_e, off, tile_rows, light_rows, tiles,
+                       ntiles);
     return launched("grouped_tiles");
 }
 
@@ -1279,8 +1290,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     if (int rc = oom_router_topk(logits, ids, weights, T, E, k, stream)) return rc;
     if (int rc = oom_moe_plan(ids, T, E, k, all_recs, plan, recs, stream)) return rc;
     if (int rc = launch_quant_rows(x, x_dtype, T, geo->hidden, xq, xs, st)) return rc;
-    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM, tiles, ntiles, st)) return rc;
-    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM2, tiles2, ntiles2, st)) return rc;
+    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM, 0, tiles, ntiles, st)) return rc;
+    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM2, 0, tiles2, ntiles2, st)) return rc;
     GArgs a{};
     a.recs = recs;
     a.off = pv.off();
