@@ -1291,7 +1291,7 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     if (int rc = oom_moe_plan(ids, T, E, k, all_recs, plan, recs, stream)) return rc;
     if (int rc = launch_quant_rows(x, x_dtype, T, geo->hidden, xq, xs, st)) return rc;
     if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM, 0, tiles, ntiles, st)) return rc;
-    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM2, 0, tiles2, ntiles2, st)) return rc;
+    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM2, GU2_LROWS, tiles2, ntiles2, st)) return rc;
     GArgs a{};
     a.recs = recs;
     a.off = pv.off();
