@@ -757,7 +757,7 @@ def bench_nvfp4_prefill(args):
         "roofline": ({"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                       "frac": tflops / PEAK_BF16_TFLOPS} if exact else
                      {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS})
-        | {"traffic": measured_traffic("nvfp4_prefill"), "kernel": "moe_tiled_nvfp4_kernel (three launches a step)",
+        | {"traffic": measured_traffic("nvfp4_prefill"), "kernel": "moe_tiled_nvfp4_wide_kernel (three launches a step)",
            "algorithmic_bytes_per_step": bytes_step, "matrix_flops_per_step": flops},
     }
     if not args.no_cpu:
