@@ -754,23 +754,19 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
 //
 // y[a, r] = sum_kb ws(r, kb) * sum_{c in kb} (hi[a, c] (+ lo[a, c])) * e4m3(W[r, c]) for the
 // assignments a of each expert (W = the down weights [N = hidden, K = inter]); e4m3 -> bf16
-// is exact and bf16 products are exact in fp32, so each 128-column block sum is an fp32 sum
-// of exact products, scaled by the weight's block scale as it joins the accumulator. One
-// term (hi = bf16(h)) is the reference's ExpertPrecision::Bf16 arithmetic; two (hi + lo,
-// 16 significant bits of the fp32 h) stand for ExpertPrecision::Exact.
+// is exact and bf16 products are exact in fp32, so each 64-column half of a 128-column
+// scale block sums exact products in fp32, scaled by the weight's block scale as it joins
+// the accumulator. One term (hi = bf16(h)) is the reference's ExpertPrecision::Bf16
+// arithmetic; two (hi + lo, 16 significant bits of the fp32 h) stand for
+// ExpertPrecision::Exact.
 //
-// Block tiles of 128 assignments x 256 outputs; wave (wm, wn) takes rows 32 wm .. + 32 and
-// outputs 128 wn .. + 128 (one 128-row weight scale block). K steps of 64 through three LDS
-// stages (direct-to-LDS loads, as the FP8 passes; 150 KB, one block a CU): a stage holds the
-// h term tiles (128 assignments x 64 bf16 = 128 bytes a row, 8 chunks, the FP8 tiles' chunk
-// swizzle), the weight tile (256 rows x 64 bytes, 4 chunks, chunk c of row r at
-// 4 r + (c ^ ((r >> 2) & 3)), so the 16 rows of an operand read, and any 8 of them, land in
-// distinct 16-byte bank groups) and the wave scales. Lane l of a wave takes K values
-// 16 (l / 16) .. + 16 of the step for its row (A: assignment l % 16 of a 16-row subtile,
-// B: weight row l % 16), as two 8-value halves, one per MFMA: the same K order on both
-// sides, so the contraction is the plain sum. The operand reads and the direct-to-LDS
-// writes are the kernel's limit: a wave reads its A rows once for 8 N subtiles (at 128 x 128
-// tiles it read them for 4, and the pass took 775 us a 2048-token step instead of 695).
+// K steps of 64 through LDS stages filled by direct-to-LDS loads, as the FP8 passes. An h
+// term tile holds 64 bf16 (128 bytes) a row in 8 chunks with the FP8 tiles' chunk swizzle;
+// the weight tile 64 bytes a row in 4 chunks, chunk c of row r at 4 r + (c ^ ((r >> 2) & 3)),
+// so the 16 rows of an operand read, and any 8 of them, land in distinct 16-byte bank
+// groups. Lane l of a wave takes K values 16 (l / 16) .. + 16 of the step for its row (A:
+// assignment l % 16 of a 16-row subtile, B: weight row l % 16), as two 8-value halves, one
+// per MFMA: the same K order on both sides, so the contraction is the plain sum.
 constexpr int GBK2 = 64;                       // K step of the down pass
 constexpr int D_HT = GBM * GBK2 * 2;           // bytes of one h term tile
 
@@ -778,184 +774,97 @@ typedef __bf16 gbf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ int wchunk_pos(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
 
-constexpr int GBNW = 256;                      // outputs per block tile
-constexpr int DW_WT = GBNW * GBK2;             // bytes of the weight tile
-template <int TERMS>
-constexpr int dw_sbytes() { return TERMS * D_HT + DW_WT; }
-// A tile of at most 32 assignments streams the weights: its stages hold two K steps (one
-// 128-column scale block), each half the 32-row h term tiles and the weight tile of one K
-// step, so four K steps of weights are in flight instead of two.
-constexpr int DL_ROWS = 32;
+constexpr int DL_ROWS = 32;                    // assignments of a light tile
 constexpr int DL_HT = DL_ROWS * GBK2 * 2;      // bytes of one light h term tile
-template <int TERMS>
-constexpr int dl_half() { return TERMS * DL_HT + DW_WT; }
-template <int TERMS>
-constexpr int dw_scales() { return dw_sbytes<TERMS>() > 2 * dl_half<TERMS>() ? dw_sbytes<TERMS>() : 2 * dl_half<TERMS>(); }
-template <int TERMS>
-constexpr int dw_stot() { return dw_scales<TERMS>() + GTHREADS * 4; }
-template <int TERMS>
-constexpr int dw_lps() { return 2 * TERMS + 2 + 1; }
-template <int TERMS>
-constexpr int dl_lps() { return (TERMS == 2 ? 2 : 1) + 4 + 1; }
 
-struct DWSrc {
+// ---- down over 512-output tiles (the prefill step) -------------------------------------
+//
+// A down tile waits on its loads more than on its work: a 256-output tile with the matrix
+// cores, the conversions and the operand reads all switched off still took three quarters
+// of its time. A tile of 128 assignments x 512 outputs moves 64 KiB a K step (the h term
+// tiles 32 KiB, the weight tile 32 KiB) for twice the multiply-adds of a 256-output tile's
+// 48 KiB. Wave (wm, wn) of the 8 takes h rows 32 wm .. + 32 (2 M subtiles) and weight rows
+// 256 wn .. + 256 (16 N subtiles, two 128-row scale blocks): 128 accumulators a lane, so
+// each K step's block sums are scaled into them at once (one K step is half a 128-column
+// scale block; both halves take its scale) instead of held across the block. Two LDS
+// stages (the two-stage protocol of grouped_gate_up256_kernel). A tile of at most 32
+// assignments streams its weights instead: wave w takes weight rows 64 w .. + 64 over the
+// tile's h rows, and a stage holds one K step's 32-row h term tiles and the weight tile.
+constexpr int GBN5 = 512;                    // outputs per block tile
+constexpr int D5_WT = GBN5 * GBK2;           // bytes of the weight tile, one K step
+template <int TERMS>
+constexpr int d5_scales() { return TERMS * D_HT + D5_WT > 2 * DL_HT + D5_WT ? TERMS * D_HT + D5_WT : 2 * DL_HT + D5_WT; }
+template <int TERMS>
+constexpr int d5_stot() { return d5_scales<TERMS>() + GTHREADS * 4; }
+
+struct D5Src {
     __amdgpu_buffer_rsrc_t hr, wr, sr;
-    int ho[2], wo[2];  // step-0 byte offsets (ho < 0: a row past the expert, loads zeros)
-    int hl_off;
-    int so;
-    int lho;           // light stages: this wave's h chunk at K step 0 (< 0: past the expert)
+    int ho[2], wo[4];  // step-0 byte offsets (ho < 0: a row past the expert, loads zeros)
+    int hl_off;        // bytes from the hi plane to the lo plane
+    int so;            // this lane's block scale at K step 0 (G_OOB: none)
+    int lho;           // light stages: this wave's h chunk (< 0: past the expert or no chunk)
 };
 
+// Heavy stage: h term t's chunks (2 wave + j) 64 + lane, the weight chunks (4 wave + j) 64
+// + lane, lanes 0-1 the wave's two block scales.
 template <int TERMS>
-__device__ __forceinline__ void dw_issue(const DWSrc& s, int kb, int nkb, uint8_t* sb, float* scw, int wave) {
+__device__ __forceinline__ void d5_issue(const D5Src& s, int kb, int nkb, uint8_t* sb, int wave) {
     const bool ok = kb < nkb;
     const int k0 = kb * GBK2 * 2;
 #pragma unroll
     for (int t = 0; t < TERMS; t++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
-            dma16(s.hr, sb + t * D_HT + (2 * wave + j) * 1024,
-                  ok && s.ho[j] >= 0 ? s.ho[j] + t * s.hl_off + k0 : G_OOB);
+            dma16(s.hr, sb + t * D_HT + (2 * wave + j) * 1024, ok && s.ho[j] >= 0 ? s.ho[j] + t * s.hl_off + k0 : G_OOB);
 #pragma unroll
-    for (int j = 0; j < 2; j++)
-        dma16(s.wr, sb + TERMS * D_HT + (2 * wave + j) * 1024, ok ? s.wo[j] + kb * GBK2 : G_OOB);
-    dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
+    for (int j = 0; j < 4; j++)
+        dma16(s.wr, sb + TERMS * D_HT + (4 * wave + j) * 1024, ok ? s.wo[j] + kb * GBK2 : G_OOB);
+    dma4(s.sr, reinterpret_cast<float*>(sb + d5_scales<TERMS>()) + 64 * wave,
+         ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
 }
 
-// A light stage: K steps kb and kb + 1 (kb even). TERMS 2: wave w loads h term w / 4 of
-// both halves; TERMS 1: wave w loads the h tile of half w / 4. Every wave loads its chunks
-// of both halves' weight tiles, lane 0 the block scale.
+// Light stage: one h chunk a wave (TERMS 2: term wave / 4; TERMS 1: waves 4-7 load zeros
+// into the unused second term area), the weight chunks as above, lane 0 the block scale.
 template <int TERMS>
-__device__ __forceinline__ void dw_issue_light(const DWSrc& s, int kb, int nkb, uint8_t* sb, float* scw, int wave) {
+__device__ __forceinline__ void d5_issue_light(const D5Src& s, int kb, int nkb, uint8_t* sb, int wave) {
     const bool ok = kb < nkb;
     const int k0 = kb * GBK2 * 2;
-    if constexpr (TERMS == 2) {
+    dma16(s.hr, sb + (wave >> 2) * DL_HT + (wave & 3) * 1024, ok && s.lho >= 0 ? s.lho + k0 : G_OOB);
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-            dma16(s.hr, sb + h * dl_half<TERMS>() + (wave >> 2) * DL_HT + (wave & 3) * 1024,
-                  ok && s.lho >= 0 ? s.lho + k0 + h * GBK2 * 2 : G_OOB);
-    } else {
-        dma16(s.hr, sb + (wave >> 2) * dl_half<TERMS>() + (wave & 3) * 1024, ok && s.lho >= 0 ? s.lho + k0 : G_OOB);
-    }
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-            dma16(s.wr, sb + h * dl_half<TERMS>() + TERMS * DL_HT + (2 * wave + j) * 1024,
-                  ok ? s.wo[j] + (kb + h) * GBK2 : G_OOB);
-    dma4(s.sr, scw + 64 * wave, ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
+    for (int j = 0; j < 4; j++)
+        dma16(s.wr, sb + 2 * DL_HT + (4 * wave + j) * 1024, ok ? s.wo[j] + kb * GBK2 : G_OOB);
+    dma4(s.sr, reinterpret_cast<float*>(sb + d5_scales<TERMS>()) + 64 * wave,
+         ok && s.so != G_OOB ? s.so + 4 * (kb >> 1) : G_OOB);
 }
 
-// A: h term t, row half hf of M subtile ms (+2048 bytes; t: +the term tile's size); B: weight
-// rows of N subtile ns (+1024 bytes each: 8 of them, or the light layout's 2); then this
-// wave's weight block scale. ab: the term-0 h tile, bt: the wave's first weight row's chunks,
-// scw: the stage's scale words. row0: the wave's first h row; wrow0: its first weight row.
-template <int TERMS, bool LIGHT>
-__device__ __forceinline__ void dw_reads(const uint8_t* ab, const uint8_t* bt, const uint8_t* scw, int row0, int wrow0,
-                                         int wave, int lane, uint4 (&ra)[2][TERMS][2], uint4 (&rb)[8], float& ws) {
-    typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
-    const uint32_t base = (uint32_t)(uintptr_t)(lds_cptr)ab;
-    const int g = lane >> 4, row = row0 + (lane & 15), wrow = wrow0 + (lane & 15);
-    const uint32_t a0 = base + 16 * chunk_pos(row, 2 * g), a1 = base + 16 * chunk_pos(row, 2 * g + 1);
-    const uint32_t bb = (uint32_t)(uintptr_t)(lds_cptr)bt + 16 * wchunk_pos(wrow, g);
-    const uint32_t sc = (uint32_t)(uintptr_t)(lds_cptr)scw + 4 * 64 * wave;
-    if constexpr (TERMS == 2 && LIGHT) {
-        static_assert(DL_HT == 4096, "light term offsets");
-        asm volatile(
-            "ds_read_b128 %0, %11\n\t"
-            "ds_read_b128 %1, %12\n\t"
-            "ds_read_b128 %2, %11 offset:2048\n\t"
-            "ds_read_b128 %3, %12 offset:2048\n\t"
-            "ds_read_b128 %4, %11 offset:4096\n\t"
-            "ds_read_b128 %5, %12 offset:4096\n\t"
-            "ds_read_b128 %6, %11 offset:6144\n\t"
-            "ds_read_b128 %7, %12 offset:6144\n\t"
-            "ds_read_b128 %8, %13\n\t"
-            "ds_read_b128 %9, %13 offset:1024\n\t"
-            "ds_read_b32 %10, %14\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(ra[0][1][0]),
-              "=&v"(ra[0][1][1]), "=&v"(ra[1][1][0]), "=&v"(ra[1][1][1]), "=&v"(rb[0]), "=&v"(rb[1]), "=&v"(ws)
-            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
-            : "memory");
-    } else if constexpr (LIGHT) {
-        asm volatile(
-            "ds_read_b128 %0, %7\n\t"
-            "ds_read_b128 %1, %8\n\t"
-            "ds_read_b128 %2, %7 offset:2048\n\t"
-            "ds_read_b128 %3, %8 offset:2048\n\t"
-            "ds_read_b128 %4, %9\n\t"
-            "ds_read_b128 %5, %9 offset:1024\n\t"
-            "ds_read_b32 %6, %10\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(rb[0]), "=&v"(rb[1]),
-              "=&v"(ws)
-            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
-            : "memory");
-    } else if constexpr (TERMS == 2) {
-        static_assert(D_HT == 16384, "term offsets");
-        asm volatile(
-            "ds_read_b128 %0, %17\n\t"
-            "ds_read_b128 %1, %18\n\t"
-            "ds_read_b128 %2, %17 offset:2048\n\t"
-            "ds_read_b128 %3, %18 offset:2048\n\t"
-            "ds_read_b128 %4, %17 offset:16384\n\t"
-            "ds_read_b128 %5, %18 offset:16384\n\t"
-            "ds_read_b128 %6, %17 offset:18432\n\t"
-            "ds_read_b128 %7, %18 offset:18432\n\t"
-            "ds_read_b128 %8, %19\n\t"
-            "ds_read_b128 %9, %19 offset:1024\n\t"
-            "ds_read_b128 %10, %19 offset:2048\n\t"
-            "ds_read_b128 %11, %19 offset:3072\n\t"
-            "ds_read_b128 %12, %19 offset:4096\n\t"
-            "ds_read_b128 %13, %19 offset:5120\n\t"
-            "ds_read_b128 %14, %19 offset:6144\n\t"
-            "ds_read_b128 %15, %19 offset:7168\n\t"
-            "ds_read_b32 %16, %20\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(ra[0][1][0]),
-              "=&v"(ra[0][1][1]), "=&v"(ra[1][1][0]), "=&v"(ra[1][1][1]), "=&v"(rb[0]), "=&v"(rb[1]), "=&v"(rb[2]),
-              "=&v"(rb[3]), "=&v"(rb[4]), "=&v"(rb[5]), "=&v"(rb[6]), "=&v"(rb[7]), "=&v"(ws)
-            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
-            : "memory");
-    } else {
-        asm volatile(
-            "ds_read_b128 %0, %13\n\t"
-            "ds_read_b128 %1, %14\n\t"
-            "ds_read_b128 %2, %13 offset:2048\n\t"
-            "ds_read_b128 %3, %14 offset:2048\n\t"
-            "ds_read_b128 %4, %15\n\t"
-            "ds_read_b128 %5, %15 offset:1024\n\t"
-            "ds_read_b128 %6, %15 offset:2048\n\t"
-            "ds_read_b128 %7, %15 offset:3072\n\t"
-            "ds_read_b128 %8, %15 offset:4096\n\t"
-            "ds_read_b128 %9, %15 offset:5120\n\t"
-            "ds_read_b128 %10, %15 offset:6144\n\t"
-            "ds_read_b128 %11, %15 offset:7168\n\t"
-            "ds_read_b32 %12, %16\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(ra[0][0][0]), "=&v"(ra[0][0][1]), "=&v"(ra[1][0][0]), "=&v"(ra[1][0][1]), "=&v"(rb[0]), "=&v"(rb[1]),
-              "=&v"(rb[2]), "=&v"(rb[3]), "=&v"(rb[4]), "=&v"(rb[5]), "=&v"(rb[6]), "=&v"(rb[7]), "=&v"(ws)
-            : "v"(a0), "v"(a1), "v"(bb), "v"(sc)
-            : "memory");
-    }
-}
-
-// act: this wave's 16-row M subtiles that hold assignments (1 or 2; a subtile past the
-// expert's last assignment holds zeros, and its products are not stored).
-// LIGHT: the wave's 2 N subtiles (32 weight rows) over the tile's at most 32 h rows;
-// otherwise its 8 N subtiles (128 rows) over its 32 h rows.
-template <int TERMS, bool LIGHT>
-__device__ __forceinline__ void dw_step(const uint8_t* ab, const uint8_t* bt, const uint8_t* scw, int row0, int wrow0,
-                                        int wave, int lane, bool fold, int act, gf32x4 (&blk)[2][8],
-                                        float (&acc)[2][8][4]) {
-    constexpr int NS = LIGHT ? 2 : 8;
-    uint4 ra[2][TERMS][2], rb[8];
-    float ws;
-    dw_reads<TERMS, LIGHT>(ab, bt, scw, row0, wrow0, wave, lane, ra, rb, ws);
+// One K step: NS N subtiles over the wave's 2 M subtiles (rows past the expert hold zeros
+// and are not stored). at: the term-0 h tile (term t at + t * toff), bt: the weight tile,
+// row0 / wrow0: the wave's first h row and weight row; scale words ws[ns / 8].
+template <int TERMS, int NS>
+__device__ __forceinline__ void d5_step(const uint8_t* at, int toff, const uint8_t* bt, const float* ws, int row0,
+                                        int wrow0, int lane, float (&acc)[2][16][4]) {
+    const int g = lane >> 4;
+    uint4 ra[2][TERMS][2];
+#pragma unroll
+    for (int ms = 0; ms < 2; ms++)
+#pragma unroll
+        for (int t = 0; t < TERMS; t++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++)
+                ra[ms][t][hf] = *reinterpret_cast<const uint4*>(
+                    at + t * toff + 16 * chunk_pos(row0 + 16 * ms + (lane & 15), 2 * g + hf));
+    const float wsc[2] = {ws[0], NS > 8 ? ws[1] : ws[0]};
+    // the weight subtiles one read ahead of their products (all of them at once beside the
+    // 128 accumulators spill)
+    auto bread = [&](int ns) {
+        return *reinterpret_cast<const uint4*>(bt + 16 * wchunk_pos(wrow0 + 16 * ns + (lane & 15), g));
+    };
+    uint4 wcur = bread(0);
 #pragma unroll
     for (int ns = 0; ns < NS; ns++) {
-        const uint32_t ww[4] = {rb[ns].x, rb[ns].y, rb[ns].z, rb[ns].w};
+        uint4 wnext = wcur;
+        if (ns + 1 < NS) wnext = bread(ns + 1);
+        const uint32_t ww[4] = {wcur.x, wcur.y, wcur.z, wcur.w};
         gbf16x8 b[2];
 #pragma unroll
         for (int hf = 0; hf < 2; hf++)
@@ -968,146 +877,123 @@ __device__ __forceinline__ void dw_step(const uint8_t* ab, const uint8_t* bt, co
                 b[hf][4 * q + 2] = p1[0];
                 b[hf][4 * q + 3] = p1[1];
             }
+        gf32x4 blk[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+            for (int t = 0; t < TERMS; t++)
+#pragma unroll
+                for (int ms = 0; ms < 2; ms++)
+                    blk[ms] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gbf16x8, ra[ms][t][hf]),
+                                                                      b[hf], blk[ms], 0, 0, 0);
 #pragma unroll
         for (int ms = 0; ms < 2; ms++)
-            if (ms < act)
 #pragma unroll
-                for (int hf = 0; hf < 2; hf++)
-#pragma unroll
-                    for (int t = 0; t < TERMS; t++)
-                        blk[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(gbf16x8, ra[ms][t][hf]), b[hf], blk[ms][ns], 0, 0, 0);
-    }
-    if (fold) {
-#pragma unroll
-        for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-            for (int ns = 0; ns < NS; ns++) {
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc[ms][ns][e] = fmaf(blk[ms][ns][e], ws, acc[ms][ns][e]);
-                blk[ms][ns] = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+            for (int e = 0; e < 4; e++) acc[ms][ns][e] = fmaf(blk[ms][e], wsc[ns >> 3], acc[ms][ns][e]);
+        __builtin_amdgcn_sched_barrier(0);
+        wcur = wnext;
     }
 }
 
-// Tiles from the device tile table: each XCD takes whole M-tiles with the N-tile fastest, so
-// the blocks an XCD runs together take the N-tiles of one M-tile, and that tile's h planes
-// come into the XCD's L2 once and serve all of them. (M-tile fastest re-fetched every
-// M-tile's h from beyond the L2 for each N-tile: 3.2 GB a 2048-token step with two terms.)
-// Outputs past N (hidden not a multiple of 256) read zero weights and are not stored.
 template <int TERMS>
-__global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
-    constexpr int STOT = dw_stot<TERMS>(), SCB = dw_scales<TERMS>();
-    __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT], sb2[STOT];
+__global__ void __launch_bounds__(GTHREADS) grouped_down512_kernel(GArgs g) {
+    constexpr int STOT = d5_stot<TERMS>(), SCB = d5_scales<TERMS>();
+    // each stage its own LDS object, so the compiler's waits for direct-to-LDS loads cover
+    // only the loads into the buffer a read touches
+    __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    // block L runs on XCD L % 8 as its item q = L / 8: M-tile 8 (q / NT) + L % 8, N-tile
-    // q % NT (M-tiles dealt to the XCDs in turn, so each XCD gets its share of heavy and
-    // light tiles)
+    // block L runs on XCD L % 8 as its item q = L / 8: M-tile 8 (q / NT) + L % 8, N-tile q % NT
     const int NT = (int)gridDim.x, MT = *g.ntiles;
     const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), q = L >> 3;
     const int mt = 8 * (q / NT) + (L & 7), nt = q % NT;
     if (mt >= MT) return;
-    const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBNW;
+    const int i = g.tiles[2 * mt], m0 = g.tiles[2 * mt + 1], n0 = nt * GBN5;
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
     G_STAMP_START(g, L, i, m0, n0, a1 - a0);
     const uint8_t* rec = reinterpret_cast<const uint8_t*>(g.recs[i]);
     const int nkb = (int)(g.K / GBK2);
-    DWSrc src;
+    const int rows = a1 - (a0 + m0);
+    const bool light = rows <= DL_ROWS;
+    D5Src src;
     src.hl_off = TERMS == 2 ? (int)((const uint8_t*)g.hl - (const uint8_t*)g.hh) : 0;
     src.hr = __builtin_amdgcn_make_buffer_rsrc(g.hh, (short)0, 0x7fff0000, G_BUF_FLAGS);
     src.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, (int)(g.w_off + g.N * g.K),
                                                G_BUF_FLAGS);
+    src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         int r, c;
         pos_chunk((2 * wave + j) * 64 + lane, r, c);
         const int a = a0 + m0 + r;
-        src.ho[j] = a < a1 ? (int)(a * g.K * 2) + 16 * c : -1;  // past the expert: zeros
-        // weights: position (2 wave + j) 64 + lane = row p / 4, chunk (p % 4) ^ ((row >> 2) & 3)
-        const int p = (2 * wave + j) * 64 + lane, wr = p >> 2, wc = (p & 3) ^ ((wr >> 2) & 3);
-        src.wo[j] = (int)(g.w_off + (int64_t)(n0 + wr) * g.K) + 16 * wc;
+        src.ho[j] = a < a1 ? (int)(a * g.K * 2) + 16 * c : -1;
     }
-    src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
-    // a light tile (at most 32 assignments; K steps come in pairs, K being a multiple of
-    // 128): wave w takes weight rows 32 w .. + 32 over all the tile's h rows; otherwise wave
-    // (wm, wn) takes h rows 32 wm .. + 32 and weight rows 128 wn .. + 128
-    const int rows = a1 - (a0 + m0);
-    const bool light = rows <= DL_ROWS;
-    const int row0 = light ? 0 : 32 * wm, wrow0 = light ? 32 * wave : 128 * wn;
-    const int nw0 = n0 + wrow0;  // this wave's first output (inside one 128-row scale block)
-    const int left = rows - row0;  // assignments from this wave's first row on
-    const int act = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : left <= 16 ? 1 : 2);
-    src.so = lane == 0 && nw0 < g.N ? (int)(g.s_off + (int64_t)(nw0 / 128) * (g.K / 128) * 4) : G_OOB;
-    // light stages: h chunk (wave % 4) 64 + lane of term wave / 4 (TERMS 2) or of K step
-    // wave / 4 (TERMS 1)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        // weight position (4 wave + j) 64 + lane = row p / 4, chunk (p % 4) ^ ((row >> 2) & 3);
+        // rows past N read zeros (their outputs are not stored)
+        const int p = (4 * wave + j) * 64 + lane, wr = p >> 2, wc = (p & 3) ^ ((wr >> 2) & 3);
+        src.wo[j] = n0 + wr < g.N ? (int)(g.w_off + (int64_t)(n0 + wr) * g.K) + 16 * wc : G_OOB - GBK2 * 64;
+    }
     {
         int r, c;
         pos_chunk((wave & 3) * 64 + lane, r, c);
         const int a = a0 + m0 + r;
-        src.lho = a < a1 ? (int)(a * g.K * 2) + 16 * c + (TERMS == 2 ? (wave >> 2) * src.hl_off : (wave >> 2) * GBK2 * 2)
-                         : -1;
+        src.lho = a < a1 && (TERMS == 2 || wave < 4) ? (int)(a * g.K * 2) + 16 * c + (wave >> 2) * src.hl_off : -1;
     }
-    float acc[2][8][4];
-    gf32x4 blk[2][8];
+    // the wave's first h row and weight row, its first output, and its scale words
+    const int row0 = light ? 0 : 32 * wm, wrow0 = light ? 64 * wave : 256 * wn;
+    const int nw0 = n0 + wrow0;
+    const int nsc = light ? 1 : 2;  // 128-row scale blocks the wave's rows span
+    src.so = lane < nsc && nw0 + 128 * lane < g.N
+                 ? (int)(g.s_off + (int64_t)(nw0 / 128 + lane) * (g.K / 128) * 4)
+                 : G_OOB;
+    const bool act = __builtin_amdgcn_readfirstlane(rows - row0 > 0);  // the wave holds assignments
+    float acc[2][16][4];
 #pragma unroll
     for (int ms = 0; ms < 2; ms++)
 #pragma unroll
-        for (int ns = 0; ns < 8; ns++) {
-            blk[ms][ns] = gf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ns = 0; ns < 16; ns++)
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[ms][ns][e] = 0.0f;
-        }
-#define DW_SW(B) reinterpret_cast<float*>((B) + SCB)
-#define DW_STEP(SB, NSB)                                                                                   \
-    {                                                                                                      \
-        wait_vm<dw_lps<TERMS>()>();                                                                        \
-        g_barrier();                                                                                       \
-        dw_issue<TERMS>(src, kb + 2, nkb, NSB, DW_SW(NSB), wave);                                          \
-        if (act > 0)                                                                                       \
-            dw_step<TERMS, false>(SB, SB + TERMS * D_HT, SB + SCB, row0, wrow0, wave, lane,                \
-                                  (kb & 1) || kb + 1 == nkb, act, blk, acc);                               \
-        if (++kb == nkb) break;                                                                            \
+#define D5_SW(B) (reinterpret_cast<const float*>((B) + SCB) + 64 * wave)
+#define D5_STEP(SB, NSB)                                                                          \
+    {                                                                                             \
+        wait_vm<0>();                                                                             \
+        g_barrier();                                                                              \
+        d5_issue<TERMS>(src, kb + 1, nkb, NSB, wave);                                             \
+        if (act) d5_step<TERMS, 16>(SB, D_HT, SB + TERMS * D_HT, D5_SW(SB), row0, wrow0, lane, acc);        \
+        if (++kb == nkb) break;                                                                   \
     }
-#define DW_LSTEP(SB, NSB)                                                                                  \
-    {                                                                                                      \
-        wait_vm<dl_lps<TERMS>()>();                                                                        \
-        g_barrier();                                                                                       \
-        dw_issue_light<TERMS>(src, kb + 4, nkb, NSB, DW_SW(NSB), wave);                                    \
-        if (act > 0) {                                                                                     \
-            dw_step<TERMS, true>(SB, SB + TERMS * DL_HT, SB + SCB, row0, wrow0, wave, lane, false, act, blk, \
-                                 acc);                                                                     \
-            dw_step<TERMS, true>(SB + dl_half<TERMS>(), SB + dl_half<TERMS>() + TERMS * DL_HT, SB + SCB, row0, \
-                                 wrow0, wave, lane, true, act, blk, acc);                                  \
-        }                                                                                                  \
-        kb += 2;                                                                                           \
-        if (kb == nkb) break;                                                                              \
+#define D5_LSTEP(SB, NSB)                                                                         \
+    {                                                                                             \
+        wait_vm<0>();                                                                             \
+        g_barrier();                                                                              \
+        d5_issue_light<TERMS>(src, kb + 1, nkb, NSB, wave);                                       \
+        if (act) d5_step<TERMS, 4>(SB, DL_HT, SB + 2 * DL_HT, D5_SW(SB), row0, wrow0, lane, acc);           \
+        if (++kb == nkb) break;                                                                   \
     }
     int kb = 0;
     if (light) {
-        dw_issue_light<TERMS>(src, 0, nkb, sb0, DW_SW(sb0), wave);
-        dw_issue_light<TERMS>(src, 2, nkb, sb1, DW_SW(sb1), wave);
+        d5_issue_light<TERMS>(src, 0, nkb, sb0, wave);
         for (;;) {
-            DW_LSTEP(sb0, sb2)
-            DW_LSTEP(sb1, sb0)
-            DW_LSTEP(sb2, sb1)
+            D5_LSTEP(sb0, sb1)
+            D5_LSTEP(sb1, sb0)
         }
     } else {
-        dw_issue<TERMS>(src, 0, nkb, sb0, DW_SW(sb0), wave);
-        dw_issue<TERMS>(src, 1, nkb, sb1, DW_SW(sb1), wave);
+        d5_issue<TERMS>(src, 0, nkb, sb0, wave);
         for (;;) {
-            DW_STEP(sb0, sb2)
-            DW_STEP(sb1, sb0)
-            DW_STEP(sb2, sb1)
+            D5_STEP(sb0, sb1)
+            D5_STEP(sb1, sb0)
         }
     }
-#undef DW_SW
-#undef DW_STEP
-#undef DW_LSTEP
-    wait_vm<0>();  // the zero-filled stages past the end have landed before the block ends
-    const int nsw = light ? 2 : 8;  // the wave's N subtiles
+#undef D5_SW
+#undef D5_STEP
+#undef D5_LSTEP
+    wait_vm<0>();  // the zero-filled stage past the end has landed before the block ends
+    const int nsw = light ? 4 : 16;  // the wave's N subtiles
 #pragma unroll
     for (int ms = 0; ms < 2; ms++)
 #pragma unroll
@@ -1115,7 +1001,7 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down_wide_kernel(GArgs g) {
             const int a = a0 + m0 + row0 + 16 * ms + 4 * (lane >> 4) + e;
             if (a >= a1) continue;
 #pragma unroll
-            for (int ns = 0; ns < 8; ns++) {
+            for (int ns = 0; ns < 16; ns++) {
                 const int64_t n = nw0 + 16 * ns + (lane & 15);
                 if (ns < nsw && n < g.N) g.y[(int64_t)a * g.N + n] = acc[ms][ns][e];
             }
@@ -1136,9 +1022,9 @@ int launch_grouped_gate_up256(const GArgs& a, dim3 grid, hipStream_t st) {
     return launched("grouped_gate_up_fp8");
 }
 
-int launch_grouped_down(const GArgs& a, int terms, dim3 grid, hipStream_t st) {
-    if (terms == 2) hipLaunchKernelGGL(grouped_down_wide_kernel<2>, grid, dim3(GTHREADS), 0, st, a);
-    else hipLaunchKernelGGL(grouped_down_wide_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
+int launch_grouped_down512(const GArgs& a, int terms, dim3 grid, hipStream_t st) {
+    if (terms == 2) hipLaunchKernelGGL(grouped_down512_kernel<2>, grid, dim3(GTHREADS), 0, st, a);
+    else hipLaunchKernelGGL(grouped_down512_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
     return launched("grouped_down_bf16");
 }
 
@@ -1332,8 +1218,8 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     d.stamps = a.stamps ? a.stamps + 4 * (size_t)(geo->inter / GBN) * (w.max_tiles2 + 8) : nullptr;
 #endif
     const int terms = precision == OOM_EXPERT_EXACT ? 2 : 1;
-    if (int rc = launch_grouped_down(d, terms, dim3((unsigned)cdiv(geo->hidden, GBNW), (unsigned)w.max_tiles + 8, 1),
-                                     st))
+    if (int rc = launch_grouped_down512(d, terms, dim3((unsigned)cdiv(geo->hidden, GBN5), (unsigned)w.max_tiles + 8, 1),
+                                        st))
         return rc;
     return launch_combine(y, pv.slot_assign(), weights, out, out_dtype, T, (int)geo->hidden, k, st);
 }
