@@ -179,14 +179,23 @@ __global__ void __launch_bounds__(256) quant_rows_vec_kernel(const void* __restr
 }
 
 // ---- the tile table of a device plan: tile mt = (expert i, assignments from off[i] + m0).
-// One block of 1024 threads; experts in chunks of 1024 with a running carry. With
+// One block of 1024 threads a table; experts in chunks of 1024 with a running carry. With
 // light_rows > 0 the table lists the tiles of more than light_rows assignments first and
 // then the others (each expert's last tile when it holds at most light_rows), so the
-// blocks that take tiles in table order start the long ones first.
+// blocks that take tiles in table order start the long ones first. Block 1, when
+// launched, builds a second table (tile_rows2, light_rows2, tiles2, ntiles2).
+struct TileTable {
+    int tile_rows, light_rows;
+    int32_t* tiles;
+    int32_t* ntiles;
+};
 __global__ void __launch_bounds__(1024) grouped_tiles_kernel(const int32_t* __restrict__ n_e_p,
-                                                             const int32_t* __restrict__ off, int tile_rows,
-                                                             int light_rows, int32_t* __restrict__ tiles,
-                                                             int32_t* __restrict__ ntiles) {
+                                                             const int32_t* __restrict__ off, TileTable t0,
+                                                             TileTable t1) {
+    const TileTable tt = blockIdx.x == 0 ? t0 : t1;
+    const int tile_rows = tt.tile_rows, light_rows = tt.light_rows;
+    int32_t* __restrict__ tiles = tt.tiles;
+    int32_t* __restrict__ ntiles = tt.ntiles;
     __shared__ int wsum[16];
     __shared__ int carry_s;
     const int n_e = *n_e_p, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1044,10 +1053,8 @@ int launch_quant_rows(const void* x, int xdt, int64_t rows, int64_t cols, uint8_
     return launched("quantize_rows_fp8");
 }
 
-int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, int tile_rows, int light_rows, int32_t* tiles,
-                         int32_t* ntiles, hipStream_t st) {
-    hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(1024), 0, st, n_e, off, tile_rows, light_rows, tiles,
-                       ntiles);
+int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, TileTable t0, const TileTable* t1, hipStream_t st) {
+    hipLaunchKernelGGL(grouped_tiles_kernel, dim3(t1 ? 2 : 1), dim3(1024), 0, st, n_e, off, t0, t1 ? *t1 : t0);
     return launched("grouped_tiles");
 }
 
@@ -1058,14 +1065,17 @@ int launch_grouped_tiles(const int32_t* n_e, const int32_t* off, int tile_rows, 
 namespace oom {
 int launch_combine(const float* y, const int32_t* slot, const float* w, void* out, int odt, int T, int H, int k,
                    hipStream_t st);
+size_t plan_multi_counts(int A, int E);
+int launch_plan_multi(const int32_t* ids, int T, int E, int k, const uint64_t* all_recs, int32_t* plan, uint64_t* recs,
+                      int32_t* counts, hipStream_t st);
 int check_geo(const OomFp8Record* g, const char* who);
 
-// Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | tiles2 | hh | hl | y
-// (tiles: the 128-row tile table of the down pass, tiles2: the 256-row one of gate/up; hh
-// and hl: the bf16 hi and lo terms of h [A, inter]; hl is written for the exact precision
-// only).
+// Workspace of oom_moe_prefill_fp8: plan | recs | xq | xs | tiles | tiles2 | hh | hl | y |
+// counts (tiles: the 128-row tile table of the down pass, tiles2: the 256-row one of
+// gate/up; hh and hl: the bf16 hi and lo terms of h [A, inter]; hl is written for the exact
+// precision only; counts: the plan's per-block expert counts).
 struct PrefillWs {
-    size_t plan, recs, xq, xs, tiles, tiles2, hh, hl, y, total;
+    size_t plan, recs, xq, xs, tiles, tiles2, hh, hl, y, counts, total;
     int max_tiles, max_tiles2;
 };
 
@@ -1085,7 +1095,8 @@ static PrefillWs prefill_ws(int T, int E, int k, const OomFp8Record& g) {
     w.hh = w.tiles2 + p_al256((2 * (size_t)w.max_tiles2 + 1) * sizeof(int32_t));
     w.hl = w.hh + p_al256(A * I * sizeof(uint16_t));
     w.y = w.hl + p_al256(A * I * sizeof(uint16_t));
-    w.total = w.y + p_al256(A * H * sizeof(float));
+    w.counts = w.y + p_al256(A * H * sizeof(float));
+    w.total = w.counts + p_al256(plan_multi_counts((int)A, E) * sizeof(int32_t));
     return w;
 }
 }  // namespace oom
@@ -1174,10 +1185,12 @@ extern "C" int oom_moe_prefill_fp8(const float* logits, const void* x, int x_dty
     const int A = T * k;
     PlanView pv{plan, E, A};
     if (int rc = oom_router_topk(logits, ids, weights, T, E, k, stream)) return rc;
-    if (int rc = oom_moe_plan(ids, T, E, k, all_recs, plan, recs, stream)) return rc;
+    if (int rc = launch_plan_multi(ids, T, E, k, all_recs, plan, recs, reinterpret_cast<int32_t*>(base + w.counts), st))
+        return rc;
     if (int rc = launch_quant_rows(x, x_dtype, T, geo->hidden, xq, xs, st)) return rc;
-    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM, 0, tiles, ntiles, st)) return rc;
-    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), GBM2, GU2_LROWS, tiles2, ntiles2, st)) return rc;
+    // both tile tables in one launch: 128-row tiles (down), 256-row tiles with the long ones first (gate/up)
+    const TileTable tt2{GBM2, GU2_LROWS, tiles2, ntiles2};
+    if (int rc = launch_grouped_tiles(pv.n_e(), pv.off(), TileTable{GBM, 0, tiles, ntiles}, &tt2, st)) return rc;
     GArgs a{};
     a.recs = recs;
     a.off = pv.off();

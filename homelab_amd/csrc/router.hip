@@ -22,7 +22,7 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict
     }
 }
 
-// Block-wide exclusive scan of one int per thread (blockDim 1024 = 16 waves).
+// Block-wide exclusive scan of one int per thread (a block of whole waves, at most 16).
 __device__ int block_exclusive_scan(int v, int* warp_tot, int& total) {
     int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int incl = v;
@@ -223,6 +223,205 @@ __global__ void __launch_bounds__(1024) moe_plan_kernel(const int32_t* __restric
         if (e >= 0) atomicAdd(&start[e], 1);
         __syncthreads();
     }
+}
+
+}  // namespace oom
+extern "C" int oom_moe_plan(const int32_t* ids, int T, int E, int k, const uint64_t* all_recs, int32_t* plan,
+                            uint64_t* recs, void* stream);
+namespace oom {
+
+// ---- the plan over many blocks (large steps, E <= PLAN_FAST_E) -------------------------
+//
+// The same plan in two launches, for steps whose slots would keep one block busy: block b
+// of 4 waves owns the slots [b C, b C + C) (C a multiple of 256; wave w the quarter
+// [b C + w C / 4, + C / 4)). plan_count_kernel counts each id over the block's slots (the
+// ballot matching above, per-wave rows in LDS) and stores the block's counts and an
+// invalid-id flag, counts[b][0 .. E) and counts[b][E]. plan_place_kernel reads every
+// block's counts: expert e's first position is the assignments of the experts below it,
+// block b's first position for e adds the blocks before it, and wave w's the waves before
+// it in the block (counted again); block 0 writes the plan's header. Slots keep slot order
+// inside each expert, as the single-block kernel's.
+constexpr int PM_WAVES = 4;
+constexpr int PM_THREADS = 64 * PM_WAVES;
+
+// Peers of this lane's id e in the wave (e < 0: none), its rank among them, their number.
+__device__ __forceinline__ int plan_match(int e, int nbits, uint64_t below, int& rank) {
+    uint64_t peers = __ballot(e >= 0);
+    for (int b = 0; b < nbits; b++) {
+        const uint64_t bal = __ballot(e >= 0 && ((e >> b) & 1));
+        peers &= ((e >> b) & 1) ? bal : ~bal;
+    }
+    rank = (int)__builtin_popcountll(peers & below);
+    return (int)__builtin_popcountll(peers);
+}
+
+// This wave's per-id counts over its slots [s0, s1) into wcnt (E ints); returns whether an
+// id was out of range.
+__device__ bool plan_wave_count(const int32_t* __restrict__ ids, int s0, int s1, int E, int* wcnt) {
+    const int lane = threadIdx.x & 63;
+    const int nbits = 32 - __builtin_clz((unsigned)max(E - 1, 1));
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    bool bad = false;
+    for (int b0 = s0; b0 < s1; b0 += 64 * PLAN_PB) {
+        int eb[PLAN_PB];
+#pragma unroll
+        for (int r = 0; r < PLAN_PB; r++) {
+            const int sl = b0 + 64 * r + lane;
+            eb[r] = sl < s1 ? ids[sl] : -1;
+        }
+#pragma unroll
+        for (int r = 0; r < PLAN_PB; r++) {
+            if (b0 + 64 * r >= s1) break;  // wave-uniform
+            const bool in = b0 + 64 * r + lane < s1;
+            const bool ok = eb[r] >= 0 && eb[r] < E;
+            bad |= in && !ok;
+            int rank;
+            const int n = plan_match(ok ? eb[r] : -1, nbits, below, rank);
+            if (ok && rank == 0) wcnt[eb[r]] += n;
+            wave_lds_order();
+        }
+    }
+    return bad;
+}
+
+__global__ void __launch_bounds__(PM_THREADS) plan_count_kernel(const int32_t* __restrict__ ids, int A, int E, int C,
+                                                                int32_t* __restrict__ counts) {
+    extern __shared__ int lds[];  // wcnt [PM_WAVES][E]
+    __shared__ int bad_s;
+    const int tid = threadIdx.x, wave = tid >> 6, b = blockIdx.x;
+    for (int i = tid; i < PM_WAVES * E; i += PM_THREADS) lds[i] = 0;
+    if (tid == 0) bad_s = 0;
+    __syncthreads();
+    const int q = C / PM_WAVES, s0 = min(A, b * C + wave * q), s1 = min(A, s0 + q);
+    if (plan_wave_count(ids, s0, s1, E, lds + wave * E)) bad_s = 1;
+    __syncthreads();
+    int32_t* row = counts + (size_t)b * (E + 1);
+    for (int e = tid; e < E; e += PM_THREADS) {
+        int c = 0;
+#pragma unroll
+        for (int w = 0; w < PM_WAVES; w++) c += lds[w * E + e];
+        row[e] = c;
+    }
+    if (tid == 0) row[E] = bad_s;
+}
+
+__global__ void __launch_bounds__(PM_THREADS) plan_place_kernel(const int32_t* __restrict__ ids, int A, int E, int k,
+                                                                int C, int NB, const int32_t* __restrict__ counts,
+                                                                const uint64_t* __restrict__ all_recs,
+                                                                int32_t* plan_base, uint64_t* __restrict__ recs) {
+    extern __shared__ int lds[];  // pos [E] (expert e's first position for this block), wcnt [PM_WAVES][E]
+    int* pos = lds;
+    int* wcnt = lds + E;
+    __shared__ int warp_tot[PM_WAVES];
+    __shared__ int bad_s;
+    PlanView plan{plan_base, E, A};
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, b = blockIdx.x;
+    if (tid == 0) bad_s = 0;
+    for (int i = tid; i < PM_WAVES * E; i += PM_THREADS) wcnt[i] = 0;
+    __syncthreads();
+    // expert totals and this block's offsets within them: thread t owns experts
+    // [t per, t per + per), per = ceil(E / PM_THREADS)
+    const int per = (E + PM_THREADS - 1) / PM_THREADS;
+    const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+    int my_assign = 0, my_experts = 0, bad = 0;
+    for (int e = e0; e < e1; e++) {
+        int tot = 0, before = 0;
+        for (int bb = 0; bb < NB; bb++) {
+            const int c = counts[(size_t)bb * (E + 1) + e];
+            tot += c;
+            before += bb < b ? c : 0;
+        }
+        pos[e] = before;  // the block's offset inside expert e, for now
+        wcnt[e] = tot;    // (wave 0's row holds the totals until the scan is done)
+        my_assign += tot;
+        my_experts += tot > 0;
+    }
+    for (int bb = tid; bb < NB; bb += PM_THREADS) bad |= counts[(size_t)bb * (E + 1) + E];
+    if (bad) bad_s = 1;
+    int total_a, n_e;
+    int a = block_exclusive_scan(my_assign, warp_tot, total_a);  // (syncs: bad_s is visible after it)
+    int x = block_exclusive_scan(my_experts, warp_tot, n_e);
+    if (bad_s) {
+        if (b == 0 && tid == 0) *plan.n_e() = -1;
+        return;
+    }
+    for (int e = e0; e < e1; e++) {
+        const int tot = wcnt[e];
+        pos[e] += a;
+        if (b == 0 && tot > 0) {
+            plan.experts()[x] = e;
+            plan.off()[x] = a;
+            recs[x] = all_recs[e];
+            x++;
+        }
+        a += tot;
+        wcnt[e] = 0;
+    }
+    if (b == 0) {
+        for (int i = n_e + tid; i < E; i += PM_THREADS) plan.experts()[i] = -1;
+        for (int i = n_e + tid; i <= E; i += PM_THREADS) plan.off()[i] = A;
+        if (tid == 0) *plan.n_e() = n_e;
+    }
+    __syncthreads();
+    // the waves' own counts, then each wave's first position per id
+    const int q = C / PM_WAVES, s0 = min(A, b * C + wave * q), s1 = min(A, s0 + q);
+    plan_wave_count(ids, s0, s1, E, wcnt + wave * E);
+    __syncthreads();
+    for (int e = tid; e < E; e += PM_THREADS) {
+        int acc = pos[e];
+#pragma unroll
+        for (int w = 0; w < PM_WAVES; w++) {
+            const int c = wcnt[w * E + e];
+            wcnt[w * E + e] = acc;
+            acc += c;
+        }
+    }
+    __syncthreads();
+    // place the wave's slots in order
+    const int nbits = 32 - __builtin_clz((unsigned)max(E - 1, 1));
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    int* wpos = wcnt + wave * E;
+    for (int b0 = s0; b0 < s1; b0 += 64 * PLAN_PB) {
+        int eb[PLAN_PB];
+#pragma unroll
+        for (int r = 0; r < PLAN_PB; r++) {
+            const int sl = b0 + 64 * r + lane;
+            eb[r] = sl < s1 ? ids[sl] : -1;
+        }
+#pragma unroll
+        for (int r = 0; r < PLAN_PB; r++) {
+            if (b0 + 64 * r >= s1) break;  // wave-uniform
+            const int sl = b0 + 64 * r + lane, e = eb[r];
+            int rank;
+            const int n = plan_match(e, nbits, below, rank);
+            if (e >= 0) {
+                const int p = wpos[e] + rank;
+                plan.assign_tok()[p] = sl / k;
+                plan.slot_assign()[sl] = p;
+            }
+            wave_lds_order();  // every lane has read the position before the leader advances it
+            if (e >= 0 && rank == 0) wpos[e] += n;
+            wave_lds_order();
+        }
+    }
+}
+
+// Slots a block of the two-launch plan takes, and its block count (at most 64).
+static int plan_multi_chunk(int A) { return std::max(1024, (int)((cdiv((int64_t)A, 64) + 255) / 256 * 256)); }
+size_t plan_multi_counts(int A, int E) {
+    const int C = plan_multi_chunk(A);
+    return (size_t)cdiv((int64_t)A, C) * (E + 1);
+}
+int launch_plan_multi(const int32_t* ids, int T, int E, int k, const uint64_t* all_recs, int32_t* plan, uint64_t* recs,
+                      int32_t* counts, hipStream_t st) {
+    if (E > PLAN_FAST_E) return oom_moe_plan(ids, T, E, k, all_recs, plan, recs, st);
+    const int A = T * k, C = plan_multi_chunk(A), NB = (int)cdiv((int64_t)A, C);
+    hipLaunchKernelGGL(plan_count_kernel, dim3(NB), dim3(PM_THREADS), PM_WAVES * E * sizeof(int), st, ids, A, E, C,
+                       counts);
+    if (int rc = launched("oom_moe_plan")) return rc;
+    hipLaunchKernelGGL(plan_place_kernel, dim3(NB), dim3(PM_THREADS), (PM_WAVES + 1) * E * sizeof(int), st, ids, A, E,
+                       k, C, NB, counts, all_recs, plan, recs);
+    return launched("oom_moe_plan");
 }
 
 }  // namespace oom

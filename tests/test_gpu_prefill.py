@@ -201,6 +201,16 @@ def prefill_check(hip, geo, recs, logits, xb, k, sample=None, precision=None):
     st = prefill_workspace(ws, T, E, k, H, I)
     ids_all, _ = oracle.router_topk(logits, k)
     experts, off, tok, slot = oracle.moe_plan(ids_all, E)
+    # the step's device plan (built over many blocks at large steps), entry for entry
+    A, pl = T * k, st["plan"]
+    n_e = int(pl[0])
+    assert n_e == len(experts)
+    np.testing.assert_array_equal(pl[1:1 + n_e], experts)
+    assert np.all(pl[1 + n_e:1 + E] == -1)
+    np.testing.assert_array_equal(pl[1 + E:2 + E + n_e], off)
+    assert np.all(pl[2 + E + n_e:2 + 2 * E] == A)
+    np.testing.assert_array_equal(pl[2 + 2 * E:2 + 2 * E + A], tok)
+    np.testing.assert_array_equal(pl[2 + 2 * E + A:2 + 2 * E + 2 * A], slot)
     # x codes and scales of the sampled tokens
     xq_or, xs_or = oracle.quantize_act(x[rows])
     np.testing.assert_array_equal(st["xq"][rows], xq_or)
