@@ -11,22 +11,22 @@
 // weight's 128 x 128 block scale (and, for per-group activations, the row's group
 // scale) before it joins the accumulator.
 //
-//  * A block takes a 128-assignment x 128-output tile of one expert (8 waves, each
-//    32 x 64); per K step of 128 the block stages the activation rows (gathered by
-//    assignment) and the weight rows in LDS (rows padded to 144 bytes), and the next
-//    step's global loads are in flight while the current step runs on the matrix cores.
-//  * The prefill step's gate/up pass takes 256-assignment tiles instead
-//    (grouped_gate_up256_kernel, two LDS stages of 64 KiB).
-//  * Gate/up: both weight tiles share the activation tile; the epilogue forms
+//  * oom_moe_grouped_gemm_fp8: a block takes a 128-assignment x 128-output tile of one
+//    expert (8 waves, each 32 x 64); per K step of 128 the block stages the activation rows
+//    (gathered by assignment) and the weight rows in LDS (16-byte chunks, swizzled), and the
+//    next step's loads are in flight while the current step runs on the matrix cores.
+//  * The prefill's gate/up pass (grouped_gate_up256_kernel): 256 assignments x 128 gate and
+//    128 up rows, both weight tiles sharing the activation tile; the epilogue forms
 //    h = silu(g) * u and writes hi = bf16(h) and, for the exact precision, lo =
 //    bf16(h - hi) (16 significant bits, relative error <= 2^-17): h is not quantised
 //    again. The two precisions are the reference's (ExpertPrecision,
 //    crates/oominf-core/src/backend.rs:142-149): Bf16 rounds the activations to bf16 for
 //    one matrix-core pass, Exact keeps them fp32 (crates/oominf-cuda/kernels/moe.cu:166-335
 //    splits them into exact bf16 terms the same way).
-//  * Down: A = the h term planes, B = e4m3 weight rows converted exactly to bf16 in
-//    registers; every term runs on the bf16 matrix cores, fp32 accumulate, the weight's
-//    128 x 128 block scale applied to each 128-column block sum.
+//  * The prefill's down pass (grouped_down512_kernel): 128 assignments x 512 outputs, A =
+//    the h term planes, B = e4m3 weight rows converted exactly to bf16 in registers; every
+//    term runs on the bf16 matrix cores, fp32 accumulate, the weight's 128 x 128 block
+//    scale applied to each block sum.
 #include <algorithm>
 
 #include "router.hpp"
@@ -260,10 +260,6 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, void* lds, int of
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 4, off, 0, 0, 0);
 }
 
-// Loads a wave issues per stage (every wave the same number, so one wait count fits all).
-template <int NB>
-constexpr int g_loads_per_stage() { return 2 + 2 * NB + 2; }
-
 // s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding): this wave's loads but the newest n have
 // completed, and its LDS accesses.
 template <int N>
@@ -369,53 +365,26 @@ __device__ __forceinline__ void g_step(const uint8_t* sb, const float* scx, cons
         }
 }
 
-// MODE 0: y = scaled xq . W^T. MODE 1: gate and up (NB = 2), h = silu(g) * u quantised.
+// y = scaled xq . W^T (oom_moe_grouped_gemm_fp8).
 //
-// K steps stream through LDS stage buffers filled by direct-to-LDS buffer loads. Three
-// buffers (gate/up: one block per CU): at step kb a wave waits for its own loads of stage
-// kb (kb + 1's may still be in flight), the block synchronises (every wave's loads of kb
-// have landed, and every wave is done reading the buffer stage kb + 2 takes), stage
-// kb + 2 is issued, and step kb runs on the matrix cores while kb + 1 and kb + 2 load.
-// Two buffers (down: two blocks per CU, which overlap each other's waits): stage kb + 1
-// is issued at step kb.
-//
-// Tiles from the device tile table go to XCDs in runs: the hardware sends block L (x
-// fastest) to XCD L % 8, and XCD x takes work items x C .. x C + C of the W = NT * MT
-// (N-tile, table tile) items, table tile fastest. So the blocks an XCD runs together walk
-// the M-tiles of one N-tile, and an expert's weight tile is fetched once and then served
-// from that XCD's L2.
-template <int MODE>
+// K steps stream through two LDS stage buffers filled by direct-to-LDS buffer loads (two
+// blocks per CU, which overlap each other's waits): at step kb a wave waits for its own
+// loads of stage kb, the block synchronises (every wave's loads of kb have landed, and
+// every wave is done reading the buffer stage kb + 1 takes), stage kb + 1 is issued, and
+// step kb runs on the matrix cores while kb + 1 loads. Grid (N / 128, M-tiles, experts).
 __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
-    constexpr int NB = MODE == 1 ? 2 : 1;
-    constexpr int NST = MODE == 1 ? 3 : 2;               // LDS stage buffers
-    constexpr int SBYTES = GBM * GBK + NB * GBN * GBK;  // one stage: A tile and NB B tiles
-    constexpr int LPS = g_loads_per_stage<NB>();
+    constexpr int NB = 1;
+    constexpr int SBYTES = GBM * GBK + NB * GBN * GBK;  // one stage: the A tile and the B tile
     // each stage its own LDS object: the compiler's wait for direct-to-LDS loads then
     // covers only the loads into the buffer a read touches
-    // a stage: the A tile, NB B tiles, then the activation and weight scales (64 words per
+    // a stage: the A tile, the B tile, then the activation and weight scales (64 words per
     // wave each)
     constexpr int STOT = SBYTES + 2 * GTHREADS * 4;
-    __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT], sb2[NST == 3 ? STOT : 16];
+    __shared__ __align__(16) uint8_t sb0[STOT], sb1[STOT];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;  // rows 32 wm .. + 32, columns 64 wn .. + 64
-    // ---- which tile ----
-    int i, m0, n0;
-    if (g.tiles) {
-        const int NT = (int)gridDim.x, MT = *g.ntiles, W = NT * MT;
-        const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x), C = (W + 7) / 8;
-        if ((L >> 3) >= C) return;
-        const int w = (L & 7) * C + (L >> 3);
-        if (w >= W) return;
-        const int nt = w / MT, mt = w - nt * MT;
-        i = g.tiles[2 * mt];
-        m0 = g.tiles[2 * mt + 1];
-        n0 = nt * GBN;
-    } else {
-        i = blockIdx.z;
-        m0 = blockIdx.y * GBM;
-        n0 = blockIdx.x * GBN;
-    }
+    const int i = blockIdx.z, m0 = blockIdx.y * GBM, n0 = blockIdx.x * GBN;
     const int a0 = g.off[i], a1 = g.off[i + 1];
     if (a0 + m0 >= a1) return;
     const int Lb = (int)(blockIdx.x + blockIdx.y * gridDim.x);
@@ -472,30 +441,20 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
                 for (int e = 0; e < 4; e++) acc[m][ms][ns][e] = 0.0f;
 #define G_SX(B) reinterpret_cast<float*>((B) + SBYTES)
 #define G_SW(B) reinterpret_cast<float*>((B) + SBYTES + GTHREADS * 4)
-    // one step on stage buffer SB while stage kb + NST - 1 goes into NSB (WAIT: this
-    // wave's loads newer than stage kb, which may still be in flight)
-#define G_STEP(SB, NSB, WAIT)                                                                       \
+    // one step on stage buffer SB while stage kb + 1 goes into NSB
+#define G_STEP(SB, NSB)                                                                             \
     {                                                                                               \
-        wait_vm<WAIT>();                                                                            \
+        wait_vm<0>();                                                                               \
         g_barrier();                                                                                \
-        g_issue<NB>(src, kb + NST - 1, nkb, NSB, G_SX(NSB), G_SW(NSB), wave);                       \
+        g_issue<NB>(src, kb + 1, nkb, NSB, G_SX(NSB), G_SW(NSB), wave);                             \
         if (act > 0) g_step<NB>(SB, G_SX(SB), G_SW(SB), xgrp, wm, wn, wave, lane, act, acc);        \
         if (++kb == nkb) break;                                                                     \
     }
     int kb = 0;
     g_issue<NB>(src, 0, nkb, sb0, G_SX(sb0), G_SW(sb0), wave);
-    if constexpr (NST == 3) {
-        g_issue<NB>(src, 1, nkb, sb1, G_SX(sb1), G_SW(sb1), wave);
-        for (;;) {
-            G_STEP(sb0, sb2, LPS)
-            G_STEP(sb1, sb0, LPS)
-            G_STEP(sb2, sb1, LPS)
-        }
-    } else {
-        for (;;) {
-            G_STEP(sb0, sb1, 0)
-            G_STEP(sb1, sb0, 0)
-        }
+    for (;;) {
+        G_STEP(sb0, sb1)
+        G_STEP(sb1, sb0)
     }
 #undef G_SX
 #undef G_SW
@@ -503,39 +462,19 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     wait_vm<0>();  // the zero-filled stages past the end have landed before LDS is reused
     __syncthreads();
     // ---- epilogue ----
-    if constexpr (MODE == 0) {
 #pragma unroll
-        for (int ms = 0; ms < 2; ms++)
+    for (int ms = 0; ms < 2; ms++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int a = arow_out[ms][e];
-                if (a >= a1) continue;
-                const float xsr = g.x_group ? 1.0f : g.xs[g.rows ? g.rows[a] : a];
+        for (int e = 0; e < 4; e++) {
+            const int a = arow_out[ms][e];
+            if (a >= a1) continue;
+            const float xsr = g.x_group ? 1.0f : g.xs[g.rows ? g.rows[a] : a];
 #pragma unroll
-                for (int ns = 0; ns < 4; ns++) {
-                    const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
-                    if (n < g.N) g.y[(int64_t)a * g.N + n] = g.x_group ? acc[0][ms][ns][e] : acc[0][ms][ns][e] * xsr;
-                }
+            for (int ns = 0; ns < 4; ns++) {
+                const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
+                if (n < g.N) g.y[(int64_t)a * g.N + n] = g.x_group ? acc[0][ms][ns][e] : acc[0][ms][ns][e] * xsr;
             }
-    } else {
-        // h = silu(xs g) * (xs u) as two bf16 terms: hi = bf16(h), lo = bf16(h - hi)
-#pragma unroll
-        for (int ms = 0; ms < 2; ms++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int a = arow_out[ms][e];
-                if (a >= a1) continue;
-                const float xsr = g.xs[g.rows ? g.rows[a] : a];
-#pragma unroll
-                for (int ns = 0; ns < 4; ns++) {
-                    const float h = siluf(acc[0][ms][ns][e] * xsr) * (acc[1][ms][ns][e] * xsr);
-                    const uint16_t hi = f32_to_bf16(h);
-                    const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
-                    g.hh[(int64_t)a * g.N + n] = hi;
-                    if (g.hl) g.hl[(int64_t)a * g.N + n] = f32_to_bf16(h - bf16_to_f32(hi));
-                }
-            }
-    }
+        }
     G_STAMP_END(g, Lb);
 }
 
@@ -1020,9 +959,8 @@ __global__ void __launch_bounds__(GTHREADS) grouped_down512_kernel(GArgs g) {
 
 // ---- host side -----------------------------------------------------------------------
 
-int launch_grouped(const GArgs& a, int mode, dim3 grid, hipStream_t st) {
-    if (mode == 1) hipLaunchKernelGGL(grouped_gemm_kernel<1>, grid, dim3(GTHREADS), 0, st, a);
-    else hipLaunchKernelGGL(grouped_gemm_kernel<0>, grid, dim3(GTHREADS), 0, st, a);
+int launch_grouped(const GArgs& a, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL(grouped_gemm_kernel, grid, dim3(GTHREADS), 0, st, a);
     return launched("grouped_gemm_fp8");
 }
 
@@ -1139,7 +1077,7 @@ extern "C" int oom_moe_grouped_gemm_fp8(const uint64_t* recs, const int32_t* off
     a.s2_off = s_off;
     a.y = y;
     dim3 grid((unsigned)(N / GBN), (unsigned)cdiv(max_per_expert, GBM), (unsigned)n_experts);
-    return launch_grouped(a, 0, grid, as_stream(stream));
+    return launch_grouped(a, grid, as_stream(stream));
 }
 
 extern "C" size_t oom_moe_prefill_fp8_workspace_size(int T, int E, int k, const OomFp8Record* geo) {
