@@ -911,7 +911,7 @@ def bench_nvfp4(args):
                    "distinct_experts_per_step": distinct},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
                      "traffic": measured_traffic("nvfp4"),
-                     "kernel": "moe_decode_nvfp4_1_kernel (oom_moe_decode_nvfp4, one launch for one token)",
+                     "kernel": "moe_decode_nvfp4_1p_kernel (oom_moe_decode_nvfp4, one launch for one token)",
                      "algorithmic_bytes_per_step": bytes_step, "copy_gbs": copy_bandwidth(torch)},
     }
     if not args.no_cpu:

@@ -91,9 +91,10 @@ __device__ __forceinline__ uint32_t ldb(__amdgpu_buffer_rsrc_t r, int off) {
 __device__ __forceinline__ float e4m3_byte(uint32_t b) { return __builtin_amdgcn_cvt_f32_fp8((int)b, 0); }
 
 // Stages rows row_of(t) (t < nb) of src (width K, element type DT) into LDS in the lane
-// order above; zeros past K and for t >= nb.
+// order above; zeros past K and for t >= nb. 256 threads take part, thread ti of them.
 template <int DT, typename RowOf>
-__device__ __forceinline__ void stage4(float4* xs4, const void* src, int K, int CH, int nb, RowOf row_of) {
+__device__ __forceinline__ void stage4(float4* xs4, const void* src, int K, int CH, int nb, RowOf row_of,
+                                       int ti = (int)threadIdx.x) {
     constexpr int EPL = DT == OOM_BF16 ? 8 : 4;  // elements per 16-byte load
     constexpr int ES = DT == OOM_BF16 ? 2 : 4;
     const int span = CH * 1024, nvec = N4_TB * span / EPL;
@@ -101,7 +102,7 @@ __device__ __forceinline__ void stage4(float4* xs4, const void* src, int K, int 
         uint4 v[4];
 #pragma unroll
         for (int n = 0; n < 4; n++) {
-            const int i = base + (int)threadIdx.x + 256 * n;
+            const int i = base + ti + 256 * n;
             const int t = i * EPL / span, kk = i * EPL - t * span;
             const bool ok = i < nvec && t < nb && kk < K;
             v[n] = ok ? *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(src) +
@@ -110,7 +111,7 @@ __device__ __forceinline__ void stage4(float4* xs4, const void* src, int K, int 
         }
 #pragma unroll
         for (int n = 0; n < 4; n++) {
-            const int i = base + (int)threadIdx.x + 256 * n;
+            const int i = base + ti + 256 * n;
             if (i >= nvec) break;
             const int t = i * EPL / span, kk = i * EPL - t * span;
             const int c = kk >> 10, l = (kk & 1023) >> 5, j = kk & 31;
@@ -189,21 +190,30 @@ __device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amd
                 float sg[2], su[2];
 #pragma unroll
                 for (int q = 0; q < 2; q++) {
-                    const bool okq = (col >> 4) + q < hg;  // a group past the row's end scales to 0
-                    sg[q] = okq ? e4m3_byte(bg[p][c][q]) * s2g : 0.0f;
-                    su[q] = okq ? e4m3_byte(bu[p][c][q]) * s2u : 0.0f;
+                    // a group past the row's end scales to 0 (its byte read as 0); the select
+                    // is on scale_2, so the byte's load is used on every lane and stays where
+                    // it was issued (a select on the product let the compiler move the load
+                    // into a branch, whose wait then covered every load in flight)
+                    const bool okq = (col >> 4) + q < hg;
+                    sg[q] = e4m3_byte(bg[p][c][q]) * (okq ? s2g : 0.0f);
+                    su[q] = e4m3_byte(bu[p][c][q]) * (okq ? s2u : 0.0f);
                 }
-                float fg[32], fu[32];
-                e2m1x32(wg[p][c], fg);
-                e2m1x32(wu[p][c], fu);
+                // the gate piece, then the up piece: one set of 32 decoded weights at a time
+                float f[32];
+                e2m1x32(wg[p][c], f);
 #pragma unroll
                 for (int t = 0; t < TB; t++) {
-                    float g0, g1, u0, u1;
-                    piece_dot(fg, xs4, t, CH, c0 + c, l, g0, g1);
-                    piece_dot(fu, xs4, t, CH, c0 + c, l, u0, u1);
+                    float g0, g1;
+                    piece_dot(f, xs4, t, CH, c0 + c, l, g0, g1);
                     float& ag = acc[(0 * TB + t) * N4_GP + p];
-                    float& au = acc[(1 * TB + t) * N4_GP + p];
                     ag = fmaf(g1, sg[1], fmaf(g0, sg[0], ag));
+                }
+                e2m1x32(wu[p][c], f);
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    float u0, u1;
+                    piece_dot(f, xs4, t, CH, c0 + c, l, u0, u1);
+                    float& au = acc[(1 * TB + t) * N4_GP + p];
                     au = fmaf(u1, su[1], fmaf(u0, su[0], au));
                 }
             }
@@ -281,7 +291,7 @@ __device__ __forceinline__ void dn4_pass(const float4* xs4, const Rec4& g, __amd
             for (int p = 0; p < N4_DP; p++) {
                 float sd[2];
 #pragma unroll
-                for (int q = 0; q < 2; q++) sd[q] = (col >> 4) + q < ig ? e4m3_byte(bd[p][c][q]) * s2 : 0.0f;
+                for (int q = 0; q < 2; q++) sd[q] = e4m3_byte(bd[p][c][q]) * ((col >> 4) + q < ig ? s2 : 0.0f);
                 float f[32];
                 e2m1x32(wd[p][c], f);
 #pragma unroll
@@ -383,17 +393,22 @@ struct Fused4Args {
 
 // Rows 0 .. rows - 1 of h (f32, width K) into LDS in stage4's lane order through
 // device-coherent 16-byte loads, eight in flight per thread (one round for 10 rows of 640:
-// each round costs a trip to the device's point of coherence); zeros past K.
+// each round costs a trip to the device's point of coherence); zeros past K. NT threads.
+// Every load's value is stored, a load past the rows into one spare LDS slot: with a store
+// under a branch the compiler moved each load into its branch, behind a wait for the one
+// before (eight round trips instead of one).
+template <int NT = 256>
 __device__ __forceinline__ void stage_rows_dev(float4* xs4, const float* h, int K, int CH, int rows) {
     constexpr int R = 8;  // loads in flight per thread
+    __shared__ float4 spare;
     const int span = CH * 1024, nvec = rows * span / 4;
     const __amdgpu_buffer_rsrc_t hr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(h), (short)0, rows * K * 4, BUF_FLAGS);
-    for (int base = 0; base < nvec; base += 256 * R) {
+    for (int base = 0; base < nvec; base += NT * R) {
         uint4 v[R];
 #pragma unroll
         for (int n = 0; n < R; n++) {
-            const int i = base + (int)threadIdx.x + 256 * n;
+            const int i = base + (int)threadIdx.x + NT * n;
             const int t = i * 4 / span, kk = i * 4 - t * span;
             const auto q = __builtin_amdgcn_raw_buffer_load_b128(hr, i < nvec && kk < K ? (t * K + kk) * 4 : OOB, 0,
                                                                  BUF_SC1);
@@ -401,12 +416,12 @@ __device__ __forceinline__ void stage_rows_dev(float4* xs4, const float* h, int 
         }
 #pragma unroll
         for (int n = 0; n < R; n++) {
-            const int i = base + (int)threadIdx.x + 256 * n;
-            if (i >= nvec) break;
+            const int i = base + (int)threadIdx.x + NT * n;
             const int t = i * 4 / span, kk = i * 4 - t * span;
             const int c = kk >> 10, l = (kk & 1023) >> 5, j = kk & 31;
-            xs4[((t * CH + c) * 8 + (j >> 2)) * 32 + l] = make_float4(__uint_as_float(v[n].x), __uint_as_float(v[n].y),
-                                                                      __uint_as_float(v[n].z), __uint_as_float(v[n].w));
+            float4* dst = i < nvec ? &xs4[((t * CH + c) * 8 + (j >> 2)) * 32 + l] : &spare;
+            *dst = make_float4(__uint_as_float(v[n].x), __uint_as_float(v[n].y), __uint_as_float(v[n].z),
+                               __uint_as_float(v[n].w));
         }
     }
 }
@@ -456,7 +471,7 @@ __device__ __forceinline__ void dn4_compute(const Dn4W& w, const float4* xs4, co
         for (int p = 0; p < N4_DP; p++) {
             float sd[2];
 #pragma unroll
-            for (int q = 0; q < 2; q++) sd[q] = (col >> 4) + q < ig ? e4m3_byte(w.bd[p][c][q]) * w.s2 : 0.0f;
+            for (int q = 0; q < 2; q++) sd[q] = e4m3_byte(w.bd[p][c][q]) * ((col >> 4) + q < ig ? w.s2 : 0.0f);
             float f[32];
             e2m1x32(w.wd[p][c], f);
             float p0, p1;
@@ -568,6 +583,180 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     grid_barrier_exit(a.bar);
 }
 
+// ---- one token in one launch, one block per CU -----------------------------------------------
+// The step above for hidden <= 3072 and inter <= 1024 (the released geometry: 2560 / 640),
+// with the same arithmetic and another schedule:
+//   - blocks of 8 waves, one a CU; wave w of block b takes the items (slot, 2 N4_GP rows)
+//     b + G (w + 8 n), so every block holds 6 or 7 of the step's 1600 items;
+//   - block b's output tile is rows 10 b .. + 10 (2560 outputs over 256 blocks); its (slot,
+//     row pair) units are u = w + 8 m of wave w, and the first N4P_UP of them load into
+//     registers before the wave's gate/up loads (a prefetch issued behind them would make
+//     the item's waits count it only on some paths), so the down weights stream in phase 1
+//     and after the barrier a block only stages h;
+//   - a unit's lane partial and the 32-lane butterfly are dn4_compute's, so the outputs equal
+//     the staged launches' bit for bit. Units past N4P_UP (k > 11) and tiles past the grid
+//     load after the barrier.
+constexpr int N4P_WAVES = 8;  // waves per block
+constexpr int N4P_DP = 5;     // row pairs of a block's output tile
+constexpr int N4P_UP = 7;     // units a wave prefetches in phase 1 (k * N4P_DP <= 8 * 7 with k <= 11)
+
+// A unit of a down tile (inter <= 1024: one 1024-column chunk): lane l of half `half` holds
+// row r0 + 2 p + half's columns 32 (l % 32) .. + 32, their two scale bytes and the record's
+// weight_scale_2.
+struct Dn4U {
+    uint4 wd;
+    uint32_t bd[2];
+    float s2;
+};
+
+__device__ __forceinline__ void dnu_load(Dn4U& w, const Rec4& g, __amdgpu_buffer_rsrc_t r, int row, int lane) {
+    const int I = g.I, ig = I >> 4, col = 32 * (lane & 31);
+    const bool ok = row < g.H && col < I;
+    w.wd = ld16(r, ok ? g.dw + row * (I >> 1) + (col >> 1) : OOB);
+#pragma unroll
+    for (int q = 0; q < 2; q++) w.bd[q] = ldb(r, ok && (col >> 4) + q < ig ? g.ds + row * ig + (col >> 4) + q : OOB);
+    w.s2 = ldf(r, g.s2d);
+}
+
+// The unit's lane partial against the slot's staged h row (dn4_compute's per-lane sum for one chunk).
+__device__ __forceinline__ float dnu_part(const Dn4U& w, const float4* hs4, int I, int lane) {
+    const int ig = I >> 4, l = lane & 31, col = 32 * l;
+    float sd[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) sd[q] = e4m3_byte(w.bd[q]) * ((col >> 4) + q < ig ? w.s2 : 0.0f);
+    float f[32];
+    e2m1x32(w.wd, f);
+    float p0, p1;
+    piece_dot(f, hs4, 0, 1, 0, l, p0, p1);
+    return fmaf(p1, sd[1], fmaf(p0, sd[0], 0.0f));
+}
+
+template <int XDT, int EQ, int ODT>
+__global__ void __launch_bounds__(64 * N4P_WAVES) moe_decode_nvfp4_1p_kernel(Fused4Args a) {
+    const uint32_t bbase = grid_barrier_base(a.bar);
+    extern __shared__ float4 xs4[];
+    __shared__ uint64_t recs_l[N4F_KMAX];
+    __shared__ float w_l[N4F_KMAX];
+    __shared__ uint64_t pk_keys[N4F_KMAX];  // routing scratch (route_picks)
+    __shared__ int pk_ids[N4F_KMAX];
+    __shared__ float pk_p[N4F_KMAX];
+    __shared__ float ylds[N4F_KMAX][2 * N4P_DP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = lane >> 5, l = lane & 31;
+    const Rec4& g = a.g;
+    const int k = a.k, H = g.H, I = g.I;
+    OOM_STAMP(a.stamps, N4P_WAVES, 0);
+    OOM_STAMP_WHERE(a.stamps, N4P_WAVES);
+    if (wave == 0) {
+        // the record addresses (lane l holds experts l + 64 q) load beside the logits
+        uint64_t rr[EQ];
+#pragma unroll
+        for (int q = 0; q < EQ; q++) rr[q] = lane + 64 * q < a.E ? a.all_recs[lane + 64 * q] : 0ull;
+        int id = 0;
+        float w = 0.0f;
+        route_picks<EQ>(a.logits, a.E, k, lane, pk_keys, pk_ids, pk_p, id, w);
+        uint64_t rec = 0;
+#pragma unroll
+        for (int q = 0; q < EQ; q++) {
+            const uint64_t v = (uint64_t)__shfl((long long)rr[q], id & 63, 64);
+            if ((id >> 6) == q) rec = v;
+        }
+        OOM_STAMP_AFTER(a.stamps, N4P_WAVES, 1, rec);  // routed (wave 0)
+        if (lane < k) {
+            recs_l[lane] = rec;
+            w_l[lane] = w;
+            if (blockIdx.x == 0) {
+                a.ids[lane] = id;
+                a.weights[lane] = w;
+            }
+        }
+    }
+    if (wave >= 4) stage4<XDT>(xs4, a.x, H, (H + 1023) >> 10, 1, [](int) { return 0; }, tid - 256);
+    __syncthreads();
+    OOM_STAMP(a.stamps, N4P_WAVES, 2);  // x staged, the picks shared
+    const int G = gridDim.x, b = blockIdx.x;
+    const int ipe = (I + 2 * N4_GP - 1) / (2 * N4_GP), NG = k * ipe;
+    const int tiles = (H + 2 * N4P_DP - 1) / (2 * N4P_DP), NU = k * N4P_DP;
+    // a slot past k loads through an empty resource: zeros, no memory access
+    const auto rsrc_of = [&](int s) { return uniform_rsrc(recs_l[s < k ? s : 0], s < k ? g.bytes : 0); };
+    Dn4U du[N4P_UP];
+    const auto prefetch = [&]() {  // (one call)
+#pragma unroll
+        for (int m = 0; m < N4P_UP; m++) {
+            const int u = wave + N4P_WAVES * m, s = u / N4P_DP, p = u - s * N4P_DP;
+            const bool ok = b < tiles && u < NU;
+            dnu_load(du[m], g, rsrc_of(ok ? s : k), b * 2 * N4P_DP + 2 * p + half, lane);
+        }
+    };
+    // ---- phase 1: the down prefetch, then items b + G (wave + 8 n) ----
+    prefetch();
+    for (int it = b + G * wave; it < NG; it += G * N4P_WAVES) {
+        const int s = it / ipe, j0 = (it - s * ipe) * 2 * N4_GP;
+        const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs_l[s], g.bytes);
+        const float s2g = ldf(r, g.s2g), s2u = ldf(r, g.s2u);
+        float* hs = a.h + (size_t)s * I;
+        gu4_pass<1, 3>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
+    }
+    OOM_STAMP(a.stamps, N4P_WAVES, 3);  // gate/up items done, the down units loaded
+    wait_mem();  // this wave's h stores are complete before its block arrives
+    grid_barrier_words(a.bar, bbase, a.status, a.spin);
+    OOM_STAMP(a.stamps, N4P_WAVES, 4);  // the grid barrier released
+    // ---- phase 2: the k h rows once, the units' rows into LDS, the slot-order combine ----
+    stage_rows_dev<64 * N4P_WAVES>(xs4, a.h, I, 1, k);
+    __syncthreads();
+    OOM_STAMP(a.stamps, N4P_WAVES, 5);  // h staged
+    const auto put_unit = [&](int u, int r0, float tot) {
+        const int s = u / N4P_DP, p = u - s * N4P_DP;
+        if (r0 + 2 * p + half < H) ylds[s][2 * p + half] = tot;
+    };
+    const auto combine = [&](int r0) {
+        const int row = r0 + tid;
+        if (tid < 2 * N4P_DP && row < H) {
+            float acc = 0.0f;
+            for (int s = 0; s < k; s++) acc = fmaf(w_l[s], ylds[s][tid], acc);
+            store_out<ODT>(a.out, row, acc);
+        }
+    };
+    // units loaded after the barrier, one at a time
+    const auto late_units = [&](int u0, int r0) {
+        for (int u = u0; u < NU; u += N4P_WAVES) {
+            const int s = u / N4P_DP, p = u - s * N4P_DP;
+            Dn4U d;
+            dnu_load(d, g, rsrc_of(s), r0 + 2 * p + half, lane);
+            float v[1] = {dnu_part(d, xs4 + (size_t)s * 256, I, lane)};
+            const float tot = wave_sum_multi<1, 16>(v, lane);
+            if (l == 0) put_unit(u, r0, tot);
+        }
+    };
+    if (b < tiles) {
+        const int r0 = b * 2 * N4P_DP;
+        constexpr int NV = 8;  // N4P_UP values (and one zero) in the butterfly
+        static_assert(N4P_UP < NV, "one butterfly for the prefetched units");
+        float v[NV];
+#pragma unroll
+        for (int m = 0; m < NV; m++) {
+            const int u = wave + N4P_WAVES * m;
+            v[m] = m < N4P_UP && u < NU ? dnu_part(du[m < N4P_UP ? m : 0], xs4 + (size_t)(u / N4P_DP) * 256, I, lane)
+                                        : 0.0f;
+        }
+        const float tot = wave_sum_multi<NV, 16>(v, lane);
+        const int m = l / (32 / NV), u = wave + N4P_WAVES * m;
+        if (l % (32 / NV) == 0 && m < N4P_UP && u < NU) put_unit(u, r0, tot);
+        late_units(wave + N4P_WAVES * N4P_UP, r0);
+        __syncthreads();
+        combine(r0);
+        OOM_STAMP(a.stamps, N4P_WAVES, 6);  // the tile combined
+    }
+    // tiles past the grid: their units load after the barrier
+    for (int tb = b + G; tb < tiles; tb += G) {
+        __syncthreads();  // the last tile's combine has read ylds
+        late_units(wave, tb * 2 * N4P_DP);
+        __syncthreads();
+        combine(tb * 2 * N4P_DP);
+    }
+    grid_barrier_exit(a.bar);
+}
+
 // LDS of the one-launch kernel: x staged for one token, then the k h rows.
 static size_t fused4_lds(const OomNvfp4Record& g, int k) {
     return std::max(stage_lds(g.hidden), (size_t)k * cdiv(g.inter, 1024) * 1024 * sizeof(float));
@@ -578,39 +767,47 @@ static bool fused4_ok(int T, int E, int k, const OomNvfp4Record& g) {
            (int64_t)k * g.inter * 4 < OOB;
 }
 
-template <int XDT, int EQ, int ODT>
+// The one-block-per-CU kernel's limits (beyond fused4_ok's): three chunks of hidden, one of inter.
+static bool fused4p_ok(int H, int I) { return H <= 3072 && I <= 1024; }
+
+// P: the one-block-per-CU kernel (8 waves), else the 4-wave kernel.
+template <bool P, int XDT, int EQ, int ODT>
 static int launch_fused4_t(const Fused4Args& a, size_t lds, hipStream_t st) {
     static thread_local int cached_dev = -1, cached_blocks = 0;
     static thread_local size_t cached_lds = 0;
+    const auto kernel = P ? moe_decode_nvfp4_1p_kernel<XDT, EQ, ODT> : moe_decode_nvfp4_1_kernel<XDT, EQ, ODT>;
+    const int threads = P ? 64 * N4P_WAVES : 64 * N4_WAVES;
     int dev = 0;
     (void)hipGetDevice(&dev);
     if (dev != cached_dev || lds != cached_lds) {
         int cus = 0, per = 0;
         cached_blocks = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, moe_decode_nvfp4_1_kernel<XDT, EQ, ODT>, 256, lds) ==
-                hipSuccess)
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) == hipSuccess)
             cached_blocks = cus * per;
         cached_dev = dev;
         cached_lds = lds;
     }
     if (cached_blocks <= 0) return fail(OOM_ERR_LAUNCH, "oom_moe_decode_nvfp4: occupancy query failed");
-    // enough blocks for one wave item each or one output tile each, never more than fit
-    const int64_t items = cdiv((int64_t)a.k * cdiv(a.g.I, 2 * N4_GP), N4_WAVES);
-    const int64_t tiles = cdiv(a.g.H, 2 * N4_DP);
+    // enough blocks for one item a wave or one output tile each, never more than fit
+    const int64_t items = cdiv((int64_t)a.k * cdiv(a.g.I, 2 * N4_GP), P ? N4P_WAVES : N4_WAVES);
+    const int64_t tiles = cdiv(a.g.H, P ? 2 * N4P_DP : 2 * N4_DP);
     const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(cached_blocks, std::max(items, tiles)));
-    hipLaunchKernelGGL((moe_decode_nvfp4_1_kernel<XDT, EQ, ODT>), dim3(blocks), dim3(256), lds, st, a);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), lds, st, a);
     return launched("oom_moe_decode_nvfp4");
 }
 
-template <int XDT, int EQ>
+template <bool P, int XDT, int EQ>
 static int launch_fused4_o(const Fused4Args& a, int odt, size_t lds, hipStream_t st) {
-    return odt == OOM_BF16 ? launch_fused4_t<XDT, EQ, OOM_BF16>(a, lds, st) : launch_fused4_t<XDT, EQ, OOM_F32>(a, lds, st);
+    return odt == OOM_BF16 ? launch_fused4_t<P, XDT, EQ, OOM_BF16>(a, lds, st)
+                           : launch_fused4_t<P, XDT, EQ, OOM_F32>(a, lds, st);
 }
 
 template <int XDT>
 static int launch_fused4_e(const Fused4Args& a, int odt, size_t lds, hipStream_t st) {
-    return a.E <= 256 ? launch_fused4_o<XDT, 4>(a, odt, lds, st) : launch_fused4_o<XDT, 8>(a, odt, lds, st);
+    if (fused4p_ok(a.g.H, a.g.I))
+        return a.E <= 256 ? launch_fused4_o<true, XDT, 4>(a, odt, lds, st) : launch_fused4_o<true, XDT, 8>(a, odt, lds, st);
+    return a.E <= 256 ? launch_fused4_o<false, XDT, 4>(a, odt, lds, st) : launch_fused4_o<false, XDT, 8>(a, odt, lds, st);
 }
 
 static int launch_gate_up4(const uint64_t* recs, const int32_t* off, const int32_t* tok, int grid_e, const void* x,

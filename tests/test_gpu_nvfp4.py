@@ -168,6 +168,7 @@ def test_decode_nvfp4_matches_oracle(hip, T, E, k, zipf, H, I, xf32):
     (64, 8, 4096, 1536, False),    # the FP8 benchmark's widths: 64 KiB of staged h rows
     (100, 16, 1040, 432, True),    # 16 slots, widths ending inside a piece, f32 activations
     (16, 1, 256, 128, False),      # one slot; fewer output tiles than blocks
+    (32, 4, 3072, 128, False),     # more 10-row output tiles than resident blocks (the second loads late)
 ])
 def test_decode_nvfp4_one_launch_matches_stages(hip, E, k, H, I, xf32):
     """One token takes the one-launch kernel; its f32 output equals, bit for bit, the staged
