@@ -23,23 +23,48 @@ constexpr int MB_WAVES = 4;    // waves a block
 constexpr int MB_DR = 4;       // down rows a wave
 constexpr int MB_MAXW = 4096;  // widths (hidden, inter): at most 8 chunks of 512 a lane row
 
-// Eight activations of a row (columns col .. col + 8) as fp32, zeros when !ok.
+// Eight activations of a row (columns col .. col + 8): their loads (one 16-byte load of
+// bf16, two of f32; zeros when !ok) ...
 template <int DT>
-__device__ __forceinline__ void mb_act8(__amdgpu_buffer_rsrc_t r, int col, bool ok, float (&v)[8]) {
+__device__ __forceinline__ void mb_act8_load(__amdgpu_buffer_rsrc_t r, int col, bool ok, uint4 (&w)[DT == OOM_BF16 ? 1 : 2]) {
     if constexpr (DT == OOM_BF16) {
-        const uint4 w = ld16(r, ok ? col * 2 : OOB);
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        w[0] = ld16(r, ok ? col * 2 : OOB);
+    } else {
+        w[0] = ld16(r, ok ? col * 4 : OOB);
+        w[1] = ld16(r, ok ? col * 4 + 16 : OOB);
+    }
+}
+
+// ... and their eight values as fp32.
+template <int DT>
+__device__ __forceinline__ void mb_act8_cvt(const uint4 (&w)[DT == OOM_BF16 ? 1 : 2], float (&v)[8]) {
+    if constexpr (DT == OOM_BF16) {
+        const uint32_t ww[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             v[2 * q] = __uint_as_float(ww[q] << 16);
             v[2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
         }
     } else {
-        const uint4 a = ld16(r, ok ? col * 4 : OOB), b = ld16(r, ok ? col * 4 + 16 : OOB);
-        const uint32_t ww[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const uint32_t ww[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
 #pragma unroll
         for (int q = 0; q < 8; q++) v[q] = __uint_as_float(ww[q]);
     }
+}
+
+// An assignment's activations (or h) for every chunk of a lane row, all loads in flight
+// before the first use (loaded chunk by chunk, the compiler put a wait for each chunk's
+// loads before the next chunk's went out).
+template <int DT, int CH>
+__device__ __forceinline__ void mb_act_row(__amdgpu_buffer_rsrc_t r, int width, int lane,
+                                           uint4 (&w)[CH][DT == OOM_BF16 ? 1 : 2]) {
+#pragma unroll
+    for (int c = 0; c < CH; c++) mb_act8_load<DT>(r, c * 512 + lane * 8, c * 512 + lane * 8 < width, w[c]);
+#pragma unroll
+    for (int c = 0; c < CH; c++)
+#pragma unroll
+        for (int q = 0; q < (DT == OOM_BF16 ? 1 : 2); q++)
+            asm volatile("" : "+v"(w[c][q].x), "+v"(w[c][q].y), "+v"(w[c][q].z), "+v"(w[c][q].w));
 }
 
 // Eight bf16 weights (one 16-byte load) times eight activations, into acc.
@@ -84,11 +109,12 @@ __global__ void __launch_bounds__(64 * MB_WAVES) moe_gate_up_bf16_kernel(const u
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(x) + (size_t)t * H * ES), (short)0, H * ES, BUF_FLAGS);
         float acc[2] = {0.0f, 0.0f};
+        uint4 xw[CH][XDT == OOM_BF16 ? 1 : 2];
+        mb_act_row<XDT, CH>(xr, H, lane, xw);
 #pragma unroll
         for (int c = 0; c < CH; c++) {
-            const int col = c * 512 + lane * 8;
             float xv[8];
-            mb_act8<XDT>(xr, col, col < H, xv);
+            mb_act8_cvt<XDT>(xw[c], xv);
             acc[0] = mb_dot8(wg[c], xv, acc[0]);
             acc[1] = mb_dot8(wu[c], xv, acc[1]);
         }
@@ -126,11 +152,12 @@ __global__ void __launch_bounds__(64 * MB_WAVES) moe_down_bf16_kernel(const uint
         float acc[MB_DR];
 #pragma unroll
         for (int q = 0; q < MB_DR; q++) acc[q] = 0.0f;
+        uint4 hw[CH][2];
+        mb_act_row<OOM_F32, CH>(hr, I, lane, hw);
 #pragma unroll
         for (int c = 0; c < CH; c++) {
-            const int col = c * 512 + lane * 8;
             float hv[8];
-            mb_act8<OOM_F32>(hr, col, col < I, hv);
+            mb_act8_cvt<OOM_F32>(hw[c], hv);
 #pragma unroll
             for (int q = 0; q < MB_DR; q++) acc[q] = mb_dot8(wd[q][c], hv, acc[q]);
         }

@@ -252,6 +252,29 @@ __device__ __forceinline__ void pos_chunk(int p, int& r, int& c) {
     c = (p & 7) ^ chunk_key(r);
 }
 
+// Activation rows of assignments a[i] (an assignment past a1 reads row `valid`'s entry), all
+// loads in flight before the first use: under a per-row test the compiler moved each load
+// into its branch, behind a wait for the load before (a round trip per row).
+template <int N>
+__device__ __forceinline__ void token_rows(const GArgs& g, const int (&a)[N], int a1, int valid, int (&r)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const int ac = a[i] < a1 ? a[i] : valid;
+        r[i] = g.rows ? g.rows[ac] : ac;
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(r[i]));
+}
+
+// The per-row activation scales xs of rows r[i], the same way.
+template <int N>
+__device__ __forceinline__ void row_scales(const GArgs& g, const int (&r)[N], float (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) x[i] = g.xs[r[i]];
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(x[i]));
+}
+
 // One 16-byte load per lane straight into LDS: lane l's bytes land at lds + 16 l.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, int off) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, off, 0, 0, 0);
@@ -401,16 +424,19 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     src.xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(g.xq), (short)0, 0x7fff0000, G_BUF_FLAGS);
     const int wbytes = (int)(max(g.w_off, NB == 2 ? g.w2_off : g.w_off) + g.N * g.K);  // end of the weight parts
     src.wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, wbytes, G_BUF_FLAGS);
+    int xa[2], xc[2], xrow[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        int r, c;
-        pos_chunk((2 * wave + j) * 64 + lane, r, c);
-        const int a = a0 + m0 + r;
-        src.xo[j] = a < a1 ? (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c : -1;
+        int r;
+        pos_chunk((2 * wave + j) * 64 + lane, r, xc[j]);
+        xa[j] = a0 + m0 + r;
 #pragma unroll
         for (int m = 0; m < NB; m++)
-            src.wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r) * g.K) + 16 * c;
+            src.wo[m][j] = (int)((m == 0 ? g.w_off : g.w2_off) + (int64_t)(n0 + r) * g.K) + 16 * xc[j];
     }
+    token_rows(g, xa, a1, a0 + m0, xrow);
+#pragma unroll
+    for (int j = 0; j < 2; j++) src.xo[j] = xa[j] < a1 ? (int)(xrow[j] * g.K) + 16 * xc[j] : -1;
     // scales: lane l < 16 of wave w loads tile row 16 w + l's group scale (x_group 128),
     // lane m < NB the block scale of weight matrix m, once per K step
     src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
@@ -462,17 +488,23 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gemm_kernel(GArgs g) {
     wait_vm<0>();  // the zero-filled stages past the end have landed before LDS is reused
     __syncthreads();
     // ---- epilogue ----
+    float xsr[8];
+    if (!g.x_group) {
+        int orow[8];
+        token_rows(g, reinterpret_cast<const int(&)[8]>(arow_out), a1, a0 + m0, orow);
+        row_scales(g, orow, xsr);
+    }
 #pragma unroll
     for (int ms = 0; ms < 2; ms++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int a = arow_out[ms][e];
             if (a >= a1) continue;
-            const float xsr = g.x_group ? 1.0f : g.xs[g.rows ? g.rows[a] : a];
 #pragma unroll
             for (int ns = 0; ns < 4; ns++) {
                 const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
-                if (n < g.N) g.y[(int64_t)a * g.N + n] = g.x_group ? acc[0][ms][ns][e] : acc[0][ms][ns][e] * xsr;
+                if (n < g.N)
+                    g.y[(int64_t)a * g.N + n] = g.x_group ? acc[0][ms][ns][e] : acc[0][ms][ns][e] * xsr[4 * ms + e];
             }
         }
     G_STAMP_END(g, Lb);
@@ -601,13 +633,17 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
     src.sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(rec), (short)0, 0x7fff0000, G_BUF_FLAGS);
     // load j of the A tile covers positions (4 wave + j) 64 + lane, of each weight tile
     // (2 wave + j) 64 + lane: chunk c of tile row r
+    // the A tile's rows (j < 4) and the light stages' row (j = 4), their row loads together
+    int xa[5], xc[5], xrow[5];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        int r, c;
-        pos_chunk((4 * wave + j) * 64 + lane, r, c);
-        const int a = a0 + m0 + r;
-        src.xo[j] = a < a1 ? (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c : -1;
+    for (int j = 0; j < 5; j++) {
+        int r;
+        pos_chunk((j < 4 ? 4 * wave + j : wave & 3) * 64 + lane, r, xc[j]);
+        xa[j] = a0 + m0 + r;
     }
+    token_rows(g, xa, a1, a0 + m0, xrow);
+#pragma unroll
+    for (int j = 0; j < 4; j++) src.xo[j] = xa[j] < a1 ? (int)(xrow[j] * g.K) + 16 * xc[j] : -1;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         int r, c;
@@ -621,10 +657,7 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
     {
         // light stages: activation chunk (wave % 4) 64 + lane of K step kb + wave / 4, and
         // lane 2 h + m's block scale of matrix m at K step kb + h
-        int r, c;
-        pos_chunk((wave & 3) * 64 + lane, r, c);
-        const int a = a0 + m0 + r;
-        src.lxo = a < a1 ? (int)((g.rows ? g.rows[a] : a) * g.K) + 16 * c + (wave >> 2) * GBK : -1;
+        src.lxo = xa[4] < a1 ? (int)(xrow[4] * g.K) + 16 * xc[4] + (wave >> 2) * GBK : -1;
         src.lso = lane < 4 ? (int)(((lane & 1) == 0 ? g.s_off : g.s2_off) + (int64_t)(n0 / 128) * nkb * 4) +
                                  4 * (lane >> 1)
                            : G_OOB;
@@ -679,16 +712,24 @@ __global__ void __launch_bounds__(GTHREADS) grouped_gate_up256_kernel(GArgs g) {
 #undef GU2_SW
     wait_vm<0>();  // the zero-filled stage past the end has landed before the block ends
     // h = silu(xs g) * (xs u) as two bf16 terms: hi = bf16(h), lo = bf16(h - hi)
+    float xsr[16];
+    {
+        int oa[16], orow[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) oa[i] = a0 + m0 + 64 * wm + 16 * (i >> 2) + 4 * (lane >> 4) + (i & 3);
+        token_rows(g, oa, a1, a0 + m0, orow);
+        row_scales(g, orow, xsr);
+    }
 #pragma unroll
     for (int ms = 0; ms < 4; ms++)
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int a = a0 + m0 + 64 * wm + 16 * ms + 4 * (lane >> 4) + e;
             if (a >= a1) continue;
-            const float xsr = g.xs[g.rows ? g.rows[a] : a];
+            const float xs_a = xsr[4 * ms + e];
 #pragma unroll
             for (int ns = 0; ns < 4; ns++) {
-                const float h = siluf(acc[0][ms][ns][e] * xsr) * (acc[1][ms][ns][e] * xsr);
+                const float h = siluf(acc[0][ms][ns][e] * xs_a) * (acc[1][ms][ns][e] * xs_a);
                 const uint16_t hi = f32_to_bf16(h);
                 const int64_t n = n0 + 64 * wn + 16 * ns + (lane & 15);
                 g.hh[(int64_t)a * g.N + n] = hi;
