@@ -256,6 +256,71 @@ def prefill_check(hip, geo, recs, logits, xb, k, sample=None, precision=None):
           f"worst abs {np.abs(got - pure).max():.2e}, f32 worst abs {np.abs(got32 - pure).max():.2e}")
 
 
+def prefill_all_tokens_fp32(hip, geo, buf, addrs, logits, xb, k):
+    """Every token of an exact-precision step, the complement of prefill_check's sample:
+    router ids of all tokens exact and weights to fp32 rounding, every token's e4m3 x codes
+    and scale equal to the oracle's, and the whole f32 output within rtol 2e-2 / atol 1e-3
+    of a float32 restatement in torch on the GPU. The restatement decodes the e4m3 codes with
+    torch's float8_e4m3fn, applies the 128 x 128 block scales and the per-token activation
+    scale, forms h = silu(g) u in fp32 (the reference's default path) and sums the slots in
+    slot order."""
+    import torch
+
+    T, E = logits.shape
+    H, I = geo.hidden, geo.inter
+    hgeo = hip.record_geometry(H, I)
+    ws = torch.zeros(hip.moe_prefill_fp8_workspace_size(T, E, k, hgeo), dtype=torch.uint8, device="cuda")
+    ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    out32 = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    xd = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).cuda()
+    hip.moe_prefill_fp8(dev(logits), xd, addrs, k, hgeo, ids, w, out32, ws, precision=hip.EXPERT_EXACT)
+    torch.cuda.synchronize()
+    want_ids, want_w = oracle.router_topk(logits, k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), want_ids)
+    np.testing.assert_allclose(w.cpu().numpy(), want_w, rtol=2e-6)
+    st = prefill_workspace(ws, T, E, k, H, I)
+    xq, xs = oracle.quantize_act(oracle.bf16_to_f32(xb))
+    np.testing.assert_array_equal(st["xq"], xq)
+    np.testing.assert_array_equal(st["xs"], xs)
+    experts, off, tok, slot = oracle.moe_plan(want_ids, E)
+
+    def e4m3(codes):
+        return codes.contiguous().view(torch.float8_e4m3fn).float()
+
+    def weights(e, w_off, s_off, n, kk):
+        q = e4m3(buf[e, w_off:w_off + n * kk]).reshape(n // 128, 128, kk // 128, 128)
+        sc = buf[e, s_off:s_off + (n // 128) * (kk // 128) * 4].clone().view(torch.float32)
+        return (q * sc.reshape(n // 128, 1, kk // 128, 1)).reshape(n, kk)
+
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        xr = e4m3(torch.from_numpy(xq).cuda()) * torch.from_numpy(xs).cuda()[:, None]
+        y = torch.empty((T * k, H), dtype=torch.float32, device="cuda")
+        for i, e in enumerate(int(v) for v in experts):
+            a0, a1 = int(off[i]), int(off[i + 1])
+            xe = xr[torch.from_numpy(tok[a0:a1].astype(np.int64)).cuda()]
+            g = torch.mm(xe, weights(e, geo.gate_weight, geo.gate_scale, I, H).t().contiguous())
+            u = torch.mm(xe, weights(e, geo.up_weight, geo.up_scale, I, H).t().contiguous())
+            h = g / (1.0 + torch.exp(-g)) * u
+            y[a0:a1] = torch.mm(h, weights(e, geo.down_weight, geo.down_scale, H, I).t().contiguous())
+        wt = torch.from_numpy(want_w).cuda()
+        sl = torch.from_numpy(slot.reshape(T, k).astype(np.int64)).cuda()
+        ref = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+        for j in range(k):
+            ref = ref + wt[:, j:j + 1] * y[sl[:, j]]
+        torch.cuda.synchronize()
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    got, ref = out32.cpu().numpy(), ref.cpu().numpy()
+    bad = ~np.isclose(got, ref, rtol=RTOL, atol=ATOL)
+    assert not bad.any(), f"all tokens: {bad.sum()} of {bad.size} outside rtol {RTOL} / atol {ATOL}; " \
+                          f"worst {np.abs(got - ref)[bad].max():.3e}"
+    print(f"prefill, all {T} tokens against the fp32 restatement: worst abs {np.abs(got - ref).max():.2e} "
+          f"(scale {np.abs(ref).max():.2e})")
+
+
 @pytest.mark.parametrize("prec", ["bf16", "exact"])
 @pytest.mark.parametrize("T,E,k,H,I", [(64, 16, 4, 512, 256), (7, 8, 2, 256, 128), (300, 32, 8, 1024, 384),
                                        (40, 8, 4, 384, 256)])
@@ -277,7 +342,9 @@ def test_prefill_full_shape_sampled_tokens(hip, prec):
     inter 1536. A token's output depends only on its own row, routing and the experts
     it picks, so the oracle checks a sample of the full step: 12 fixed tokens, the last
     two tokens of each of the two heaviest experts' runs (their last, partial 128-row
-    M-tiles) and the tokens of the lightest experts' runs (one or two assignments)."""
+    M-tiles) and the tokens of the lightest experts' runs (one or two assignments). At the
+    exact precision every token is then checked against a float32 restatement in torch
+    (prefill_all_tokens_fp32)."""
     import torch
 
     T, E, k, H, I = 2048, 128, 8, 4096, 1536
@@ -315,3 +382,5 @@ def test_prefill_full_shape_sampled_tokens(hip, prec):
           f"{light.size} experts with <= 2)", flush=True)
     prefill_check(hip, geo, (buf, addrs), logits, xb, k, sample,
                   precision=hip.EXPERT_EXACT if prec == "exact" else hip.EXPERT_BF16)
+    if prec == "exact":
+        prefill_all_tokens_fp32(hip, geo, buf, addrs, logits, xb, k)
