@@ -53,6 +53,7 @@ constexpr int B_DEPTH = 8;         // K steps in flight per wave (3 loads each)
 constexpr int B_XS = B_HMAX + 8;   // LDS row stride (bf16) of the activations
 constexpr int B_HS = B_IMAX + 8;   // LDS row stride (bf16) of h
 constexpr int B_TILE = 16;         // output rows of a phase-2 item
+constexpr int B_Q = 16;            // a wave's queue of claimed items (issue cursor -> consume cursor)
 
 typedef __bf16 bbf16x8 __attribute__((ext_vector_type(8)));
 typedef float bf32x4 __attribute__((ext_vector_type(4)));
@@ -101,6 +102,8 @@ struct alignas(16) BLds {
     int assign_tok[B_ASH];
     int slot_assign[B_AMAX];
     float gate[B_T];  // the shared expert's gate logits
+    int queue[B_W][B_Q];  // each wave's claimed items, from its issue cursor to its consume cursor
+    uint32_t claims[2];   // items claimed by the block's waves: phase 1, phase 2
     int n_e;
 };
 static_assert(offsetof(BLds, u) == 0 && (B_XS * 2) % 16 == 0 && (B_HS * 2) % 16 == 0 &&
@@ -334,6 +337,7 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         if (tid == E) L.recs[E] = a.shared_rec[0];
     }
     if (tid < 256) L.mask[tid] = 0u;  // (512 threads, 256 masks)
+    if (tid == 256) L.claims[0] = L.claims[1] = 0u;
     // activations: thread tid takes columns 8 (tid + NT c) .. + 8 of every token row (zeros
     // past T and H); the loads stay in flight through the routing below and reach LDS after it
     static_assert(B_HMAX / 8 / NT == 1, "one pass of activation loads");
@@ -428,45 +432,62 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, AS * I * 4, BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, AS * H * 4, BUF_FLAGS);
     const int m16 = lane & 15, kq = lane >> 4;
-    // ---- phase 1: my items gw + n NW (n < mine), K steps in order; an issue cursor runs
-    // B_DEPTH steps ahead of the consume cursor ----
+    // ---- phase 1: block b's items are the contiguous range [b NG / G, (b + 1) NG / G), so
+    // blocks differ by at most one item; its waves claim them in order from a counter in
+    // LDS, so every wave streams until the block's items run out. (Items dealt to waves
+    // statically, gw + n NW, gave some blocks a third more items than others whenever the
+    // routed expert count passed a multiple of the grid's waves, and one 64 KiB item takes
+    // a lone wave ~8 us.) K steps in order, an issue cursor B_DEPTH steps ahead of the
+    // consume cursor, each claimed item handed from the one to the other through the
+    // wave's queue in LDS ----
+    int* const queue = L.queue[wave];
     {
         const int nrt = (I + 7) >> 3, NG = n_e * nrt;
-        const int mine = gw < NG ? (NG - gw + NW - 1) / NW : 0, nq = mine * nksH;
-        int ni = 0, ksi = 0;
-        GuRow gi = gu_row(a, L, gw, 0 < mine, nrt, lane);
+        const int lo = (int)((int64_t)blockIdx.x * NG / gridDim.x), hi = (int)((int64_t)(blockIdx.x + 1) * NG / gridDim.x);
+        auto claim = [&]() -> int {
+            uint32_t c = 0;
+            if (lane == 0) c = __hip_atomic_fetch_add(&L.claims[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            c = __builtin_amdgcn_readfirstlane(c);
+            return lo + (int)c;
+        };
+        int iti = claim(), ni = 0, ksi = 0;  // the issue cursor's item (from hi on: claims stop)
+        if (lane == 0) queue[0] = iti;
+        GuRow gi = gu_row(a, L, iti, iti < hi, nrt, lane);
         auto issue = [&](KStep& t, const bf32x4& dep) {
             gu_issue(a, gi, ksi, lane, dep, t);
             if (++ksi == nksH) {
                 ksi = 0;
+                if (iti < hi) iti = claim();
                 ++ni;
-                gi = gu_row(a, L, gw + ni * NW, ni < mine, nrt, lane);
+                if (lane == 0) queue[ni & (B_Q - 1)] = iti;
+                gi = gu_row(a, L, iti, iti < hi, nrt, lane);
             }
         };
         KStep ring[B_DEPTH];
 #pragma unroll
         for (int d = 0; d < B_DEPTH; d++) issue(ring[d], bf32x4{0.0f, 0.0f, 0.0f, 0.0f});
-        int nc = 0, ksc = 0, j0 = 0, a0 = 0, nb = 0, xo = 0;
+        int nc = 0, ksc = 0, itc = 0, j0 = 0, a0 = 0, nb = 0, xo = 0;
         auto con_item = [&]() {
-            const bool valid = nc < mine;
-            const int it = gw + nc * NW, i = valid ? it / nrt : 0;
-            j0 = (it - i * nrt) * 8;
+            itc = __builtin_amdgcn_readfirstlane(queue[nc & (B_Q - 1)]);
+            const int i = itc < hi ? itc / nrt : 0;
+            j0 = (itc - i * nrt) * 8;
             a0 = L.off[i];
             nb = L.off[i + 1] - a0;
             xo = L.assign_tok[a0 + (m16 < nb ? m16 : 0)] * B_XS + 32 * kq;
         };
         con_item();
         bf32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-        // every ring slot is consumed and refilled on every step (steps past nq read zeros
-        // and store nothing), so the slots stay in fixed registers across iterations
-        for (int q0 = 0; q0 < nq; q0 += B_DEPTH) {
+        // every ring slot is consumed and refilled on every step (steps past the last item
+        // read zeros and store nothing), so the slots stay in fixed registers across
+        // iterations
+        while (itc < hi) {
 #pragma unroll
             for (int d = 0; d < B_DEPTH; d++) {
                 gu_mfma(L, ring[d], xo + ksc * 128, c);
                 issue(ring[d], c);
                 if (++ksc == nksH) {
                     ksc = 0;
-                    if (nc < mine) gu_store(a, hr, j0, a0, nb, lane, c);
+                    if (itc < hi) gu_store(a, hr, j0, a0, nb, lane, c);
                     c = bf32x4{0.0f, 0.0f, 0.0f, 0.0f};
                     ++nc;
                     con_item();
@@ -496,18 +517,30 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         first = min(ND, (int)blockIdx.x * per);
         last = min(ND, first + per);
     }
-    int r0 = first, i = 0, t0 = 0, t1 = 0, mt = 0, nq = 0;
-    // the run at r0: slot i, tiles t0 .. t1; this wave's tiles t0 + wave + B_W m (m < mt),
-    // K steps in order, issued B_DEPTH ahead of their use
+    int r0 = first, i = 0, t0 = 0, t1 = 0;
+    // the run at r0: slot i, tiles t0 .. t1, which the block's waves claim in order from a
+    // counter in LDS; K steps in order, issued B_DEPTH ahead of their use, the claimed tiles
+    // handed from the issue cursor to the consume cursor through the wave's queue. Every
+    // wave claims each run's tiles until its first claim past t1, so a run takes exactly
+    // (t1 - t0) + B_W claims and the next run's claims count from there.
+    uint32_t cbase = 0;  // phase-2 claims before this run
+    auto claim = [&]() -> int {
+        uint32_t c = 0;
+        if (lane == 0) c = __hip_atomic_fetch_add(&L.claims[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        c = __builtin_amdgcn_readfirstlane(c);
+        return t0 + (int)(c - cbase);
+    };
     __amdgpu_buffer_rsrc_t rr = uniform_rsrc(0, 0);
-    int mi = 0, ksi = 0;
+    int ti = 0, ni = 0, ksi = 0;  // the issue cursor's tile (from t1 on: claims stop)
     DnRow di = dn_row(a, 0, false, lane);
     auto issue = [&](KStep& t, const bf32x4& dep) {
         dn_issue(a, rr, di, ksi, lane, dep, t);
         if (++ksi == nksI) {
             ksi = 0;
-            ++mi;
-            di = dn_row(a, t0 + wave + mi * B_W, mi < mt, lane);
+            if (ti < t1) ti = claim();
+            ++ni;
+            if (lane == 0) queue[ni & (B_Q - 1)] = ti;
+            di = dn_row(a, ti, ti < t1, lane);
         }
     };
     KStep ring[B_DEPTH];
@@ -516,12 +549,12 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         i = any ? r0 / ntile : 0;
         t0 = any ? r0 - i * ntile : 0;
         t1 = any ? min(ntile, t0 + (last - r0)) : 0;
-        mt = t0 + wave < t1 ? (t1 - t0 - wave + B_W - 1) / B_W : 0;
-        nq = mt * nksI;
         rr = uniform_rsrc(L.recs[L.experts[i]], any ? a.rec_bytes : 0);
-        mi = 0;
+        ni = 0;
         ksi = 0;
-        di = dn_row(a, t0 + wave, 0 < mt, lane);
+        ti = any ? claim() : t1;
+        if (lane == 0) queue[0] = ti;
+        di = dn_row(a, ti, ti < t1, lane);
 #pragma unroll
         for (int d = 0; d < B_DEPTH; d++) issue(ring[d], bf32x4{0.0f, 0.0f, 0.0f, 0.0f});
     };
@@ -564,9 +597,9 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
         if (!staged_once) OOM_STAMP(a.stamps, B_W, 4);  // the first run's h staged
         staged_once = true;
         const int a0 = L.off[i], nb = L.off[i + 1] - a0, ho = m16 * B_HS + 32 * kq;
-        int mc = 0, ksc = 0;
+        int nc = 0, ksc = 0, tc = __builtin_amdgcn_readfirstlane(queue[0]);
         bf32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int q0 = 0; q0 < nq; q0 += B_DEPTH) {
+        while (tc < t1) {
 #pragma unroll
             for (int d = 0; d < B_DEPTH; d++) {
                 dn_mfma(L, ring[d], ho + ksc * 128, c);
@@ -574,14 +607,16 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
                 if (++ksc == nksI) {
                     // y rows 16 tile + 4 (l / 16) + e of assignment a0 + l % 16
                     ksc = 0;
-                    const int row = (t0 + wave + mc * B_W) * B_TILE + 4 * kq;
+                    const int row = tc * B_TILE + 4 * kq;
                     const float yv[4] = {c[0], c[1], c[2], c[3]};
-                    if (mc < mt && m16 < nb && row < H) st_dev16(yr, ((a0 + m16) * H + row) * 4, yv);
+                    if (tc < t1 && m16 < nb && row < H) st_dev16(yr, ((a0 + m16) * H + row) * 4, yv);
                     c = bf32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    ++mc;
+                    ++nc;
+                    tc = __builtin_amdgcn_readfirstlane(queue[nc & (B_Q - 1)]);
                 }
             }
         }
+        cbase += (uint32_t)(t1 - t0 + B_W);
         r0 += t1 - t0;
         __syncthreads();  // every wave is done with this run's h before the next is staged
         start_run();
