@@ -432,23 +432,23 @@ __global__ void __launch_bounds__(64 * B_W) moe_batch_kernel(BArgs a) {
     const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(a.h, (short)0, AS * I * 4, BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, AS * H * 4, BUF_FLAGS);
     const int m16 = lane & 15, kq = lane >> 4;
-    // ---- phase 1: block b's items are the contiguous range [b NG / G, (b + 1) NG / G), so
-    // blocks differ by at most one item; its waves claim them in order from a counter in
-    // LDS, so every wave streams until the block's items run out. (Items dealt to waves
-    // statically, gw + n NW, gave some blocks a third more items than others whenever the
-    // routed expert count passed a multiple of the grid's waves, and one 64 KiB item takes
-    // a lone wave ~8 us.) K steps in order, an issue cursor B_DEPTH steps ahead of the
-    // consume cursor, each claimed item handed from the one to the other through the
-    // wave's queue in LDS ----
+    // ---- phase 1: block b's items are b, b + G, b + 2 G, ..., so blocks differ by at most
+    // one item and the grid's waves stream neighbouring items at any time; its waves claim
+    // them in order from a counter in LDS, so every wave streams until the block's items run
+    // out. (Items dealt to waves statically, gw + n NW, gave some blocks a third more items
+    // than others whenever the routed expert count passed a multiple of the grid's waves,
+    // and one 64 KiB item takes a lone wave ~8 us.) K steps in order, an issue cursor
+    // B_DEPTH steps ahead of the consume cursor, each claimed item handed from the one to
+    // the other through the wave's queue in LDS ----
     int* const queue = L.queue[wave];
     {
         const int nrt = (I + 7) >> 3, NG = n_e * nrt;
-        const int lo = (int)((int64_t)blockIdx.x * NG / gridDim.x), hi = (int)((int64_t)(blockIdx.x + 1) * NG / gridDim.x);
+        const int hi = NG;
         auto claim = [&]() -> int {
             uint32_t c = 0;
             if (lane == 0) c = __hip_atomic_fetch_add(&L.claims[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             c = __builtin_amdgcn_readfirstlane(c);
-            return lo + (int)c;
+            return (int)blockIdx.x + (int)c * (int)gridDim.x;
         };
         int iti = claim(), ni = 0, ksi = 0;  // the issue cursor's item (from hi on: claims stop)
         if (lane == 0) queue[0] = iti;

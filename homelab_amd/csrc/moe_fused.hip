@@ -653,7 +653,7 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
             uint32_t c = 0;
             if (lane == 0) c = __hip_atomic_fetch_add(&pl.claims, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             c = __builtin_amdgcn_readfirstlane(c);
-            it_pre = (int)(blockIdx.x * FW1 + c % FW1 + (c / FW1) * gridDim.x * FW1);
+            it_pre = (int)(blockIdx.x + c * gridDim.x);
             if (it_pre < (int)a.I) gate1_load(a, pl, it_pre, (int)a.I, lane, w0, true);
         }
     }
@@ -738,14 +738,17 @@ __global__ void __launch_bounds__(TG == 1 ? 64 * FW1 : 64 * FW) moe_decode_fused
         // ---- phase 1, one token: item it = (expert it / I, row it % I); the next item's
         // loads are in flight while the current one is reduced ----
         const int NG = (n_e + (SH ? 1 : 0)) * (int)a.I;  // the shared expert's rows first
-        // Block b owns items b WB + c % WB + (c / WB) NW (c = 0, 1, ...); its waves claim
-        // them in that order from a counter in LDS, so a wave that gets fewer issue slots
-        // (the second wave of a SIMD) takes fewer items than its partner.
+        // Block b owns items b WB + c % WB + (c / WB) NW (c = 0, 1, ...; with the shared
+        // expert b + c G, so that every block holds the same number of items to one and
+        // starts on shared rows); its waves claim them in that order from a counter in LDS,
+        // so a wave that gets fewer issue slots (the second wave of a SIMD) takes fewer
+        // items than its partner.
         auto claim = [&]() -> int {
             uint32_t c = 0;
             if (lane == 0) c = __hip_atomic_fetch_add(&pl.claims, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             c = __builtin_amdgcn_readfirstlane(c);
-            return (int)(blockIdx.x * WB + c % WB + (c / WB) * NW);
+            if constexpr (SH) return (int)(blockIdx.x + c * gridDim.x);
+            else return (int)(blockIdx.x * WB + c % WB + (c / WB) * NW);
         };
         int it0;
         if constexpr (SH) {
