@@ -150,75 +150,86 @@ __device__ __forceinline__ void piece_dot(const float* f, const float4* xs4, int
     }
 }
 
-// One gate/up pass over TB staged tokens (nb real): the wave's rows j0 + 2p + half;
-// put(t, j, v) stores h of staged token t at intermediate row j.
-// CS chunks of 1024 columns load per round (all of a row's with CS = 4).
-template <int TB, int CS = 2, typename Put>
-__device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amdgpu_buffer_rsrc_t r, float s2g,
-                                         float s2u, int j0, int lane, int nb, Put put) {
+// One round of a gate/up pass's loads: chunks c0 .. c0 + CS - 1 (1024 columns each) of the
+// wave's rows j0 + 2 p + half, codes and scale bytes (a chunk or group past the row reads 0).
+template <int CS>
+struct Gu4Ld {
+    uint4 wg[N4_GP][CS], wu[N4_GP][CS];
+    uint32_t bg[N4_GP][CS][2], bu[N4_GP][CS][2];
+};
+template <int CS>
+__device__ __forceinline__ void gu4_load(const Rec4& g, __amdgpu_buffer_rsrc_t r, int j0, int lane, int c0,
+                                         Gu4Ld<CS>& t) {
     const int H = g.H, I = g.I, CH = (H + 1023) >> 10, hg = H >> 4;
     const int half = lane >> 5, l = lane & 31;
-    float acc[2 * TB * N4_GP];  // [gate|up][t][p]
 #pragma unroll
-    for (int i = 0; i < 2 * TB * N4_GP; i++) acc[i] = 0.0f;
-    for (int c0 = 0; c0 < CH; c0 += CS) {
-        uint4 wg[N4_GP][CS], wu[N4_GP][CS];
-        uint32_t bg[N4_GP][CS][2], bu[N4_GP][CS][2];
-#pragma unroll
-        for (int p = 0; p < N4_GP; p++) {
-            const int j = j0 + 2 * p + half;
-#pragma unroll
-            for (int c = 0; c < CS; c++) {
-                const int col = (c0 + c) * 1024 + 32 * l;
-                const bool ok = j < I && c0 + c < CH && col < H;
-                wg[p][c] = ld16(r, ok ? g.gw + j * (H >> 1) + (col >> 1) : OOB);
-                wu[p][c] = ld16(r, ok ? g.uw + j * (H >> 1) + (col >> 1) : OOB);
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    const bool okq = ok && (col >> 4) + q < hg;
-                    bg[p][c][q] = ldb(r, okq ? g.gs + j * hg + (col >> 4) + q : OOB);
-                    bu[p][c][q] = ldb(r, okq ? g.us + j * hg + (col >> 4) + q : OOB);
-                }
-            }
-        }
+    for (int p = 0; p < N4_GP; p++) {
+        const int j = j0 + 2 * p + half;
 #pragma unroll
         for (int c = 0; c < CS; c++) {
-            if (c0 + c >= CH) break;
             const int col = (c0 + c) * 1024 + 32 * l;
+            const bool ok = j < I && c0 + c < CH && col < H;
+            t.wg[p][c] = ld16(r, ok ? g.gw + j * (H >> 1) + (col >> 1) : OOB);
+            t.wu[p][c] = ld16(r, ok ? g.uw + j * (H >> 1) + (col >> 1) : OOB);
 #pragma unroll
-            for (int p = 0; p < N4_GP; p++) {
-                float sg[2], su[2];
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    // a group past the row's end scales to 0 (its byte read as 0); the select
-                    // is on scale_2, so the byte's load is used on every lane and stays where
-                    // it was issued (a select on the product let the compiler move the load
-                    // into a branch, whose wait then covered every load in flight)
-                    const bool okq = (col >> 4) + q < hg;
-                    sg[q] = e4m3_byte(bg[p][c][q]) * (okq ? s2g : 0.0f);
-                    su[q] = e4m3_byte(bu[p][c][q]) * (okq ? s2u : 0.0f);
-                }
-                // the gate piece, then the up piece: one set of 32 decoded weights at a time
-                float f[32];
-                e2m1x32(wg[p][c], f);
-#pragma unroll
-                for (int t = 0; t < TB; t++) {
-                    float g0, g1;
-                    piece_dot(f, xs4, t, CH, c0 + c, l, g0, g1);
-                    float& ag = acc[(0 * TB + t) * N4_GP + p];
-                    ag = fmaf(g1, sg[1], fmaf(g0, sg[0], ag));
-                }
-                e2m1x32(wu[p][c], f);
-#pragma unroll
-                for (int t = 0; t < TB; t++) {
-                    float u0, u1;
-                    piece_dot(f, xs4, t, CH, c0 + c, l, u0, u1);
-                    float& au = acc[(1 * TB + t) * N4_GP + p];
-                    au = fmaf(u1, su[1], fmaf(u0, su[0], au));
-                }
+            for (int q = 0; q < 2; q++) {
+                const bool okq = ok && (col >> 4) + q < hg;
+                t.bg[p][c][q] = ldb(r, okq ? g.gs + j * hg + (col >> 4) + q : OOB);
+                t.bu[p][c][q] = ldb(r, okq ? g.us + j * hg + (col >> 4) + q : OOB);
             }
         }
     }
+}
+
+// That round's sums into acc[(gate|up, t, p)] over TB staged tokens.
+template <int TB, int CS>
+__device__ __forceinline__ void gu4_math(const float4* xs4, const Rec4& g, float s2g, float s2u, int lane, int c0,
+                                         const Gu4Ld<CS>& t, float (&acc)[2 * TB * N4_GP]) {
+    const int H = g.H, CH = (H + 1023) >> 10, hg = H >> 4;
+    const int l = lane & 31;
+#pragma unroll
+    for (int c = 0; c < CS; c++) {
+        if (c0 + c >= CH) break;
+        const int col = (c0 + c) * 1024 + 32 * l;
+#pragma unroll
+        for (int p = 0; p < N4_GP; p++) {
+            float sg[2], su[2];
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                // a group past the row's end scales to 0 (its byte read as 0); the select
+                // is on scale_2, so the byte's load is used on every lane and stays where
+                // it was issued (a select on the product let the compiler move the load
+                // into a branch, whose wait then covered every load in flight)
+                const bool okq = (col >> 4) + q < hg;
+                sg[q] = e4m3_byte(t.bg[p][c][q]) * (okq ? s2g : 0.0f);
+                su[q] = e4m3_byte(t.bu[p][c][q]) * (okq ? s2u : 0.0f);
+            }
+            // the gate piece, then the up piece: one set of 32 decoded weights at a time
+            float f[32];
+            e2m1x32(t.wg[p][c], f);
+#pragma unroll
+            for (int tt = 0; tt < TB; tt++) {
+                float g0, g1;
+                piece_dot(f, xs4, tt, CH, c0 + c, l, g0, g1);
+                float& ag = acc[(0 * TB + tt) * N4_GP + p];
+                ag = fmaf(g1, sg[1], fmaf(g0, sg[0], ag));
+            }
+            e2m1x32(t.wu[p][c], f);
+#pragma unroll
+            for (int tt = 0; tt < TB; tt++) {
+                float u0, u1;
+                piece_dot(f, xs4, tt, CH, c0 + c, l, u0, u1);
+                float& au = acc[(1 * TB + tt) * N4_GP + p];
+                au = fmaf(u1, su[1], fmaf(u0, su[0], au));
+            }
+        }
+    }
+}
+
+// The pass's end: the wave sums, then put(t, j, silu(gate) * up) for each of the wave's rows.
+template <int TB, typename Put>
+__device__ __forceinline__ void gu4_put(float (&acc)[2 * TB * N4_GP], int I, int j0, int lane, int nb, Put put) {
+    const int half = lane >> 5, l = lane & 31;
     // value v = (gu * TB + t) * GP + p ends in sub-group v of each half; its up sum sits
     // 16 lanes on, in the same half
     constexpr int NV = 2 * TB * N4_GP, GROUP = 32 / NV;
@@ -229,6 +240,24 @@ __device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amd
         const int t = v / N4_GP, j = j0 + 2 * (v % N4_GP) + half;
         if (t < nb && j < I) put(t, j, siluf(tot) * up);
     }
+}
+
+// One gate/up pass over TB staged tokens (nb real): the wave's rows j0 + 2p + half;
+// put(t, j, v) stores h of staged token t at intermediate row j.
+// CS chunks of 1024 columns load per round (all of a row's with CS = 4).
+template <int TB, int CS = 2, typename Put>
+__device__ __forceinline__ void gu4_pass(const float4* xs4, const Rec4& g, __amdgpu_buffer_rsrc_t r, float s2g,
+                                         float s2u, int j0, int lane, int nb, Put put) {
+    const int CH = (g.H + 1023) >> 10;
+    float acc[2 * TB * N4_GP];  // [gate|up][t][p]
+#pragma unroll
+    for (int i = 0; i < 2 * TB * N4_GP; i++) acc[i] = 0.0f;
+    for (int c0 = 0; c0 < CH; c0 += CS) {
+        Gu4Ld<CS> t;
+        gu4_load<CS>(g, r, j0, lane, c0, t);
+        gu4_math<TB, CS>(xs4, g, s2g, s2u, lane, c0, t, acc);
+    }
+    gu4_put<TB>(acc, g.I, j0, lane, nb, put);
 }
 
 template <int XDT>
@@ -609,12 +638,15 @@ struct Dn4U {
     float s2;
 };
 
-__device__ __forceinline__ void dnu_load(Dn4U& w, const Rec4& g, __amdgpu_buffer_rsrc_t r, int row, int lane) {
-    const int I = g.I, ig = I >> 4, col = 32 * (lane & 31);
-    const bool ok = row < g.H && col < I;
-    w.wd = ld16(r, ok ? g.dw + row * (I >> 1) + (col >> 1) : OOB);
+// row2: the pair's first row (the same on every lane); the row's offsets are a scalar product
+// plus the lane's part, so no vector multiply-add reads a register a load in flight will write.
+__device__ __forceinline__ void dnu_load(Dn4U& w, const Rec4& g, __amdgpu_buffer_rsrc_t r, int row2, int lane) {
+    const int I = g.I, ig = I >> 4, half = lane >> 5, col = 32 * (lane & 31);
+    const bool ok = row2 + half < g.H && col < I;
+    const int wrow = __builtin_amdgcn_readfirstlane(g.dw + row2 * (I >> 1)), srow = __builtin_amdgcn_readfirstlane(g.ds + row2 * ig);
+    w.wd = ld16(r, ok ? wrow + half * (I >> 1) + (col >> 1) : OOB);
 #pragma unroll
-    for (int q = 0; q < 2; q++) w.bd[q] = ldb(r, ok && (col >> 4) + q < ig ? g.ds + row * ig + (col >> 4) + q : OOB);
+    for (int q = 0; q < 2; q++) w.bd[q] = ldb(r, ok && (col >> 4) + q < ig ? srow + half * ig + (col >> 4) + q : OOB);
     w.s2 = ldf(r, g.s2d);
 }
 
@@ -685,17 +717,45 @@ __global__ void __launch_bounds__(64 * N4P_WAVES) moe_decode_nvfp4_1p_kernel(Fus
         for (int m = 0; m < N4P_UP; m++) {
             const int u = wave + N4P_WAVES * m, s = u / N4P_DP, p = u - s * N4P_DP;
             const bool ok = b < tiles && u < NU;
-            dnu_load(du[m], g, rsrc_of(ok ? s : k), b * 2 * N4P_DP + 2 * p + half, lane);
+            dnu_load(du[m], g, rsrc_of(ok ? s : k), b * 2 * N4P_DP + 2 * p, lane);
         }
     };
-    // ---- phase 1: the down prefetch, then items b + G (wave + 8 n) ----
-    prefetch();
-    for (int it = b + G * wave; it < NG; it += G * N4P_WAVES) {
+    // ---- phase 1: items b + G (wave + 8 n); the down prefetch goes out behind the first
+    // item's loads, so the rows h needs arrive first. The first item is straight-line code
+    // (its one round of loads, the prefetch, its math: CH <= 3 here), so the item's waits
+    // leave the prefetch in flight ----
+    int it = b + G * wave;
+    if (it < NG) {
         const int s = it / ipe, j0 = (it - s * ipe) * 2 * N4_GP;
         const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs_l[s], g.bytes);
         const float s2g = ldf(r, g.s2g), s2u = ldf(r, g.s2u);
         float* hs = a.h + (size_t)s * I;
-        gu4_pass<1, 3>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
+        float acc[2 * N4_GP];
+#pragma unroll
+        for (int i = 0; i < 2 * N4_GP; i++) acc[i] = 0.0f;
+        {
+            Gu4Ld<3> t;
+            gu4_load<3>(g, r, j0, lane, 0, t);
+            __builtin_amdgcn_sched_barrier(0);
+            prefetch();
+            __builtin_amdgcn_sched_barrier(0);
+            gu4_math<1, 3>(xs4, g, s2g, s2u, lane, 0, t, acc);
+        }
+        for (int c0 = 3; c0 < (H + 1023) >> 10; c0 += 3) {  // hidden > 3072: not launched here
+            Gu4Ld<3> t;
+            gu4_load<3>(g, r, j0, lane, c0, t);
+            gu4_math<1, 3>(xs4, g, s2g, s2u, lane, c0, t, acc);
+        }
+        gu4_put<1>(acc, I, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
+        for (it += G * N4P_WAVES; it < NG; it += G * N4P_WAVES) {
+            const int s = it / ipe, j0 = (it - s * ipe) * 2 * N4_GP;
+            const __amdgpu_buffer_rsrc_t r = uniform_rsrc(recs_l[s], g.bytes);
+            const float s2g = ldf(r, g.s2g), s2u = ldf(r, g.s2u);
+            float* hs = a.h + (size_t)s * I;
+            gu4_pass<1, 3>(xs4, g, r, s2g, s2u, j0, lane, 1, [&](int, int j, float v) { st_dev(hs + j, v); });
+        }
+    } else {
+        prefetch();
     }
     OOM_STAMP(a.stamps, N4P_WAVES, 3);  // gate/up items done, the down units loaded
     wait_mem();  // this wave's h stores are complete before its block arrives
@@ -722,7 +782,7 @@ __global__ void __launch_bounds__(64 * N4P_WAVES) moe_decode_nvfp4_1p_kernel(Fus
         for (int u = u0; u < NU; u += N4P_WAVES) {
             const int s = u / N4P_DP, p = u - s * N4P_DP;
             Dn4U d;
-            dnu_load(d, g, rsrc_of(s), r0 + 2 * p + half, lane);
+            dnu_load(d, g, rsrc_of(s), r0 + 2 * p, lane);
             float v[1] = {dnu_part(d, xs4 + (size_t)s * 256, I, lane)};
             const float tot = wave_sum_multi<1, 16>(v, lane);
             if (l == 0) put_unit(u, r0, tot);

@@ -169,6 +169,7 @@ def test_decode_nvfp4_matches_oracle(hip, T, E, k, zipf, H, I, xf32):
     (100, 16, 1040, 432, True),    # 16 slots, widths ending inside a piece, f32 activations
     (16, 1, 256, 128, False),      # one slot; fewer output tiles than blocks
     (32, 4, 3072, 128, False),     # more 10-row output tiles than resident blocks (the second loads late)
+    (64, 12, 2048, 1024, False),   # 3072 gate/up items over 2048 waves: half the waves take a second item
 ])
 def test_decode_nvfp4_one_launch_matches_stages(hip, E, k, H, I, xf32):
     """One token takes the one-launch kernel; its f32 output equals, bit for bit, the staged
