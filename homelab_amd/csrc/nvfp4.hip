@@ -523,7 +523,7 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
     extern __shared__ float4 xs4[];
     __shared__ uint64_t recs_l[N4F_KMAX];
     __shared__ float w_l[N4F_KMAX];
-    __shared__ uint64_t pk_keys[N4F_KMAX];  // routing scratch (route_picks)
+    __shared__ uint64_t pk_keys[64];  // routing scratch (route_picks: 64 entries with 8 logits a lane)
     __shared__ int pk_ids[N4F_KMAX];
     __shared__ float pk_p[N4F_KMAX];
     __shared__ float ylds[N4F_KMAX][2 * N4_DP];
@@ -669,7 +669,7 @@ __global__ void __launch_bounds__(64 * N4P_WAVES) moe_decode_nvfp4_1p_kernel(Fus
     extern __shared__ float4 xs4[];
     __shared__ uint64_t recs_l[N4F_KMAX];
     __shared__ float w_l[N4F_KMAX];
-    __shared__ uint64_t pk_keys[N4F_KMAX];  // routing scratch (route_picks)
+    __shared__ uint64_t pk_keys[64];  // routing scratch (route_picks: 64 entries with 8 logits a lane)
     __shared__ int pk_ids[N4F_KMAX];
     __shared__ float pk_p[N4F_KMAX];
     __shared__ float ylds[N4F_KMAX][2 * N4P_DP];
