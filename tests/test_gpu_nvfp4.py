@@ -170,6 +170,8 @@ def test_decode_nvfp4_matches_oracle(hip, T, E, k, zipf, H, I, xf32):
     (16, 1, 256, 128, False),      # one slot; fewer output tiles than blocks
     (32, 4, 3072, 128, False),     # more 10-row output tiles than resident blocks (the second loads late)
     (64, 12, 2048, 1024, False),   # 3072 gate/up items over 2048 waves: half the waves take a second item
+    (300, 6, 1024, 256, True),     # past 256 experts: 8 logits a lane, the last 212 lanes of the 5th..8th absent
+    (512, 16, 4096, 640, False),   # 16 picks of 512, hidden past 3072: the 4-wave kernel with 8 logits a lane
 ])
 def test_decode_nvfp4_one_launch_matches_stages(hip, E, k, H, I, xf32):
     """One token takes the one-launch kernel; its f32 output equals, bit for bit, the staged
