@@ -619,9 +619,9 @@ __global__ void __launch_bounds__(256) moe_decode_nvfp4_1_kernel(Fused4Args a) {
 //     b + G (w + 8 n), so every block holds 6 or 7 of the step's 1600 items;
 //   - block b's output tile is rows 10 b .. + 10 (2560 outputs over 256 blocks); its (slot,
 //     row pair) units are u = w + 8 m of wave w, and the first N4P_UP of them load into
-//     registers before the wave's gate/up loads (a prefetch issued behind them would make
-//     the item's waits count it only on some paths), so the down weights stream in phase 1
-//     and after the barrier a block only stages h;
+//     registers right behind the loads of the wave's first gate/up item (so the rows h
+//     needs arrive first), so the down weights stream in phase 1 and after the barrier a
+//     block only stages h;
 //   - a unit's lane partial and the 32-lane butterfly are dn4_compute's, so the outputs equal
 //     the staged launches' bit for bit. Units past N4P_UP (k > 11) and tiles past the grid
 //     load after the barrier.
