@@ -177,13 +177,28 @@ def test_decode_nvfp4_one_launch_matches_stages(hip, E, k, H, I, xf32):
     """One token takes the one-launch kernel; its f32 output equals, bit for bit, the staged
     launches (router, gate/up, down, slot-order combine) over the same routing, on three
     calls in a row on one workspace (the grid barrier's generations advance)."""
-    import torch
-
     print(f"case: nvfp4 one-launch E={E} k={k} H={H} I={I} x={'f32' if xf32 else 'bf16'}", flush=True)
     seed = 900 + E + H
+    _one_launch_check(hip, E, k, H, I, xf32, seed, synth.decode_logits(seed, 1, E, None))
+
+
+@pytest.mark.parametrize("E,k,levels", [(512, 10, 2.0), (512, 16, 0.0), (300, 8, 4.0)])
+def test_decode_nvfp4_one_launch_router_ties(hip, E, k, levels):
+    """Logits on a coarse grid (levels a unit; 0: all equal), so many experts tie in p at the
+    k-th pick: the one-launch router's descent (gathered one key a lane once at most 64
+    remain) picks the lower ids among equals, as the router kernel and the oracle do."""
+    print(f"case: nvfp4 one-launch router ties E={E} k={k} levels={levels}", flush=True)
+    seed = 77 + E + k
+    z = np.random.default_rng(seed).standard_normal((1, E))
+    logits = (np.round(z * levels) / levels if levels else np.zeros_like(z)).astype(np.float32)
+    _one_launch_check(hip, E, k, 1024, 256, False, seed, logits)
+
+
+def _one_launch_check(hip, E, k, H, I, xf32, seed, logits):
+    import torch
+
     geo = oracle.nvfp4_geometry(H, I)
     hgeo = hip.nvfp4_geometry(H, I)
-    logits = synth.decode_logits(seed, 1, E, None)
     ids0, _ = oracle.router_topk(logits, k)
     recs = synth.nvfp4_records(geo, seed, E, only=set(int(e) for e in np.unique(ids0)))
     xb = synth.activations_bf16(seed, 1, H)
